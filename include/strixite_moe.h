@@ -1,0 +1,142 @@
+/*
+ * C-ABI of the gfx950 MoE FFN library (libstrixite_moe.so): the drop-in boundary for strixite's quantized MoE
+ * sublayer. Plain pointers and sizes; no C++ or torch types. Each entry point wraps the C++ launcher of the same name
+ * in include/strixite_moe.hpp and cites the reference declaration it replaces.
+ *
+ * Conventions (strixite kernels/ headers): every buffer is caller-owned device memory; launches are asynchronous on
+ * `stream` (a hipStream_t, NULL = the default stream); nothing is allocated or freed. Return value: 0 on success,
+ * STRIX_E_PRECONDITION when a host-detectable precondition fails (the reference throws strix::Error),
+ * STRIX_E_GPU when the HIP runtime reports an error; strix_moe_last_error() then holds the message (thread-local).
+ * Device-detected data errors (non-finite logits, invalid expert ids) never trap: they set the caller-zeroed
+ * uint32_t err[3] word ({1, token or id, expert or slot}, first flag wins) and make the affected rows NaN.
+ * act / out_act: 0 = F32, 1 = BF16 (strixite kernels/norm.hpp:20 Act). math: strixite MoeMath (accepted, one path).
+ */
+#ifndef STRIXITE_MOE_H
+#define STRIXITE_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STRIX_MOE_ABI_VERSION 1
+#define STRIX_E_PRECONDITION 1
+#define STRIX_E_GPU 2
+#define STRIX_E_OTHER 3
+
+/* strixite runtime/q4_device.hpp:13-18 Q4DeviceView / runtime/q8_device.hpp:12-17 Q8DeviceView */
+typedef struct {
+    const uint8_t *q;
+    const uint16_t *scale;
+    const uint16_t *minv;
+    int64_t N, K, G;
+} strix_qview;
+
+/* strixite kernels/moe_grouped.hpp:75-81 MoeSharedAdd */
+typedef struct {
+    const void *s;
+    const float *gate_logit;
+    int64_t gate_ld;
+    uint32_t gate_index;
+    uint32_t *err;
+} strix_moe_shared_add_t;
+
+int strix_moe_abi_version(void);
+const char *strix_moe_last_error(void);
+
+/* strixite kernels/linear.hpp:23-26 linear_bf16w (router logits; the fixed FP32 summation order) */
+int strix_linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, int act,
+                       int out_act, void *stream);
+
+/* strixite kernels/moe_router.hpp:38-40 moe_router */
+int strix_moe_router(const void *logits, int64_t ld, int64_t M, int64_t E, int64_t k, const void *shared_logit,
+                     int64_t shared_ld, int32_t shared_id, int32_t *ids, float *coef, int act, uint32_t *err,
+                     void *stream);
+/* strixite kernels/moe_router.hpp:41-43 check_router_error / report_router_error (host words) */
+int strix_check_router_error(const uint32_t *err, const char *what);
+int strix_report_router_error(const uint32_t *err_host, const char *what);
+
+/* strixite kernels/moe_router.hpp:52-53 moe_shared_add, :61-63 moe_shared_add_inject */
+int strix_moe_shared_add(void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M, int64_t N,
+                         uint32_t gate_index, int act, uint32_t *err, void *stream);
+int strix_moe_shared_add_inject(void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M,
+                                int64_t N, uint32_t gate_index, void *x, const float *w_in, int64_t H, int act,
+                                uint32_t *err, void *stream);
+
+/* strixite kernels/moe_grouped.hpp:47 moe_route_workspace_bytes (-1 on bad arguments), :52-53 moe_group_routes */
+int64_t strix_moe_route_workspace_bytes(int64_t M, int64_t A, int64_t E);
+int strix_moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void *ws, size_t ws_bytes,
+                           uint32_t *err, void *stream);
+
+/* strixite kernels/moe_grouped.hpp:56-58, :66-69, :88-91 (Q4 experts); the Q8 family (BITS = 8) has no reference
+ * GPU counterpart - the reference's converter refuses Q8 experts (formats/convert_qwen4exp.cpp:347-349) - and serves
+ * 8-bit routed experts behind the same signatures. */
+int strix_linear_q4_experts_gather_grouped(const void *x, const strix_qview *w, int64_t E, const void *ws,
+                                           size_t ws_bytes, int64_t M, int64_t A, void *y, int act, int math,
+                                           void *stream);
+int strix_linear_q4_experts_gather_grouped_swiglu(const void *x, const strix_qview *w, int64_t E, const void *ws,
+                                                  size_t ws_bytes, int64_t M, int64_t A, void *h, int act, int math,
+                                                  void *stream, int h_f16);
+int strix_linear_q4_experts_combine_grouped(const void *h, const strix_qview *w, int64_t E, const int32_t *ids,
+                                            const float *coef, const void *ws, size_t ws_bytes, float *partial,
+                                            int64_t M, int64_t A, void *y, int act, int math, void *stream,
+                                            const strix_moe_shared_add_t *shared, int h_f16);
+int strix_linear_q8_experts_gather_grouped_swiglu(const void *x, const strix_qview *w, int64_t E, const void *ws,
+                                                  size_t ws_bytes, int64_t M, int64_t A, void *h, int act, int math,
+                                                  void *stream, int h_f16);
+int strix_linear_q8_experts_combine_grouped(const void *h, const strix_qview *w, int64_t E, const int32_t *ids,
+                                            const float *coef, const void *ws, size_t ws_bytes, float *partial,
+                                            int64_t M, int64_t A, void *y, int act, int math, void *stream,
+                                            const strix_moe_shared_add_t *shared, int h_f16);
+
+/* strixite kernels/linear_q4.hpp:42-43, :44-46, :55-56 (per-slot decode forms), :59-61 check / report */
+int strix_linear_q4_experts_gather(const void *x, const strix_qview *w, int64_t E, const int32_t *ids, int64_t M,
+                                   int64_t A, void *y, int act, uint32_t *err, void *stream);
+int strix_linear_q4_experts_gather_swiglu(const void *x, const strix_qview *w, int64_t E, const int32_t *ids,
+                                          int64_t M, int64_t A, void *h, int act, uint32_t *err, void *stream);
+int strix_linear_q4_experts_combine(const void *h, const strix_qview *w, int64_t E, const int32_t *ids,
+                                    const float *coef, int64_t M, int64_t A, void *y, int act, uint32_t *err,
+                                    void *stream);
+int strix_check_expert_error(const uint32_t *err, const char *what);
+int strix_report_expert_error(const uint32_t *err_host, const char *what);
+
+/* strixite kernels/swiglu.hpp:21 swiglu */
+int strix_swiglu(const void *gu, void *h, int64_t rows, int64_t I, int act, void *stream);
+
+/* strixite kernels/linear_q8.hpp:13-14 linear_q8 (the shared expert's projections) */
+int strix_linear_q8(const void *x, const strix_qview *w, void *y, int64_t M, int act, int out_act, void *stream);
+
+/* The MoE sublayer in the order of strixite runtime/qwen4exp.cpp:3143-3217 (its caller), as one entry point:
+ * router projection, moe_router, moe_group_routes, gate_up + SwiGLU, down, ordered combine with the shared expert's
+ * gated add folded in, residual write. routed_bits: 4 or 8 (gate_up and down alike). router_bias (optional, [E]) is a
+ * harness-side routing bias added once in FP32; logits_in (optional, [M, E + has_shared] FP32) bypasses the
+ * router projection. err: 6 caller-zeroed words (router word, expert word). */
+typedef struct {
+    int64_t H, E, k, I;
+    const uint16_t *router;
+    const float *router_bias;
+    int routed_bits;
+    strix_qview gate_up, down;
+    int has_shared;
+    strix_qview sh_gate_up, sh_down;
+} strix_moe_layer_weights;
+
+int64_t strix_moe_layer_workspace_bytes(const strix_moe_layer_weights *w, int64_t M);
+int strix_moe_layer_forward(const strix_moe_layer_weights *w, const void *x, int64_t M, const float *logits_in,
+                            void *y, void *x_out, int32_t *ids, float *coef, void *ws, size_t ws_bytes, uint32_t *err,
+                            void *stream);
+
+/* Seeded synthetic tensors on the device (no reference counterpart: the bench's input generator). Element i of a
+ * tensor is a function of (key, i) only; key = strix_synth_tensor_key(seed, tensor id, layer). */
+uint64_t strix_synth_tensor_key(uint64_t seed, uint32_t tensor, uint32_t layer);
+int strix_synth_bf16_normal(uint64_t key, float sigma, uint16_t *out, int64_t n, void *stream);
+int strix_synth_q_weight(int bits, uint64_t key_codes, uint64_t key_scales, int64_t rows, int64_t K, int64_t G,
+                         uint8_t *q, uint16_t *scale, uint16_t *minv, void *stream);
+int strix_synth_uniform_pm1(uint64_t key, float *out, int64_t n, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

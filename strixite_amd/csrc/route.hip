@@ -1,0 +1,291 @@
+// Ragged token -> expert packing on gfx950 (moe_route_workspace_bytes, moe_group_routes): per-expert counts,
+// exclusive-scan offsets and the slot permutation, stable (ascending slot order inside an expert's bucket), plus the
+// tile tables the grouped expert kernels walk.
+//
+// Work is split into chunks of kChunk slots, one wave64 per chunk. Inside a wave, the lanes holding the same bucket
+// find each other with ballots over the bucket's bits (an exact "match any"), so each lane knows its rank among
+// equal buckets in lane order and one leader lane updates the bucket's count - no atomics, so the placement is the
+// stable order by construction. Small S (<= 16 chunks) runs as one 1024-thread block with everything in LDS; larger S
+// as three launches (chunk histograms, scan, placement) through the workspace.
+#include "common.hpp"
+
+#include <climits>
+
+namespace strix::kernels {
+
+namespace route {
+
+constexpr int kWave = 64;
+constexpr int kChunk = 256;          // slots per wave chunk
+constexpr int kSmallWaves = 16;      // the one-block path: 1024 threads
+constexpr int kTileRows = 16;        // slots per tile of the grouped expert kernels
+constexpr int kWideRows = 64;        // slots per wide tile (kept for the large-M kernels)
+
+struct Layout {
+    int64_t S, E, T16, T64, nch;
+    __host__ __device__ int64_t offsets() const { return 4; }
+    __host__ __device__ int64_t slots() const { return offsets() + E + 2; }
+    __host__ __device__ int64_t t16_bucket() const { return slots() + S; }
+    __host__ __device__ int64_t t16_start() const { return t16_bucket() + T16; }
+    __host__ __device__ int64_t t64_bucket() const { return t16_start() + T16; }
+    __host__ __device__ int64_t t64_start() const { return t64_bucket() + T64; }
+    __host__ __device__ int64_t hist() const { return t64_start() + T64; }        // [nch][E + 1]
+    __host__ __device__ int64_t bad() const { return hist() + nch * (E + 1); }    // [nch]
+    __host__ __device__ int64_t ints() const { return bad() + nch; }
+};
+
+inline Layout layout(int64_t M, int64_t A, int64_t E) {
+    const int64_t S = M * A;
+    // sum over buckets of ceil(count / R) <= S / R + (E + 1)
+    return {S, E, S / kTileRows + E + 2, S / kWideRows + E + 2, (S + kChunk - 1) / kChunk};
+}
+
+}  // namespace route
+
+namespace {
+
+using namespace route;
+
+__device__ __forceinline__ int bucket_of(int32_t id, int E) { return (id < 0 || id >= E) ? E : id; }
+
+// Lanes of the wave whose (valid) bucket equals this lane's: a ballot per bucket bit.
+__device__ __forceinline__ uint64_t match_bucket(int b, bool valid, int nbits) {
+    uint64_t m = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+        const bool one = (b >> bit) & 1;
+        const uint64_t bb = __ballot(one);
+        m &= one ? bb : ~bb;
+    }
+    return m;
+}
+
+__device__ __forceinline__ uint64_t lanes_below() { return (1ull << (threadIdx.x % kWave)) - 1ull; }
+
+// Histogram of chunk [s0, s1) into the wave-private counters h[E + 1] (zeroed by the caller); returns the chunk's
+// smallest invalid slot (INT_MAX if none) on every lane.
+__device__ int chunk_hist(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *h) {
+    const int lane = threadIdx.x % kWave;
+    int first_bad = INT_MAX;
+    for (int64_t base = s0; base < s1; base += kWave) {
+        const int64_t s = base + lane;
+        const bool valid = s < s1;
+        const int32_t id = valid ? ids[s] : 0;
+        const int b = bucket_of(id, E);
+        const uint64_t same = match_bucket(b, valid, nbits);
+        if (valid && (same & lanes_below()) == 0) h[b] += __popcll(same);
+        if (valid && b == E && (int)s < first_bad) first_bad = (int)s;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, off, kWave));
+    return first_bad;
+}
+
+// Stable placement of chunk [s0, s1) through the wave-private cursors c[E + 1] (each at the bucket's first free
+// position for this chunk).
+__device__ void chunk_place(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *c, int32_t *slots) {
+    const int lane = threadIdx.x % kWave;
+    for (int64_t base = s0; base < s1; base += kWave) {
+        const int64_t s = base + lane;
+        const bool valid = s < s1;
+        const int32_t id = valid ? ids[s] : 0;
+        const int b = bucket_of(id, E);
+        const uint64_t same = match_bucket(b, valid, nbits);
+        const int rank = __popcll(same & lanes_below());
+        int cur = 0;
+        if (valid) cur = c[b];
+        if (valid) slots[cur + rank] = (int32_t)s;
+        if (valid && rank == 0) c[b] = cur + __popcll(same);
+    }
+}
+
+// Exclusive scan of three ints over the 1024 threads of a block; totals returned through tot[3].
+__device__ void block_scan3(int (&v)[3], int *wsum /* [16][3] LDS */, int (&tot)[3]) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    int inc[3] = {v[0], v[1], v[2]};
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int o = __shfl_up(inc[j], off, kWave);
+            if (lane >= off) inc[j] += o;
+        }
+    if (lane == kWave - 1)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) wsum[wave * 3 + j] = inc[j];
+    __syncthreads();
+    int before[3] = {0, 0, 0};
+    for (int w = 0; w < (int)(blockDim.x / kWave); ++w)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int t = wsum[w * 3 + j];
+            if (w < wave) before[j] += t;
+            if (w == 0) tot[j] = 0;
+            tot[j] += t;
+        }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) v[j] = before[j] + inc[j] - v[j];
+    __syncthreads();
+}
+
+// Bucket t's offsets and tile tables, given its exclusive prefixes (slots, 16-slot tiles, 64-slot tiles).
+__device__ void write_bucket(int t, int cnt, const int (&pre)[3], int32_t *ws, const Layout &L) {
+    int32_t *offsets = ws + L.offsets();
+    offsets[t] = pre[0];
+    const int n16 = (cnt + kTileRows - 1) / kTileRows, n64 = (cnt + kWideRows - 1) / kWideRows;
+    for (int i = 0; i < n16; ++i) ws[L.t16_bucket() + pre[1] + i] = t, ws[L.t16_start() + pre[1] + i] = pre[0] + i * kTileRows;
+    for (int i = 0; i < n64; ++i) ws[L.t64_bucket() + pre[2] + i] = t, ws[L.t64_start() + pre[2] + i] = pre[0] + i * kWideRows;
+}
+
+__device__ void write_header(int32_t *ws, const Layout &L, const int (&tot)[3]) {
+    ws[0] = tot[1];
+    ws[1] = (int32_t)L.S;
+    ws[2] = (int32_t)L.E;
+    ws[3] = tot[2];
+    ws[L.offsets() + L.E + 1] = tot[0];
+}
+
+__device__ void report_bad(const int32_t *ids, int first_bad, uint32_t *err) {
+    if (first_bad != INT_MAX && atomicCAS(&err[0], 0u, 1u) == 0u) {
+        err[1] = (uint32_t)ids[first_bad];
+        err[2] = (uint32_t)first_bad;
+    }
+}
+
+// ---- S <= kSmallWaves * kChunk: one block -------------------------------------------------------------------------
+__global__ void __launch_bounds__(1024) route_small_kernel(const int32_t *ids, Layout L, int nbits, int32_t *ws,
+                                                           uint32_t *err) {
+    extern __shared__ int lds[];  // [kSmallWaves][E + 1] counters, then [16][3] scan sums, then first_bad
+    const int E = (int)L.E, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    int *h = lds + wave * (E + 1);
+    int *wsum = lds + kSmallWaves * (E + 1);
+    int *bad = wsum + 48;
+    for (int b = lane; b <= E; b += kWave) h[b] = 0;
+    if (threadIdx.x == 0) *bad = INT_MAX;
+    __syncthreads();
+    const int64_t s0 = (int64_t)wave * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
+    if (s0 < L.S) {
+        const int fb = chunk_hist(ids, s0, s1, E, nbits, h);
+        if (lane == 0 && fb != INT_MAX) atomicMin(bad, fb);
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    int cnt = 0;
+    if (t <= E)
+        for (int w = 0; w < kSmallWaves; ++w) cnt += lds[w * (E + 1) + t];
+    int v[3] = {cnt, (cnt + kTileRows - 1) / kTileRows, (cnt + kWideRows - 1) / kWideRows}, tot[3];
+    block_scan3(v, wsum, tot);
+    if (t <= E) {
+        write_bucket(t, cnt, v, ws, L);
+        int run = v[0];
+        for (int w = 0; w < kSmallWaves; ++w) {
+            const int c = lds[w * (E + 1) + t];
+            lds[w * (E + 1) + t] = run;
+            run += c;
+        }
+    }
+    if (t == 0) {
+        write_header(ws, L, tot);
+        report_bad(ids, *bad, err);
+    }
+    __syncthreads();
+    if (s0 < L.S) chunk_place(ids, s0, s1, E, nbits, h, ws + L.slots());
+}
+
+// ---- larger S: chunk histograms, one scan block, placement ----------------------------------------------------------
+constexpr int kWavesPerBlock = 4;
+
+__global__ void __launch_bounds__(kWavesPerBlock * kWave) route_hist_kernel(const int32_t *ids, Layout L, int nbits,
+                                                                           int32_t *ws) {
+    extern __shared__ int lds[];  // [kWavesPerBlock][E + 1]
+    const int E = (int)L.E, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int64_t ch = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+    if (ch >= L.nch) return;  // whole wave; no barrier in this kernel
+    int *h = lds + wave * (E + 1);
+    for (int b = lane; b <= E; b += kWave) h[b] = 0;
+    const int64_t s0 = ch * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
+    const int fb = chunk_hist(ids, s0, s1, E, nbits, h);
+    int32_t *gh = ws + L.hist() + ch * (E + 1);
+    for (int b = lane; b <= E; b += kWave) gh[b] = h[b];
+    if (lane == 0) ws[L.bad() + ch] = fb;
+}
+
+__global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, Layout L, int32_t *ws, uint32_t *err) {
+    __shared__ int wsum[48];
+    __shared__ int bad_lds;
+    const int E = (int)L.E, t = threadIdx.x;
+    if (t == 0) bad_lds = INT_MAX;
+    __syncthreads();
+    int fb = INT_MAX;
+    for (int64_t c = t; c < L.nch; c += blockDim.x) fb = min(fb, ws[L.bad() + c]);
+    if (fb != INT_MAX) atomicMin(&bad_lds, fb);
+    int cnt = 0;
+    if (t <= E)
+        for (int64_t c = 0; c < L.nch; ++c) cnt += ws[L.hist() + c * (E + 1) + t];
+    int v[3] = {cnt, (cnt + kTileRows - 1) / kTileRows, (cnt + kWideRows - 1) / kWideRows}, tot[3];
+    block_scan3(v, wsum, tot);
+    if (t <= E) {
+        write_bucket(t, cnt, v, ws, L);
+        int run = v[0];
+        for (int64_t c = 0; c < L.nch; ++c) {
+            int32_t *p = ws + L.hist() + c * (E + 1) + t;
+            const int k = *p;
+            *p = run;
+            run += k;
+        }
+    }
+    if (t == 0) {
+        write_header(ws, L, tot);
+        report_bad(ids, bad_lds, err);
+    }
+}
+
+__global__ void __launch_bounds__(kWavesPerBlock * kWave) route_place_kernel(const int32_t *ids, Layout L, int nbits,
+                                                                            int32_t *ws) {
+    extern __shared__ int lds[];
+    const int E = (int)L.E, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int64_t ch = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+    if (ch >= L.nch) return;
+    int *c = lds + wave * (E + 1);
+    const int32_t *gh = ws + L.hist() + ch * (E + 1);
+    for (int b = lane; b <= E; b += kWave) c[b] = gh[b];
+    const int64_t s0 = ch * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
+    chunk_place(ids, s0, s1, E, nbits, c, ws + L.slots());
+}
+
+}  // namespace
+
+size_t moe_route_workspace_bytes(int64_t M, int64_t A, int64_t E) {
+    STRIX_CHECK(M >= 1 && A >= 1 && E >= 1 && E <= kMoeMaxExperts && M * A <= kMoeMaxSlots,
+                "moe_route_workspace_bytes: M = ", M, ", A = ", A, ", E = ", E, " (E <= ", kMoeMaxExperts,
+                ", M*A <= ", kMoeMaxSlots, ")");
+    return (size_t)route::layout(M, A, E).ints() * 4;
+}
+
+void moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void *ws, size_t ws_bytes, uint32_t *err,
+                      hipStream_t stream) {
+    const char *fn = "moe_group_routes";
+    STRIX_CHECK(ids != nullptr && ws != nullptr && err != nullptr, fn, ": null pointer (ids=", (const void *)ids,
+                ", ws=", ws, ", err=", (const void *)err, ")");
+    STRIX_CHECK(M >= 1 && A >= 1 && A <= 64 && E >= 1 && E <= kMoeMaxExperts && M * A <= kMoeMaxSlots, fn, ": M = ",
+                M, ", A = ", A, ", E = ", E, " (A 1..64, E 1..", kMoeMaxExperts, ", M*A <= ", kMoeMaxSlots, ")");
+    STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, A, E), fn, ": workspace of ", ws_bytes, " bytes, needs ",
+                moe_route_workspace_bytes(M, A, E));
+    STRIX_CHECK(disjoint(ids, M * A * 4, ws, (int64_t)ws_bytes), fn, ": ids overlaps the workspace");
+    const Layout L = route::layout(M, A, E);
+    int nbits = 0;
+    while ((1ll << nbits) <= E) ++nbits;  // buckets 0..E
+    int32_t *w = static_cast<int32_t *>(ws);
+    if (L.nch <= kSmallWaves) {
+        const size_t lds = ((size_t)kSmallWaves * (E + 1) + 48 + 1) * 4;
+        route_small_kernel<<<1, 1024, lds, stream>>>(ids, L, nbits, w, err);
+    } else {
+        const unsigned blocks = (unsigned)((L.nch + kWavesPerBlock - 1) / kWavesPerBlock);
+        const size_t lds = (size_t)kWavesPerBlock * (E + 1) * 4;
+        route_hist_kernel<<<blocks, kWavesPerBlock * kWave, lds, stream>>>(ids, L, nbits, w);
+        route_scan_kernel<<<1, 1024, 0, stream>>>(ids, L, w, err);
+        route_place_kernel<<<blocks, kWavesPerBlock * kWave, lds, stream>>>(ids, L, nbits, w);
+    }
+    STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E);
+}
+
+}  // namespace strix::kernels

@@ -1,0 +1,345 @@
+// Router side of the MoE sublayer on gfx950: the router projection (linear_bf16w, one fixed FP32 summation order),
+// the top-k / softmax (moe_router, one wave64 per token, logits in registers), and the shared expert's gated add
+// (moe_shared_add, moe_shared_add_inject).
+#include "common.hpp"
+
+#include <climits>
+#include <type_traits>
+
+namespace strix::kernels {
+
+const char *act_name(Act a) { return a == Act::F32 ? "F32" : a == Act::BF16 ? "BF16" : "?"; }
+
+namespace {
+
+using namespace strix::dev;
+
+constexpr int kWave = 64;
+constexpr int kThreads = 256;
+
+// ---- router projection ----------------------------------------------------------------------------------------
+// One wave per output row n, MR token rows a block. Lane l owns the 8-element chunks c = l, l + 64, ...: its
+// partial is an fmaf chain over them (chunk order, then element order), then a butterfly over the 64 lanes. The
+// order depends on nothing but K, so every M, grid and launch gives the same bits (oracle: orc_router_logits).
+// VEC: K % 8 == 0 and 16-byte aligned x / w rows - 16-byte loads; else element loads, the same arithmetic.
+template <typename TY, int MR, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+    router_rows_kernel(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int64_t n = (int64_t)blockIdx.x * (kThreads / kWave) + wave;
+    const int64_t m0 = (int64_t)blockIdx.y * MR;
+    if (n >= N) return;  // no barrier in this kernel
+    const int rows = (int)(M - m0 < MR ? M - m0 : MR);
+    float acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[r] = 0.f;
+    const int64_t chunks = (K + 7) / 8;
+    const uint16_t *wr = w + n * K;
+    for (int64_t c = lane; c < chunks; c += kWave) {
+        float wv[8];
+        if constexpr (VEC) {
+            const uint4 u = *reinterpret_cast<const uint4 *>(wr + c * 8);
+            const uint32_t d[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wv[2 * i] = __uint_as_float(d[i] << 16), wv[2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wv[i] = c * 8 + i < K ? bf16_to_f32(wr[c * 8 + i]) : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            if (r < rows) {
+                const uint16_t *xr = x + (m0 + r) * K;
+                float xv[8];
+                if constexpr (VEC) {
+                    const uint4 u = *reinterpret_cast<const uint4 *>(xr + c * 8);
+                    const uint32_t d[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) xv[2 * i] = __uint_as_float(d[i] << 16), xv[2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[r] = fmaf(xv[i], wv[i], acc[r]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        if (c * 8 + i < K) acc[r] = fmaf(bf16_to_f32(xr[c * 8 + i]), wv[i], acc[r]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) acc[r] = acc[r] + __shfl_xor(acc[r], off, kWave);
+    if (lane == 0)
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+            if (r < rows) {
+                if constexpr (std::is_same_v<TY, float>) y[(m0 + r) * N + n] = acc[r];
+                else y[(m0 + r) * N + n] = f32_to_bf16(acc[r]);
+            }
+}
+
+template <typename TY>
+void launch_router_rows(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K,
+                        hipStream_t stream) {
+    const bool vec = K % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    const unsigned bx = (unsigned)((N + kThreads / kWave - 1) / (kThreads / kWave));
+    auto go = [&](auto mr) {
+        constexpr int MR = decltype(mr)::value;
+        const int64_t by = (M + MR - 1) / MR;
+        STRIX_CHECK(by <= 65535, "linear_bf16w: M = ", M, " needs ", by, " row blocks, grid.y holds 65535");
+        dim3 grid(bx, (unsigned)by), block(kThreads);
+        if (vec) router_rows_kernel<TY, MR, true><<<grid, block, 0, stream>>>(x, w, y, M, N, K);
+        else router_rows_kernel<TY, MR, false><<<grid, block, 0, stream>>>(x, w, y, M, N, K);
+    };
+    if (M == 1) go(std::integral_constant<int, 1>{});
+    else if (M <= 4) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 16>{});
+}
+
+// ---- top-k ----------------------------------------------------------------------------------------------------
+// One wave64 per token (4 a block). Lane l holds experts l, l + 64, ... (NV registers, -inf past E). A round is a
+// 64-lane arg-max over the lanes' bests (larger value, then lower index); the winner lane masks its pick and rescans
+// its registers. Lane r keeps the r-th pick, so the softmax over the k is one butterfly sum.
+template <typename T> __device__ __forceinline__ float load_logit(const T *p, int64_t i);
+template <> __device__ __forceinline__ float load_logit<float>(const float *p, int64_t i) { return p[i]; }
+template <> __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t *p, int64_t i) { return bf16_to_f32(p[i]); }
+
+template <typename T, int NV>
+__global__ void __launch_bounds__(kThreads)
+    topk_kernel(const T *logits, int64_t ld, int64_t M, int E, int k, const T *shared, int64_t shared_ld,
+                int32_t shared_id, int32_t *ids, float *coef, int A, uint32_t *err) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t m = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+    if (m >= M) return;  // whole wave; no barrier in this kernel
+    const T *row = logits + m * ld;
+    float v[NV];
+    int bad = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int e = lane + j * kWave;
+        const float xv = e < E ? load_logit(row, e) : -INFINITY;
+        v[j] = xv;
+        if (e < E && !isfinite(xv) && e < bad) bad = e;
+    }
+    float sl = 0.f;
+    if (shared != nullptr) {
+        sl = load_logit(shared, m * shared_ld);
+        if (!isfinite(sl) && E < bad) bad = E;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off, kWave));
+    int32_t *id_row = ids + m * A;
+    float *coef_row = coef + m * A;
+    if (bad != INT_MAX) {
+        if (lane == 0 && atomicCAS(&err[0], 0u, 1u) == 0u) {
+            err[1] = (uint32_t)m;
+            err[2] = (uint32_t)bad;
+        }
+        for (int a = lane; a < A; a += kWave) id_row[a] = -1, coef_row[a] = qnan();
+        return;
+    }
+    // finite from here: -inf marks a taken expert and the padding past E
+    float lv = -INFINITY;
+    int li = INT_MAX;
+    auto lane_best = [&]() {
+        lv = -INFINITY, li = INT_MAX;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (v[j] > lv) lv = v[j], li = lane + j * kWave;  // ascending scan, strict >: lower index on ties
+    };
+    lane_best();
+    float my_v = -INFINITY, top = 0.f;
+    int my_i = -1;
+    for (int r = 0; r < k; ++r) {
+        float bv = lv;
+        int bi = li;
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, kWave);
+            const int oi = __shfl_xor(bi, off, kWave);
+            if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+        }
+        if (r == 0) top = bv;
+        if (lane == r) my_v = bv, my_i = bi;
+        if (bi == li) {  // the pick is this lane's best (an index lives in one lane only)
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                if (lane + j * kWave == bi) v[j] = -INFINITY;
+            lane_best();
+        }
+    }
+    const float ex = lane < k ? expf(my_v - top) : 0.f;
+    float sum = ex;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, kWave);
+    if (lane < k) {
+        id_row[lane] = my_i;
+        coef_row[lane] = ex / sum;
+    }
+    if (shared != nullptr && lane == 0) {
+        id_row[k] = shared_id;
+        coef_row[k] = 1.0f / (1.0f + expf(-sl));
+    }
+}
+
+// ---- shared expert add ----------------------------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ float ld_act(const T *p, int64_t i);
+template <> __device__ __forceinline__ float ld_act<float>(const float *p, int64_t i) { return p[i]; }
+template <> __device__ __forceinline__ float ld_act<uint16_t>(const uint16_t *p, int64_t i) { return bf16_to_f32(p[i]); }
+template <typename T> __device__ __forceinline__ void st_act(T *p, int64_t i, float v);
+template <> __device__ __forceinline__ void st_act<float>(float *p, int64_t i, float v) { p[i] = v; }
+template <> __device__ __forceinline__ void st_act<uint16_t>(uint16_t *p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+template <typename T> __device__ __forceinline__ float as_stored(float v) {
+    if constexpr (std::is_same_v<T, float>) return v;
+    else return bf16_round(v);
+}
+
+// y = stored(y + sigmoid(gl) * s) (strixite kernels/moe_router.hip:129-146); INJECT: then for the H streams
+// x[m, st * N + n] = stored(fma(w_in[m, st], y, x)) (moe_router.hip:154-180). Grid-stride over M * N.
+template <typename T, bool INJECT>
+__global__ void __launch_bounds__(kThreads)
+    shared_add_kernel(T *y, const T *s, const float *gate_logit, int64_t gate_ld, int64_t M, int64_t N,
+                      uint32_t gate_index, T *x, const float *w_in, int64_t H, uint32_t *err) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < M * N; i += (int64_t)gridDim.x * kThreads) {
+        const int64_t m = i / N, n = i % N;
+        const float gl = gate_logit[m * gate_ld];
+        const bool ok = isfinite(gl);
+        if (!ok && n == 0 && atomicCAS(&err[0], 0u, 1u) == 0u) {
+            err[1] = (uint32_t)m;
+            err[2] = gate_index;
+        }
+        const float g = ok ? 1.f / (1.f + expf(-gl)) : qnan();
+        const float v = as_stored<T>(ld_act(y, i) + g * ld_act(s, i));
+        st_act(y, i, v);
+        if constexpr (INJECT)
+            for (int64_t st = 0; st < H; ++st) {
+                const int64_t xi = (m * H + st) * N + n;
+                st_act(x, xi, fmaf(w_in[m * H + st], v, ld_act(x, xi)));
+            }
+    }
+}
+
+unsigned elementwise_blocks(int64_t n) {
+    const int64_t b = (n + kThreads - 1) / kThreads;
+    return (unsigned)(b < 65536 ? b : 65536);
+}
+
+}  // namespace
+
+void linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, Act act,
+                  hipStream_t stream) {
+    linear_bf16w(x, w, y, M, N, K, act, act, stream);
+}
+
+void linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, Act act, Act out_act,
+                  hipStream_t stream) {
+    STRIX_CHECK(x != nullptr && w != nullptr && y != nullptr, "linear_bf16w: null pointer (x=", x, ", w=",
+                (const void *)w, ", y=", y, ")");
+    STRIX_CHECK(M >= 1 && N >= 1 && K >= 1 && K <= (1 << 24) && N <= 0x7fffffff, "linear_bf16w: M = ", M, ", N = ",
+                N, ", K = ", K, " out of range");
+    STRIX_CHECK(act == Act::BF16, "linear_bf16w: activations must be BF16 on this path, got ", act_name(act));
+    STRIX_CHECK(out_act == Act::F32 || out_act == Act::BF16, "linear_bf16w: output dtype ", (int)out_act);
+    const int64_t oes = out_act == Act::F32 ? 4 : 2;
+    STRIX_CHECK(disjoint(y, M * N * oes, x, M * K * 2), "linear_bf16w: output y overlaps input x");
+    if (out_act == Act::F32)
+        launch_router_rows(static_cast<const uint16_t *>(x), w, static_cast<float *>(y), M, N, K, stream);
+    else
+        launch_router_rows(static_cast<const uint16_t *>(x), w, static_cast<uint16_t *>(y), M, N, K, stream);
+    STRIX_HIP_CHECK_LAUNCH("linear_bf16w M=", M, " N=", N, " K=", K);
+}
+
+void moe_router(const void *logits, int64_t ld, int64_t M, int64_t E, int64_t k, const void *shared_logit,
+                int64_t shared_ld, int32_t shared_id, int32_t *ids, float *coef, Act act, uint32_t *err,
+                hipStream_t stream) {
+    STRIX_CHECK(logits != nullptr && ids != nullptr && coef != nullptr && err != nullptr,
+                "moe_router: null pointer (logits=", logits, ", ids=", (const void *)ids, ", coef=",
+                (const void *)coef, ", err=", (const void *)err, ")");
+    STRIX_CHECK(M >= 1 && M <= 0x7fffffff, "moe_router: M = ", M, " tokens, expected 1..2^31-1");
+    STRIX_CHECK(E >= 1 && E <= 1024, "moe_router: E = ", E, " experts, expected 1..1024");
+    STRIX_CHECK(k >= 1 && k <= E && k <= 32, "moe_router: k = ", k, ", expected 1..min(E = ", E, ", 32)");
+    STRIX_CHECK(ld >= E, "moe_router: logits row stride ld = ", ld, " < E = ", E);
+    if (shared_logit != nullptr) {
+        STRIX_CHECK(shared_ld >= 1, "moe_router: shared_ld = ", shared_ld, ", expected >= 1");
+        STRIX_CHECK(shared_id >= 0, "moe_router: shared_id = ", shared_id, ", expected >= 0");
+    }
+    STRIX_CHECK((const void *)ids != (const void *)coef, "moe_router: ids and coef are the same buffer");
+    STRIX_CHECK(act == Act::F32 || act == Act::BF16, "moe_router: unsupported logit dtype ", (int)act);
+    const int A = (int)k + (shared_logit != nullptr ? 1 : 0);
+    dim3 grid((unsigned)((M + 3) / 4)), block(kThreads);
+    const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
+    auto go = [&](auto tag, auto nvc) {
+        using T = decltype(tag);
+        topk_kernel<T, decltype(nvc)::value><<<grid, block, 0, stream>>>(
+            static_cast<const T *>(logits), ld, M, (int)E, (int)k, static_cast<const T *>(shared_logit), shared_ld,
+            shared_id, ids, coef, A, err);
+    };
+    auto by_nv = [&](auto tag) {
+        switch (nv) {
+            case 1: go(tag, std::integral_constant<int, 1>{}); break;
+            case 2: go(tag, std::integral_constant<int, 2>{}); break;
+            case 4: go(tag, std::integral_constant<int, 4>{}); break;
+            case 8: go(tag, std::integral_constant<int, 8>{}); break;
+            default: go(tag, std::integral_constant<int, 16>{}); break;
+        }
+    };
+    if (act == Act::F32) by_nv(float{});
+    else by_nv(uint16_t{});
+    STRIX_HIP_CHECK_LAUNCH("moe_router ", act_name(act), " M=", M, " E=", E, " k=", k, shared_logit ? " +shared" : "");
+}
+
+void check_router_error(const uint32_t *err, const char *what) {
+    STRIX_CHECK(err != nullptr, "check_router_error(", what, "): null err");
+    uint32_t e[3];
+    STRIX_HIP_CHECK(hipMemcpy(e, err, sizeof(e), hipMemcpyDeviceToHost), "reading the router error word for ", what);
+    report_router_error(e, what);
+}
+
+void report_router_error(const uint32_t e[3], const char *what) {
+    STRIX_CHECK(e[0] == 0, what, ": non-finite router logit at token ", e[1], ", expert ", e[2],
+                " (E = the shared-expert gate); that token's ids are -1 and its coefficients NaN");
+}
+
+namespace {
+template <bool INJECT>
+void shared_add_common(const char *fn, void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M,
+                       int64_t N, uint32_t gate_index, void *x, const float *w_in, int64_t H, Act act, uint32_t *err,
+                       hipStream_t stream) {
+    STRIX_CHECK(y != nullptr && s != nullptr && gate_logit != nullptr && err != nullptr, fn, ": null pointer");
+    STRIX_CHECK(!INJECT || (x != nullptr && w_in != nullptr), fn, ": null x or w_in");
+    STRIX_CHECK(M >= 1 && N >= 1 && N <= (1ll << 24), fn, ": M = ", M, ", N = ", N, " out of range");
+    STRIX_CHECK(gate_ld >= 1, fn, ": gate_ld = ", gate_ld, ", expected >= 1");
+    STRIX_CHECK(!INJECT || H == 4, fn, ": H = ", H, " streams, expected 4 (strixite's hc_count)");
+    STRIX_CHECK(act == Act::F32 || act == Act::BF16, fn, ": unsupported activation dtype ", (int)act);
+    const int64_t es = act == Act::F32 ? 4 : 2;
+    STRIX_CHECK(disjoint(y, M * N * es, s, M * N * es), fn, ": s overlaps y");
+    if (INJECT)
+        STRIX_CHECK(disjoint(x, M * H * N * es, y, M * N * es) && disjoint(x, M * H * N * es, s, M * N * es), fn,
+                    ": x overlaps y or s");
+    const unsigned blocks = elementwise_blocks(M * N);
+    if (act == Act::F32)
+        shared_add_kernel<float, INJECT><<<blocks, kThreads, 0, stream>>>(
+            static_cast<float *>(y), static_cast<const float *>(s), gate_logit, gate_ld, M, N, gate_index,
+            static_cast<float *>(x), w_in, H, err);
+    else
+        shared_add_kernel<uint16_t, INJECT><<<blocks, kThreads, 0, stream>>>(
+            static_cast<uint16_t *>(y), static_cast<const uint16_t *>(s), gate_logit, gate_ld, M, N, gate_index,
+            static_cast<uint16_t *>(x), w_in, H, err);
+    STRIX_HIP_CHECK_LAUNCH(fn, " ", act_name(act), " M=", M, " N=", N);
+}
+}  // namespace
+
+void moe_shared_add(void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M, int64_t N,
+                    uint32_t gate_index, Act act, uint32_t *err, hipStream_t stream) {
+    shared_add_common<false>("moe_shared_add", y, s, gate_logit, gate_ld, M, N, gate_index, nullptr, nullptr, 0, act,
+                             err, stream);
+}
+
+void moe_shared_add_inject(void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M, int64_t N,
+                           uint32_t gate_index, void *x, const float *w_in, int64_t H, Act act, uint32_t *err,
+                           hipStream_t stream) {
+    shared_add_common<true>("moe_shared_add_inject", y, s, gate_logit, gate_ld, M, N, gate_index, x, w_in, H, act,
+                            err, stream);
+}
+
+}  // namespace strix::kernels

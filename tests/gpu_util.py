@@ -1,0 +1,44 @@
+"""Shared helpers of the GPU parity tests: seeded layers built on the device through the product's generator,
+their weights copied to the host for the CPU oracle, and the comparison metrics."""
+import numpy as np
+import torch
+
+import oracle as orc
+from strixite_amd import moe
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.int16:
+        return t.numpy().view(np.uint16)
+    return t.numpy()
+
+
+def qspec(w: moe.QWeight):
+    return (w.bits, to_np(w.q), to_np(w.scale), to_np(w.minv), w.G)
+
+
+def oracle_weights(layer: moe.MoeLayer) -> dict:
+    w = {"E": layer.E, "k": layer.k, "I": layer.I, "router": to_np(layer.router), "gu": qspec(layer.gate_up),
+         "dn": qspec(layer.down)}
+    if layer.router_bias is not None:
+        w["router_bias"] = to_np(layer.router_bias)
+    if layer.has_shared:
+        w["sh_gu"], w["sh_dn"] = qspec(layer.shared_gate_up), qspec(layer.shared_down)
+    return w
+
+
+def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
+    """max |got - ref| / max |ref| (normwise; the layer tolerance is 1e-2 in bf16)."""
+    g = orc.bf16_to_f32(got) if got.dtype == np.uint16 else got
+    r = orc.bf16_to_f32(ref) if ref.dtype == np.uint16 else ref
+    return float(np.abs(g.astype(np.float64) - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+def zipf_bias(seed: int, E: int, beta: float, s: float = 1.1) -> np.ndarray:
+    """b_e = -beta * s * ln(rank_e) over a seeded permutation of the experts (host-side, float64 then float32)."""
+    rng = np.random.default_rng(orc.tensor_key(seed, "zipf") & 0xFFFFFFFF)
+    rank = rng.permutation(E) + 1
+    return (-beta * s * np.log(rank.astype(np.float64))).astype(np.float32)

@@ -1,0 +1,347 @@
+"""Parity of the gfx950 HIP path against the CPU oracle, through the C-ABI (strixite_amd.moe forwards to it).
+
+Bars: bit-exact for integer / index work and for the router logits (one specified FP32 order); for the expert math
+max|got - ref| / max|ref| <= 1e-2 in bf16 (BASELINE's layer tolerance), with tighter bounds where the f16 weight
+rounding allows. Sizes keep the oracle to seconds; the full-size configs check the routing on every token and the
+layer output on a seeded subset of tokens (the layer is token-independent once routed).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import oracle as orc  # noqa: E402
+from gpu_util import oracle_weights, qspec, rel_err, to_np, zipf_bias  # noqa: E402
+from strixite_amd import moe  # noqa: E402
+
+DEV = "cuda"
+
+
+def say(*a):
+    print("[gpu]", *a, file=sys.stderr, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    moe.L.lib()  # loud failure if the library is missing
+    yield
+    torch.cuda.synchronize()
+
+
+def bf16(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(a.view(np.int16)).to(DEV).view(torch.bfloat16)
+
+
+# ---- generator --------------------------------------------------------------------------------------------------
+def test_synth_matches_host_generator():
+    say("synth")
+    x = moe.synth_bf16_normal(7, "x", 3, (5, 1000), 1.0)
+    ref = orc.gen_bf16_normal(orc.tensor_key(7, "x", 3), 1.0, (5, 1000))
+    assert np.array_equal(to_np(x), ref)
+    for bits, G in ((4, 128), (8, 64)):
+        w = moe.QWeight.synth(bits, 7, "gu_q", "gu_s", 2, 48, 512, G)
+        q, s, m = orc.gen_q(bits, orc.tensor_key(7, "gu_q", 2), orc.tensor_key(7, "gu_s", 2), 48, 512, G)
+        assert np.array_equal(to_np(w.q), q) and np.array_equal(to_np(w.scale), s) and np.array_equal(to_np(w.minv), m)
+    u = moe.synth_uniform_pm1(7, "logits", 0, (3, 513))
+    assert np.array_equal(to_np(u), orc.gen_uniform_pm1(orc.tensor_key(7, "logits", 0), (3, 513)))
+
+
+# ---- router -----------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K", [(1, 65, 2048), (16, 513, 3072), (5, 7, 1000), (37, 129, 512)])
+def test_linear_bf16w_bit_exact(M, N, K):
+    say("linear_bf16w", M, N, K)
+    x = orc.gen_bf16_normal(orc.tensor_key(1, "x"), 1.0, (M, K))
+    w = orc.gen_bf16_normal(orc.tensor_key(1, "router"), 0.02, (N, K))
+    y = moe.linear_bf16w(bf16(x), bf16(w))
+    ref = orc.router_logits(x, w)
+    assert np.array_equal(to_np(y).view(np.uint32), ref.view(np.uint32))
+    yb = moe.linear_bf16w(bf16(x), bf16(w), out_dtype=torch.bfloat16)
+    assert np.array_equal(to_np(yb), orc.f32_to_bf16(ref))
+
+
+@pytest.mark.parametrize("E,k", [(64, 8), (512, 10), (1024, 32), (100, 32), (7, 7)])
+def test_moe_router_matches_oracle(E, k):
+    say("moe_router", E, k)
+    rng = np.random.default_rng(E * 100 + k)
+    M = 300
+    lg = rng.standard_normal((M, E + 3)).astype(np.float32)
+    lg[5, :] = 0.25  # all equal: ids 0..k-1
+    lg[6, 3:9] = lg[6, :E].max() + 1  # a tie at the top
+    lg[7, : E // 2] = lg[7, E // 2: 2 * (E // 2)]  # pairwise ties everywhere
+    ids, coef, err = moe.moe_router(torch.from_numpy(lg).to(DEV), E, k, ld=E + 3)
+    rids, rcoef, rerr = orc.topk(lg, E, k)
+    assert np.array_equal(to_np(ids), rids)
+    assert np.allclose(to_np(coef), rcoef, rtol=2e-6, atol=1e-7)
+    assert to_np(err)[0] == 0 and rerr[0] == 0
+    # bf16 logits
+    lb = orc.f32_to_bf16(lg)
+    ids_b, coef_b, _ = moe.moe_router(bf16(lb), E, k, ld=E + 3)
+    rids_b, rcoef_b, _ = orc.topk(orc.bf16_to_f32(lb), E, k)
+    assert np.array_equal(to_np(ids_b), rids_b)
+    assert np.allclose(to_np(coef_b), rcoef_b, rtol=2e-6, atol=1e-7)
+
+
+def test_moe_router_shared_and_nonfinite():
+    say("moe_router nonfinite")
+    E, k, M = 512, 10, 64
+    lg = np.random.default_rng(3).standard_normal((M, E + 1)).astype(np.float32)
+    lg[9, 100] = np.nan
+    lg[9, 7] = np.inf
+    lg[20, E] = -np.inf
+    t = torch.from_numpy(lg).to(DEV)
+    ids, coef, err = moe.moe_router(t, E, k, shared_logit=t[:, E:], shared_ld=E + 1, shared_id=E, ld=E + 1)
+    rids, rcoef, _ = orc.topk(lg, E, k, shared=np.ascontiguousarray(lg[:, E:]), shared_ld=1, shared_id=E)
+    assert np.array_equal(to_np(ids), rids)
+    ok = ~np.isnan(rcoef)
+    assert np.array_equal(np.isnan(to_np(coef)), ~ok)
+    assert np.allclose(to_np(coef)[ok], rcoef[ok], rtol=2e-6, atol=1e-7)
+    e = to_np(err).view(np.uint32)
+    assert e[0] == 1 and (tuple(e[1:]) in {(9, 7), (20, E)})  # the first flag of either failing token wins
+    with pytest.raises(moe.StrixError, match="non-finite router logit"):
+        moe.check_router_error(err, "L0 moe")
+
+
+# ---- packing -----------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M,A,E", [(1, 8, 64), (16, 10, 512), (6, 11, 1023), (300, 10, 512), (4096, 10, 512),
+                                   (513, 64, 1023), (3, 1, 1)])
+def test_group_routes_bit_exact(M, A, E):
+    say("group_routes", M, A, E)
+    rng = np.random.default_rng(M + A + E)
+    ids = rng.integers(0, E, (M, A)).astype(np.int32)
+    if M * A > 200:  # Zipf-like skew: one hot bucket
+        ids[rng.random((M, A)) < 0.3] = E // 2
+    ws, err = moe.moe_group_routes(torch.from_numpy(ids).to(DEV), E)
+    t = moe.route_tables(ws, M, A, E)
+    off, slots, rerr = orc.group_routes(ids, E)
+    assert np.array_equal(to_np(t["offsets"]), off)
+    assert np.array_equal(to_np(t["slots"]), slots)
+    assert int(t["S"]) == M * A and int(t["E"]) == E
+    assert int(t["n_tiles"]) == int(sum((c + 15) // 16 for c in np.diff(off)))
+    assert to_np(err)[0] == 0
+
+
+def test_group_routes_invalid_ids():
+    say("group_routes invalid")
+    for M, A in ((16, 10), (2000, 10)):
+        E = 512
+        ids = np.random.default_rng(M).integers(0, E, (M, A)).astype(np.int32)
+        ids[3, 4], ids[11, 0], ids[12, 9] = -1, E, 99999
+        ws, err = moe.moe_group_routes(torch.from_numpy(ids).to(DEV), E)
+        off, slots, rerr = orc.group_routes(ids, E)
+        t = moe.route_tables(ws, M, A, E)
+        assert np.array_equal(to_np(t["offsets"]), off) and np.array_equal(to_np(t["slots"]), slots)
+        assert np.array_equal(to_np(err).view(np.uint32), rerr)  # the first invalid slot in slot order
+        with pytest.raises(moe.StrixError, match="out of range"):
+            moe.check_expert_error(err)
+
+
+# ---- expert projections ------------------------------------------------------------------------------------------
+def _experts(bits, E, H, I, seed=11):
+    G = 128 if bits == 4 else 64
+    gu = moe.QWeight.synth(bits, seed, "gu_q", "gu_s", 0, E * 2 * I, H, G)
+    dn = moe.QWeight.synth(bits, seed, "dn_q", "dn_s", 0, E * H, I, G)
+    return gu, dn
+
+
+@pytest.mark.parametrize("bits,M,A,E,H,I", [(4, 16, 10, 64, 512, 256), (8, 1, 8, 64, 512, 128),
+                                            (4, 300, 8, 16, 256, 128), (8, 40, 4, 8, 256, 64)])
+def test_grouped_gate_up_swiglu_and_down(bits, M, A, E, H, I):
+    say("grouped experts", bits, M, A, E, H, I)
+    gu, dn = _experts(bits, E, H, I)
+    x = orc.gen_bf16_normal(orc.tensor_key(2, "x"), 1.0, (M, H))
+    ids = np.stack([np.random.default_rng(m).permutation(E)[:A] for m in range(M)]).astype(np.int32)
+    tid = torch.from_numpy(ids).to(DEV)
+    ws, _ = moe.moe_group_routes(tid, E)
+    h = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)
+    b, q, s, m, G = qspec(gu)
+    href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G), E, ids)
+    assert rel_err(to_np(h), href) < 1e-2
+    # the f16-bits form is the same values
+    hf = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A, h_f16=True)
+    assert torch.equal(hf.float(), h.float())
+    coef = np.random.default_rng(5).random((M, A)).astype(np.float32)
+    y = moe.experts_combine_grouped(h, dn, E, tid, torch.from_numpy(coef).to(DEV), ws, M, A)
+    b, q, s, m, G = qspec(dn)
+    part = orc.experts_down(to_np(h), orc.qview(b, q, s, m, dn.N, I, G), E, ids)
+    yref, _ = orc.combine(part, ids, coef, E, H)
+    assert rel_err(to_np(y), yref) < 1e-2
+    y2 = moe.experts_combine_grouped(hf, dn, E, tid, torch.from_numpy(coef).to(DEV), ws, M, A, h_f16=True)
+    assert torch.equal(y2, y)
+
+
+def test_grouped_gather_plain_q4():
+    say("grouped gather plain")
+    M, A, E, H, I = 9, 3, 8, 256, 64
+    gu, _ = _experts(4, E, H, I)
+    x = orc.gen_bf16_normal(orc.tensor_key(3, "x"), 1.0, (M, H))
+    ids = np.random.default_rng(1).integers(0, E, (M, A)).astype(np.int32)
+    ws, _ = moe.moe_group_routes(torch.from_numpy(ids).to(DEV), E)
+    y = to_np(moe.experts_gather_grouped(bf16(x), gu, E, ws, M, A))
+    w = orc.dequantize(4, *qspec(gu)[1:4], gu.N, H, gu.G).astype(np.float64)
+    xf = orc.bf16_to_f32(x).astype(np.float64)
+    N = 2 * I
+    ref = np.stack([w[ids.ravel()[s] * N:(ids.ravel()[s] + 1) * N] @ xf[s // A] for s in range(M * A)])
+    assert rel_err(y, ref) < 1e-2
+
+
+def test_invalid_ids_make_nan_rows():
+    say("experts invalid ids")
+    M, A, E, H, I = 4, 2, 8, 256, 64
+    gu, dn = _experts(4, E, H, I)
+    x = orc.gen_bf16_normal(orc.tensor_key(4, "x"), 1.0, (M, H))
+    ids = np.array([[0, 1], [2, -1], [3, 4], [5, 8]], np.int32)
+    tid = torch.from_numpy(ids).to(DEV)
+    ws, err = moe.moe_group_routes(tid, E)
+    h = to_np(moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)).copy()
+    hf = orc.bf16_to_f32(h)
+    assert np.all(np.isnan(hf[3])) and np.all(np.isnan(hf[7])) and not np.isnan(hf[[0, 1, 2, 4, 5, 6]]).any()
+    h[[3, 7]] = 0
+    coef = torch.full((M, A), 0.5, device=DEV)
+    y = orc.bf16_to_f32(to_np(moe.experts_combine_grouped(torch.from_numpy(h.view(np.int16)).to(DEV).view(torch.bfloat16),
+                                                          dn, E, tid, coef, ws, M, A)))
+    assert np.all(np.isnan(y[1])) and np.all(np.isnan(y[3])) and not np.isnan(y[[0, 2]]).any()
+
+
+def test_perslot_kernels_match_grouped():
+    say("per-slot")
+    M, A, E, H, I = 3, 4, 16, 512, 128
+    gu, dn = _experts(4, E, H, I)
+    x = orc.gen_bf16_normal(orc.tensor_key(5, "x"), 1.0, (M, H))
+    ids = np.random.default_rng(2).integers(0, E, (M, A)).astype(np.int32)
+    tid = torch.from_numpy(ids).to(DEV)
+    err = moe.zero_err()
+    h = moe.experts_gather(bf16(x), gu, E, tid, err, swiglu=True)
+    b, q, s, m, G = qspec(gu)
+    href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G), E, ids)
+    assert rel_err(to_np(h), href) < 1e-2
+    ws, _ = moe.moe_group_routes(tid, E)
+    hg = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)
+    assert torch.equal(h, hg)  # same per-slot MFMA sequence, so the same bits
+    g = moe.experts_gather(bf16(x), gu, E, tid, err)
+    gg = moe.experts_gather_grouped(bf16(x), gu, E, ws, M, A)
+    assert torch.equal(g, gg)
+    coef = torch.from_numpy(np.random.default_rng(3).random((M, A)).astype(np.float32)).to(DEV)
+    y = moe.experts_combine(h, dn, E, tid, coef, err)
+    yg = moe.experts_combine_grouped(h, dn, E, tid, coef, ws, M, A)
+    assert torch.equal(y, yg)  # per-slot dots summed over a in order: the same arithmetic
+    assert to_np(err)[0] == 0
+    bad = tid.clone()
+    bad[1, 2] = E + 5
+    y = moe.experts_combine(h, dn, E, bad, coef, err)
+    assert torch.isnan(y[1].float()).all() and not torch.isnan(y[[0, 2]].float()).any()
+    assert to_np(err).view(np.uint32).tolist() == [1, E + 5, 6]
+
+
+def test_linear_q8_and_swiglu():
+    say("linear_q8 / swiglu")
+    M, N, K = 20, 1024, 3072
+    w = moe.QWeight.synth(8, 9, "sh_gu_q", "sh_gu_s", 0, N, K, 64)
+    x = orc.gen_bf16_normal(orc.tensor_key(9, "x"), 1.0, (M, K))
+    y = moe.linear_q8(bf16(x), w)
+    ref = orc.dense(x, orc.qview(*qspec(w)[:4], N, K, 64))
+    assert rel_err(to_np(y), ref) < 1e-2
+    yf = moe.linear_q8(bf16(x), w, out_dtype=torch.float32)
+    assert torch.equal(yf.to(torch.bfloat16), y)
+    h = moe.swiglu(y, N // 2)
+    href = orc.swiglu_bf16(to_np(y), N // 2)
+    assert np.abs(to_np(h).astype(np.int32) - href.astype(np.int32)).max() <= 1  # expf ulps
+
+
+def test_shared_add_and_inject():
+    say("shared add")
+    M, N = 16, 3072
+    rng = np.random.default_rng(4)
+    y0 = orc.f32_to_bf16(rng.standard_normal((M, N)).astype(np.float32))
+    s = orc.f32_to_bf16(rng.standard_normal((M, N)).astype(np.float32))
+    gl = rng.standard_normal((M, 5)).astype(np.float32)
+    gl[3, 2] = np.nan
+    x = orc.f32_to_bf16(rng.standard_normal((M, 4 * N)).astype(np.float32))
+    w_in = rng.standard_normal((M, 4)).astype(np.float32)
+    y = bf16(y0.copy())
+    err = moe.zero_err()
+    moe.moe_shared_add(y, bf16(s), torch.from_numpy(np.ascontiguousarray(gl[:, 2])).to(DEV), 1, 512, err)
+    g = 1 / (1 + np.exp(-gl[:, 2:3].astype(np.float64)))
+    ref = orc.bf16_to_f32(y0) + g * orc.bf16_to_f32(s)
+    got = orc.bf16_to_f32(to_np(y))
+    assert np.all(np.isnan(got[3])) and to_np(err).view(np.uint32).tolist() == [1, 3, 512]
+    ok = np.arange(M) != 3
+    assert np.abs(got[ok] - ref[ok]).max() <= 2 ** -7 * np.abs(ref[ok]).max()
+    # inject: bit-identical to the add then x += w_in * y on the stored y
+    y2, xt, err2 = bf16(y0.copy()), bf16(x.copy()), moe.zero_err()
+    glt = torch.from_numpy(gl).to(DEV)
+    moe.moe_shared_add_inject(y2, bf16(s), glt[:, 1:], 5, 512, xt, torch.from_numpy(w_in).to(DEV), 4, err2)
+    y3 = bf16(y0.copy())
+    moe.moe_shared_add(y3, bf16(s), glt[:, 1:], 5, 512, moe.zero_err())
+    assert torch.equal(y2, y3)
+    xf = orc.bf16_to_f32(x).reshape(M, 4, N).astype(np.float64)
+    xr = xf + w_in[:, :, None] * orc.bf16_to_f32(to_np(y3))[:, None, :]
+    assert np.abs(orc.bf16_to_f32(to_np(xt)).reshape(M, 4, N) - xr).max() <= 2 ** -7 * np.abs(xr).max()
+
+
+# ---- the sublayer ------------------------------------------------------------------------------------------------
+def _layer_parity(layer, M, seed, logits_in=None, sample=None):
+    x = moe.synth_bf16_normal(seed, "x", 0, (M, layer.H), 1.0)
+    out = layer.forward(x, logits_in=logits_in)
+    torch.cuda.synchronize()
+    w = oracle_weights(layer)
+    xn = to_np(x)
+    rows = np.arange(M) if sample is None else np.sort(np.random.default_rng(seed).choice(M, sample, replace=False))
+    lg = None if logits_in is None else np.ascontiguousarray(to_np(logits_in)[rows])
+    o = orc.moe_layer(w, np.ascontiguousarray(xn[rows]), logits_in=lg)
+    ids = to_np(out["ids"])
+    assert np.array_equal(ids[rows], o["ids"]), "routing differs from the oracle"
+    assert np.allclose(to_np(out["coef"])[rows], o["coef"], rtol=2e-6, atol=1e-7)
+    e = rel_err(to_np(out["y"])[rows], o["y"])
+    assert e < 1e-2, e
+    assert rel_err(to_np(out["x_out"])[rows], o["out"]) < 1e-2
+    assert to_np(out["err"])[0] == 0 and to_np(out["err"])[3] == 0
+    return out, o, e
+
+
+def test_layer_config1_decode_q8():
+    """1 token, H 2048, 64 experts, top-8, I 512, Q8 routed experts, no shared expert."""
+    say("layer cfg1")
+    layer = moe.MoeLayer.synth(2048, 64, 8, 512, seed=0, routed_bits=8, shared=False)
+    _, _, e = _layer_parity(layer, 1, 0)
+    say("cfg1 rel err", e)
+
+
+def test_layer_config2_decode_16_tokens():
+    """2 slots x (1 + 7 MTP drafts) = 16 tokens, H 3072, 512 experts, top-10 + shared Q8."""
+    say("layer cfg2")
+    layer = moe.MoeLayer.synth(3072, 512, 10, 512, seed=0)
+    out, o, e = _layer_parity(layer, 16, 0)
+    say("cfg2 rel err", e)
+    # grouping of the layer's routing
+    ws, _ = moe.moe_group_routes(out["ids"], 512)
+    off, _, _ = orc.group_routes(o["ids"], 512)
+    assert np.array_equal(to_np(moe.route_tables(ws, 16, 10, 512)["offsets"]), off)
+
+
+def test_layer_config3_uniform_logits():
+    """512-token prefill chunk with uniform random router logits (the router GEMV bypassed)."""
+    say("layer cfg3")
+    layer = moe.MoeLayer.synth(3072, 512, 10, 512, seed=0)
+    lg = moe.synth_uniform_pm1(0, "logits", 0, (512, 513))
+    _layer_parity(layer, 512, 1, logits_in=lg, sample=48)
+
+
+def test_layer_config4_zipf_prefill():
+    """4096-token prefill, router biased to Zipf(1.1) expert popularity: every token's routing
+    bit-exact, the output on 48 seeded tokens."""
+    say("layer cfg4")
+    bias = torch.from_numpy(zipf_bias(0, 512, 1.0)).to(DEV)
+    layer = moe.MoeLayer.synth(3072, 512, 10, 512, seed=0, router_bias=bias)
+    out, o, e = _layer_parity(layer, 4096, 0, sample=48)
+    # routing on all tokens: the oracle's canonical logits for every token
+    x = to_np(moe.synth_bf16_normal(0, "x", 0, (4096, 3072), 1.0))
+    lg = orc.router_logits(x, to_np(layer.router), bias=to_np(bias))
+    rids, _, _ = orc.topk(lg, 512, 10)
+    assert np.array_equal(to_np(out["ids"]), rids)
+    cnt = np.bincount(rids.ravel(), minlength=512)
+    assert cnt.min() == 0 and cnt.max() > 400  # the load imbalance the config asks for
