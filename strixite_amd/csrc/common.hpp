@@ -1,5 +1,5 @@
 // Shared host + device pieces of the gfx950 MoE library: precondition errors, HIP launch checks, bf16 / f16 bit
-// helpers, the weight views the launchers take, and the wave64 MFMA operand decoders for the Q4 / Q8 block layout.
+// helpers, and the wave64 MFMA operand decoders for the Q4 / Q8 block layout.
 #pragma once
 
 #include "strixite_moe.hpp"
@@ -49,10 +49,7 @@ inline bool disjoint(const void *a, int64_t an, const void *b, int64_t bn) {
 // ---- device bit helpers ---------------------------------------------------------------------------------------
 namespace dev {
 
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
-typedef float float16v __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 // RNE, NaN kept quiet (strixite common/bf16.hpp:19-26).
@@ -65,65 +62,65 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 __device__ __forceinline__ float qnan() { return __uint_as_float(0x7fc00000u); }
 
-__device__ __forceinline__ half2v as_h2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
-__device__ __forceinline__ uint32_t h2_bits(half2v h) { return __builtin_bit_cast(uint32_t, h); }
-
-// A bf16 scale or min as a splatted f16 pair (exact for values in f16's normal range).
-__device__ __forceinline__ half2v bf16_splat_h2(uint16_t b) {
-    const _Float16 h = (_Float16)bf16_to_f32(b);
-    return half2v{h, h};
-}
 
 // ---- MFMA operand decoders ------------------------------------------------------------------------------------
-// Every MFMA here is v_mfma_f32_16x16x32_f16: a lane supplies 8 f16 of an A row and 8 of a B column for the same
-// 8 k positions. Which 8 k a lane's slots stand for is this file's choice, made identically for A (weights) and B
-// (activations), so the product is the plain dot product. For 8 consecutive codes k0..k7 the slot order is
-//   [k0, k4, k1, k5, k2, k6, k3, k7]
-// - the order in which a Q4 dword's nibbles fall out of (w >> 4j) & 0x000F000F without any byte shuffling.
+// The expert kernels use v_mfma_f32_16x16x32_bf16 with A = activations (16 token rows) and B = weights (16 weight
+// rows as columns): a lane supplies 8 bf16 of a token row and 8 of a weight row for the same 8 k positions. Which
+// 8 k a lane's slots stand for is chosen identically for A and B, so the product is the plain dot product.
 //
-// Dequantization: w = f16(code * s + m), one rounding (strixite kernels/wmma_gemm.hpp:120-141 uses the same
-// one-rounding F16 form). code -> f16 by the exponent trick: the f16 bits 0x6400 | c are 1024 + c exactly for
-// c < 1024, so subtracting 1024 is exact; then one packed fma with (s, m).
+// Weights enter as their exact integer codes ("scaled codes"): D = sum_k code_k * x_k over one quantization group,
+// then w . x = s * D + m * sum_k x_k on the FP32 accumulator (code * s + m per formats/q4.hpp:3-6). Nothing is
+// rounded on the weight side; activations stay bf16 (full range).
+//
+// Q4: the bf16 bits 0x4300 | n are exactly 128 + n (n < 16), so a byte shuffle with the constant 0x43 turns a
+// masked dword into bf16 pairs; the offset is folded into the min: m' = m - 128 s. The pairs come out as
+//   [k0, k2, k4, k6, k1, k3, k5, k7]
+// of the dword's 8 codes (even nibbles, then odd), and the activations are shuffled to the same order.
+// Q8: codes 0..255 are exact in bf16 (8 significant bits): byte -> f32 (v_cvt_f32_ubyte) -> high half; natural order.
 
-__device__ __forceinline__ half2v dq_pair(uint32_t bits_1024, half2v s, half2v m) {
-    const half2v c = as_h2(bits_1024) - half2v{(_Float16)1024.0f, (_Float16)1024.0f};
-    return __builtin_elementwise_fma(c, s, m);
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+struct Frag {  // 8 bf16 as 4 dwords
+    uint32_t d[4];
+};
+__device__ __forceinline__ bf16x8v as_bf16x8(const Frag &f) { return __builtin_bit_cast(bf16x8v, f); }
+
+__device__ __forceinline__ Frag q4_codes_to_bf16(uint32_t w) {
+    const uint32_t t = w & 0x0F0F0F0Fu, u = (w >> 4) & 0x0F0F0F0Fu, c = 0x43434343u;
+    // perm(S0 = c, S1 = t, sel): selector 0..3 picks t's bytes, 4..7 c's
+    return Frag{{__builtin_amdgcn_perm(c, t, 0x04010400u), __builtin_amdgcn_perm(c, t, 0x04030402u),
+                 __builtin_amdgcn_perm(c, u, 0x04010400u), __builtin_amdgcn_perm(c, u, 0x04030402u)}};
 }
 
-// Q4: one dword = codes k0..k7 (low nibble = even k, formats/q4.hpp:4) -> A slots [k0,k4,k1,k5,k2,k6,k3,k7].
-__device__ __forceinline__ half8v dq4_dword(uint32_t w, half2v s, half2v m) {
-    const half2v p0 = dq_pair((w & 0x000F000Fu) | 0x64006400u, s, m);
-    const half2v p1 = dq_pair(((w >> 4) & 0x000F000Fu) | 0x64006400u, s, m);
-    const half2v p2 = dq_pair(((w >> 8) & 0x000F000Fu) | 0x64006400u, s, m);
-    const half2v p3 = dq_pair(((w >> 12) & 0x000F000Fu) | 0x64006400u, s, m);
-    return half8v{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+// 8 natural-order bf16 activations -> the Q4 slot order [k0, k2, k4, k6, k1, k3, k5, k7]
+__device__ __forceinline__ Frag q4_order(const uint4 &v) {
+    return Frag{{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
+                 __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)}};
 }
 
-// Q8: two dwords = codes k0..k3, k4..k7 (one byte each) -> the same slot order, bytes paired by v_perm_b32.
-__device__ __forceinline__ half8v dq8_dwords(uint32_t lo, uint32_t hi, half2v s, half2v m) {
-    // perm(S0 = hi, S1 = lo, sel): byte selector 0..3 picks lo's bytes, 4..7 hi's, 0x0C gives 0x00.
-    const half2v p0 = dq_pair(__builtin_amdgcn_perm(hi, lo, 0x0C040C00u) | 0x64006400u, s, m);
-    const half2v p1 = dq_pair(__builtin_amdgcn_perm(hi, lo, 0x0C050C01u) | 0x64006400u, s, m);
-    const half2v p2 = dq_pair(__builtin_amdgcn_perm(hi, lo, 0x0C060C02u) | 0x64006400u, s, m);
-    const half2v p3 = dq_pair(__builtin_amdgcn_perm(hi, lo, 0x0C070C03u) | 0x64006400u, s, m);
-    return half8v{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+__device__ __forceinline__ uint32_t hi16_pair(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+// Q8: two dwords = codes k0..k7 -> bf16 in natural order
+__device__ __forceinline__ Frag q8_codes_to_bf16(uint32_t lo, uint32_t hi) {
+    return Frag{{hi16_pair((float)(lo & 0xFF), (float)((lo >> 8) & 0xFF)),
+                 hi16_pair((float)((lo >> 16) & 0xFF), (float)(lo >> 24)),
+                 hi16_pair((float)(hi & 0xFF), (float)((hi >> 8) & 0xFF)),
+                 hi16_pair((float)((hi >> 16) & 0xFF), (float)(hi >> 24))}};
 }
 
-// B operand: 8 consecutive bf16 activations (16 bytes) -> f16 in the slot order above. bf16 -> f16 rounds toward
-// zero (v_cvt_pkrtz): exact for values in f16's normal range, which the activations must lie in.
-__device__ __forceinline__ half2v pkrtz(float a, float b) {
-    return __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
-}
-__device__ __forceinline__ half8v bf16x8_to_b(uint4 v) {
-    const half2v p0 = pkrtz(__uint_as_float(v.x << 16), __uint_as_float(v.z << 16));
-    const half2v p1 = pkrtz(__uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.z & 0xffff0000u));
-    const half2v p2 = pkrtz(__uint_as_float(v.y << 16), __uint_as_float(v.w << 16));
-    const half2v p3 = pkrtz(__uint_as_float(v.y & 0xffff0000u), __uint_as_float(v.w & 0xffff0000u));
-    return half8v{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+// sum of the 8 bf16 activations of a fragment, FP32 (v_dot2_f32_bf16 against (1, 1))
+__device__ __forceinline__ float frag_sum(const uint4 &v, float acc) {
+    const bf16x2v one = __builtin_bit_cast(bf16x2v, 0x3F803F80u);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.x), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.y), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.z), one, acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.w), one, acc, false);
 }
 
-__device__ __forceinline__ float4v mfma16(half8v a, half8v b, float4v c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ float4v mfma_bf16(const Frag &a, const Frag &b, float4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }  // strixite kernels/swiglu.hip:22

@@ -2,13 +2,16 @@
 // experts, the per-slot decode forms, the dense Q8 projection (the shared expert), the ordered combine reduce
 // (the routing-weighted un-permute) and the standalone SwiGLU.
 //
-// One kernel family does every projection. A wave64 owns a 16-slot token tile (the B operand's 16 columns: the
-// slots of one expert's bucket, 16 dense tokens, or one slot) and two 16-row weight tiles (SwiGLU: gate rows j0..
-// j0+15 and the matching up rows; otherwise 32 consecutive rows). Each K step ("span") a lane loads 16 bytes of
-// codes per weight tile - 64 contiguous bytes per row per span across the lane's 4 lane groups - its rows' scale and
-// min, and 8 activations per MFMA; dequantizes in registers (common.hpp: f16(code * s + m), one rounding) and issues
-// v_mfma_f32_16x16x32_f16. FP32 accumulation over all of K. A span (Q4: 128 codes, Q8: 64) never crosses a group,
-// so G must be a multiple of it: Q4 G = 128, Q8 G = 64 or 128 (the reference's served layout: q4g128, q8g64).
+// One kernel family does every projection. A wave64 owns a 16-slot token tile (the MFMA's A rows: the slots of one
+// expert's bucket, 16 dense tokens, or one slot) and two 16-row weight tiles (B columns; SwiGLU: gate rows j0..j0+15
+// and the matching up rows, else 32 consecutive rows). Each K step ("span", one quantization group or half of one)
+// a lane loads 16 bytes of codes per weight tile - 64 contiguous bytes per row across the lane's 4 lane groups -,
+// its row's scale and min, and 8 activations per MFMA; the codes go to bf16 exactly (common.hpp), one
+// v_mfma_f32_16x16x32_bf16 per 32 k, and each span's sum is rescaled on the FP32 accumulator:
+//   acc += s * D_span + m' * sum(x over the span)
+// D layout: lane (j, g) holds tokens 4g..4g+3 of weight column j, so a lane's outputs share one row's (s, m).
+// A span (Q4: 128 codes, Q8: 64) never crosses a group: Q4 needs G = 128, Q8 G = 64 or 128 (the reference's
+// served layout: q4g128, q8g64).
 #include "common.hpp"
 
 #include <type_traits>
@@ -37,7 +40,7 @@ template <int BITS> struct QFmt {
 };
 
 struct GemmArgs {
-    const uint16_t *x;  // B rows (bf16, or f16 bits when XF16), row stride K
+    const uint16_t *x;  // A rows (bf16, or f16 bits when XF16), row stride K
     const uint8_t *q;
     const uint16_t *scale, *minv;
     int64_t N;          // weight rows per expert
@@ -51,69 +54,61 @@ struct GemmArgs {
 
 __device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// 8 f16 (natural order, 16 bytes) into the MFMA slot order [k0,k4,k1,k5,k2,k6,k3,k7]
-__device__ __forceinline__ half8v f16x8_to_b(uint4 v) {
-    const half2v p0 = as_h2(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u));
-    const half2v p1 = as_h2(__builtin_amdgcn_perm(v.z, v.x, 0x07060302u));
-    const half2v p2 = as_h2(__builtin_amdgcn_perm(v.w, v.y, 0x05040100u));
-    const half2v p3 = as_h2(__builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
-    return half8v{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-}
-
-template <bool XF16> __device__ __forceinline__ half8v load_b(const uint16_t *p) {
-    const uint4 v = ld16(p);
-    if constexpr (XF16) return f16x8_to_b(v);
-    else return bf16x8_to_b(v);
-}
-
-template <int BITS> __device__ __forceinline__ half8v dq(const uint4 &c, int t, half2v s, half2v m) {
-    if constexpr (BITS == 4) {
-        const uint32_t w = t == 0 ? c.x : t == 1 ? c.y : t == 2 ? c.z : c.w;
-        return dq4_dword(w, s, m);
-    } else {
-        return t == 0 ? dq8_dwords(c.x, c.y, s, m) : dq8_dwords(c.z, c.w, s, m);
+// f16 activations (the h_f16 form) -> bf16 bits, 8 at a time
+__device__ __forceinline__ uint4 f16x8_to_bf16x8(const uint4 &v) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFF));
+        const float hi = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+        o[i] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
     }
+    return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// The token tile of this block (B columns) and its expert. Lane column j = lane % 16.
+template <int BITS> __device__ __forceinline__ Frag b_frag(const uint4 &c, int u) {
+    if constexpr (BITS == 4) return q4_codes_to_bf16(u == 0 ? c.x : u == 1 ? c.y : u == 2 ? c.z : c.w);
+    else return u == 0 ? q8_codes_to_bf16(c.x, c.y) : q8_codes_to_bf16(c.z, c.w);
+}
+template <int BITS> __device__ __forceinline__ Frag a_frag(const uint4 &v) {
+    if constexpr (BITS == 4) return q4_order(v);
+    else return Frag{{v.x, v.y, v.z, v.w}};
+}
+
+// The token tile of this block and its expert. Token j of the tile (j < 16) is slot(j), -1 past the tile's rows.
 struct Tile {
     int64_t expert;
-    bool nan;        // invalid ids: outputs are NaN
-    bool valid;      // this lane's column holds a slot
-    int64_t xrow;    // B row of the lane's column
-    int64_t orow;    // output row of the lane's column
+    bool nan;   // invalid ids: outputs are NaN
+    int rows;
+    int64_t st;  // GROUPED: first index into slots[]; DENSE: first token; PERSLOT: the slot
 };
 
-template <int MODE, bool XROW_DIV>
+template <int MODE>
 __device__ __forceinline__ bool get_tile(const GemmArgs &a, Tile &t) {
-    const int j = (int)(threadIdx.x % 16);
     if constexpr (MODE == GROUPED) {
         const int64_t S = a.ws[1], E = a.ws[2];
         const int64_t tile = blockIdx.y;
         if (tile >= a.ws[0]) return false;
         const int32_t bucket = a.ws[route::t16_bucket_at(S, E) + tile], st = a.ws[route::t16_start_at(S, E) + tile];
         const int32_t end = a.ws[4 + bucket + 1];
-        const int rows = end - st < 16 ? end - st : 16;
+        t.rows = end - st < 16 ? end - st : 16;
         t.expert = bucket;
         t.nan = bucket >= a.E;
-        t.valid = j < rows;
-        const int64_t slot = t.valid ? a.ws[4 + E + 2 + st + j] : 0;
-        t.xrow = XROW_DIV ? slot / a.A : slot;
-        t.orow = slot;
+        t.st = st;
     } else if constexpr (MODE == DENSE) {
         const int64_t m0 = (int64_t)blockIdx.y * 16;
         t.expert = 0;
         t.nan = false;
-        t.valid = m0 + j < a.M;
-        t.xrow = t.orow = t.valid ? m0 + j : 0;
+        t.rows = a.M - m0 < 16 ? (int)(a.M - m0) : 16;
+        t.st = m0;
     } else {
         const int64_t slot = blockIdx.y;
         const int32_t id = a.ids[slot];
         t.nan = id < 0 || id >= a.E;
         t.expert = t.nan ? 0 : id;
-        t.valid = j == 0;
-        t.xrow = XROW_DIV ? slot / a.A : slot;
-        t.orow = slot;
+        t.rows = 1;
+        t.st = slot;
         if (t.nan && blockIdx.x == 0 && threadIdx.x == 0 && atomicCAS(&a.err[0], 0u, 1u) == 0u) {
             a.err[1] = (uint32_t)id;
             a.err[2] = (uint32_t)slot;
@@ -122,33 +117,98 @@ __device__ __forceinline__ bool get_tile(const GemmArgs &a, Tile &t) {
     return true;
 }
 
-template <typename T> __device__ __forceinline__ void store4(T *p, const float (&v)[4]);
-template <> __device__ __forceinline__ void store4<uint16_t>(uint16_t *p, const float (&v)[4]) {
-    const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-    const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-    *reinterpret_cast<uint2 *>(p) = make_uint2(lo, hi);
-}
-template <> __device__ __forceinline__ void store4<float>(float *p, const float (&v)[4]) {
-    *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+template <int MODE> __device__ __forceinline__ int64_t slot_of(const GemmArgs &a, const Tile &t, int j) {
+    if (j >= t.rows) return -1;
+    if constexpr (MODE == GROUPED) return a.ws[4 + a.ws[2] + 2 + t.st + j];
+    else return t.st + j;
 }
 
-// h as f16 bits of its bf16 rounding (exact conversion in f16's range), for a down projection that reads f16.
-__device__ __forceinline__ void store4_hf16(uint16_t *p, const float (&v)[4]) {
-    uint16_t b[4];
+template <typename T> __device__ __forceinline__ void store1(T *p, float v);
+template <> __device__ __forceinline__ void store1<uint16_t>(uint16_t *p, float v) { *p = f32_to_bf16(v); }
+template <> __device__ __forceinline__ void store1<float>(float *p, float v) { *p = v; }
+// h as f16 bits of its bf16 rounding (the reference's h_f16 form)
+__device__ __forceinline__ void store1_hf16(uint16_t *p, float v) {
+    *p = __builtin_bit_cast(uint16_t, (_Float16)bf16_round(v));
+}
+
+// One 16-token x (2 x 16)-row wave tile over all of K: returns acc[rt][r] = token 4g + r, weight column (lane % 16)
+// of tile rt.
+template <int BITS, bool XF16>
+__device__ __forceinline__ void wave_gemm(const GemmArgs &a, const uint16_t *xrow, const int64_t (&tile_row)[2],
+                                          float4v (&acc)[2]) {
+    using F = QFmt<BITS>;
+    const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
+    const int64_t row_bytes = a.K * BITS / 8, groups = a.K / a.G;
+    const uint8_t *qp[2];
+    const uint16_t *sp[2], *mp[2];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) b[r] = __builtin_bit_cast(uint16_t, (_Float16)bf16_round(v[r]));
-    *reinterpret_cast<uint2 *>(p) = make_uint2(b[0] | ((uint32_t)b[1] << 16), b[2] | ((uint32_t)b[3] << 16));
+    for (int rt = 0; rt < 2; ++rt) {
+        const int64_t r = tile_row[rt] + j;
+        qp[rt] = a.q + r * row_bytes + g * 16;
+        sp[rt] = a.scale + r * groups;
+        mp[rt] = a.minv + r * groups;
+    }
+    const uint16_t *xp = xrow ? xrow + g * F::CPL : nullptr;
+    acc[0] = float4v{0, 0, 0, 0};
+    acc[1] = float4v{0, 0, 0, 0};
+    const int64_t spans = a.K / F::SPAN;
+    // software pipeline: span s + 1's loads are in flight during span s's math
+    uint4 cq[2], xv[F::NT];
+    uint16_t cs[2], cm[2];
+    auto fetch = [&](int64_t s) {
+        const int64_t gi = s * F::SPAN / a.G;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            cq[rt] = ld16(qp[rt] + s * 64);
+            cs[rt] = sp[rt][gi];
+            cm[rt] = mp[rt][gi];
+        }
+#pragma unroll
+        for (int u = 0; u < F::NT; ++u) xv[u] = xp ? ld16(xp + s * F::SPAN + 8 * u) : make_uint4(0, 0, 0, 0);
+    };
+    fetch(0);
+    for (int64_t s = 0; s < spans; ++s) {
+        const uint4 q0 = cq[0], q1 = cq[1];
+        float sc[2], mn[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            sc[rt] = bf16_to_f32(cs[rt]);
+            mn[rt] = BITS == 4 ? bf16_to_f32(cm[rt]) - 128.0f * sc[rt] : bf16_to_f32(cm[rt]);
+        }
+        Frag af[F::NT];
+        float xs = 0.f;
+#pragma unroll
+        for (int u = 0; u < F::NT; ++u) {
+            const uint4 v = XF16 ? f16x8_to_bf16x8(xv[u]) : xv[u];
+            af[u] = a_frag<BITS>(v);
+            xs = frag_sum(v, xs);
+        }
+        if (s + 1 < spans) fetch(s + 1);
+        float4v d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < F::NT; ++u) {
+            d0 = mfma_bf16(af[u], b_frag<BITS>(q0, u), d0);
+            d1 = mfma_bf16(af[u], b_frag<BITS>(q1, u), d1);
+        }
+        // the span's activation sum per token: over the 4 lane groups, then to the lanes holding tokens 4g..4g+3
+        xs += __shfl_xor(xs, 16, kWave);
+        xs += __shfl_xor(xs, 32, kWave);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float xr = __shfl(xs, 4 * g + r, kWave);
+            acc[0][r] = fmaf(sc[0], d0[r], fmaf(mn[0], xr, acc[0][r]));
+            acc[1][r] = fmaf(sc[1], d1[r], fmaf(mn[1], xr, acc[1][r]));
+        }
+    }
 }
 
 // Grid: x over weight-row blocks (kWaves waves x 32 rows, or x 16 SwiGLU columns), y over token tiles.
 template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
 __global__ void __launch_bounds__(kThreads) expert_gemm_kernel(GemmArgs a) {
-    using F = QFmt<BITS>;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int g = lane / 16, i = lane % 16;
+    const int g = lane / 16, j = lane % 16;
     Tile t;
-    if (!get_tile<MODE, XROW_DIV>(a, t)) return;  // uniform per block; no barrier in this kernel
-    // this wave's two weight tiles, as rows of the stacked matrix
+    if (!get_tile<MODE>(a, t)) return;  // uniform per block; no barrier in this kernel
     const int64_t I = a.N / 2;
     int64_t tile_row[2];
     int64_t c0;  // SwiGLU: first h column; else first output row (within the expert)
@@ -163,102 +223,49 @@ __global__ void __launch_bounds__(kThreads) expert_gemm_kernel(GemmArgs a) {
         tile_row[0] = t.expert * a.N + c0;
         tile_row[1] = t.expert * a.N + (c0 + 16 < a.N ? c0 + 16 : c0);  // a.N % 16 == 0: the tile exists or is skipped
     }
+    // output rows of this lane's tokens 4g + r
+    int64_t orow[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) orow[r] = slot_of<MODE>(a, t, 4 * g + r);
+    float4v acc[2];
     if (t.nan) {
-        if (t.valid) {
-            const float v[4] = {qnan(), qnan(), qnan(), qnan()};
-            if constexpr (EPI == EPI_SWIGLU) {
-                uint16_t *h = static_cast<uint16_t *>(a.y) + t.orow * a.ldy + c0 + 4 * g;
-                if constexpr (HF16) store4_hf16(h, v);
-                else store4(h, v);
-            } else {
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const int64_t n = c0 + 16 * rt + 4 * g;
-                    if (n < a.N) {
-                        if constexpr (EPI == EPI_F32) store4(static_cast<float *>(a.y) + t.orow * a.ldy + n, v);
-                        else store4(static_cast<uint16_t *>(a.y) + t.orow * a.ldy + n, v);
-                    }
-                }
-            }
-        }
-        return;
+        acc[0] = acc[1] = float4v{qnan(), qnan(), qnan(), qnan()};
+    } else {
+        const int64_t my = slot_of<MODE>(a, t, j);  // this lane's A row (token j)
+        const uint16_t *xrow = my < 0 ? nullptr : a.x + (XROW_DIV ? my / a.A : my) * a.K;
+        wave_gemm<BITS, XF16>(a, xrow, tile_row, acc);
     }
-    const int64_t row_bytes = a.K * BITS / 8, groups = a.K / a.G;
-    const uint8_t *qp[2];
-    const uint16_t *sp[2], *mp[2];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const int64_t r = tile_row[rt] + i;
-        qp[rt] = a.q + r * row_bytes + g * 16;
-        sp[rt] = a.scale + r * groups;
-        mp[rt] = a.minv + r * groups;
-    }
-    const uint16_t *xp = a.x + t.xrow * a.K + g * F::CPL;
-    float4v acc[2] = {float4v{0, 0, 0, 0}, float4v{0, 0, 0, 0}};
-    const int64_t spans = a.K / F::SPAN;
-    // software pipeline: span s + 1's loads are in flight during span s's math
-    uint4 cq[2];
-    uint16_t cs[2], cm[2];
-    uint4 xb[F::NT];
-    auto fetch = [&](int64_t s) {
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            cq[rt] = ld16(qp[rt] + s * 64);
-            const int64_t gi = s * F::SPAN / a.G;
-            cs[rt] = sp[rt][gi];
-            cm[rt] = mp[rt][gi];
-        }
-#pragma unroll
-        for (int u = 0; u < F::NT; ++u) xb[u] = t.valid ? ld16(xp + s * F::SPAN + 8 * u) : make_uint4(0, 0, 0, 0);
-    };
-    fetch(0);
-    for (int64_t s = 0; s < spans; ++s) {
-        const uint4 q0 = cq[0], q1 = cq[1];
-        const half2v s0 = bf16_splat_h2(cs[0]), m0 = bf16_splat_h2(cm[0]);
-        const half2v s1 = bf16_splat_h2(cs[1]), m1 = bf16_splat_h2(cm[1]);
-        half8v b[F::NT];
-#pragma unroll
-        for (int u = 0; u < F::NT; ++u) {
-            if constexpr (XF16) b[u] = f16x8_to_b(xb[u]);
-            else b[u] = bf16x8_to_b(xb[u]);
-        }
-        if (s + 1 < spans) fetch(s + 1);
-#pragma unroll
-        for (int u = 0; u < F::NT; ++u) {
-            acc[0] = mfma16(dq<BITS>(q0, u, s0, m0), b[u], acc[0]);
-            acc[1] = mfma16(dq<BITS>(q1, u, s1, m1), b[u], acc[1]);
-        }
-    }
-    // D layout: lane (i, g) holds rows 4g + r (r = 0..3) of column i (the lane's token column is i too)
-    if (!t.valid) return;
     if constexpr (EPI == EPI_SWIGLU) {
-        float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = silu(acc[0][r]) * acc[1][r];
-        uint16_t *h = static_cast<uint16_t *>(a.y) + t.orow * a.ldy + c0 + 4 * g;
-        if constexpr (HF16) store4_hf16(h, v);
-        else store4(h, v);
+        for (int r = 0; r < 4; ++r)
+            if (orow[r] >= 0) {
+                uint16_t *h = static_cast<uint16_t *>(a.y) + orow[r] * a.ldy + c0 + j;
+                const float v = t.nan ? qnan() : silu(acc[0][r]) * acc[1][r];
+                if constexpr (HF16) store1_hf16(h, v);
+                else store1(h, v);
+            }
     } else {
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-            const int64_t n = c0 + 16 * rt + 4 * g;
-            if (n < a.N) {
-                const float v[4] = {acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]};
-                if constexpr (EPI == EPI_F32) store4(static_cast<float *>(a.y) + t.orow * a.ldy + n, v);
-                else store4(static_cast<uint16_t *>(a.y) + t.orow * a.ldy + n, v);
-            }
+            const int64_t n = c0 + 16 * rt + j;
+            if (rt == 1 && c0 + 16 >= a.N) break;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (orow[r] >= 0) {
+                    if constexpr (EPI == EPI_F32) store1(static_cast<float *>(a.y) + orow[r] * a.ldy + n, acc[rt][r]);
+                    else store1(static_cast<uint16_t *>(a.y) + orow[r] * a.ldy + n, acc[rt][r]);
+                }
         }
     }
 }
 
 // Per-slot combine (strixite kernels/linear_q4.hip:283-322): y[m, n] = sum_a coef[m, a] * (h[m, a, :] . Wd[id] row n),
-// the slot dots in FP32 from the MFMA, summed over a in order with fmaf, rounded once. One token a block column
-// (B column 0), two 16-row tiles a wave. Any invalid id of the token: NaN row, err.
+// the slot dots in FP32 from the MFMA (token row 0 of the tile), summed over a in order with fmaf, rounded once.
+// Two 16-row tiles a wave. Any invalid id of the token: NaN row, err.
 template <int BITS, bool XF16>
 __global__ void __launch_bounds__(kThreads) perslot_combine_kernel(GemmArgs a, const float *coef) {
-    using F = QFmt<BITS>;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int g = lane / 16, i = lane % 16;
+    const int g = lane / 16, j = lane % 16;
     const int64_t m = blockIdx.y;
     const int64_t c0 = ((int64_t)blockIdx.x * kWaves + wave) * 32;
     if (c0 >= a.N) return;
@@ -274,49 +281,25 @@ __global__ void __launch_bounds__(kThreads) perslot_combine_kernel(GemmArgs a, c
             break;
         }
     }
+    float out[2] = {0.f, 0.f};
+    if (ok) {
+        for (int64_t s = 0; s < a.A; ++s) {
+            const int64_t e = a.ids[m * a.A + s];
+            const int64_t tile_row[2] = {e * a.N + c0, e * a.N + (c0 + 16 < a.N ? c0 + 16 : c0)};
+            float4v acc[2];
+            wave_gemm<BITS, XF16>(a, j == 0 ? a.x + (m * a.A + s) * a.K : nullptr, tile_row, acc);
+            const float c = coef[m * a.A + s];
+            out[0] = fmaf(c, acc[0][0], out[0]);
+            out[1] = fmaf(c, acc[1][0], out[1]);
+        }
+    } else {
+        out[0] = out[1] = qnan();
+    }
     uint16_t *yrow = static_cast<uint16_t *>(a.y) + m * a.ldy;
-    if (!ok) {
-        if (i == 0)
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const int64_t n = c0 + 16 * rt + 4 * g;
-                const float v[4] = {qnan(), qnan(), qnan(), qnan()};
-                if (n < a.N) store4(yrow + n, v);
-            }
-        return;
+    if (g == 0) {  // token 0 of the tile: lanes 0..15, r = 0
+        store1(yrow + c0 + j, out[0]);
+        if (c0 + 16 < a.N) store1(yrow + c0 + 16 + j, out[1]);
     }
-    const int64_t row_bytes = a.K * BITS / 8, groups = a.K / a.G, spans = a.K / F::SPAN;
-    float out[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-    for (int64_t s = 0; s < a.A; ++s) {
-        const int64_t e = a.ids[m * a.A + s];
-        const int64_t r0 = e * a.N + c0 + i, r1 = e * a.N + (c0 + 16 < a.N ? c0 + 16 : c0) + i;
-        const uint16_t *xp = a.x + (m * a.A + s) * a.K + g * F::CPL;
-        float4v acc[2] = {float4v{0, 0, 0, 0}, float4v{0, 0, 0, 0}};
-        for (int64_t sp = 0; sp < spans; ++sp) {
-            const uint4 q0 = ld16(a.q + r0 * row_bytes + g * 16 + sp * 64);
-            const uint4 q1 = ld16(a.q + r1 * row_bytes + g * 16 + sp * 64);
-            const int64_t gi = sp * F::SPAN / a.G;
-            const half2v s0 = bf16_splat_h2(a.scale[r0 * groups + gi]), m0 = bf16_splat_h2(a.minv[r0 * groups + gi]);
-            const half2v s1 = bf16_splat_h2(a.scale[r1 * groups + gi]), m1 = bf16_splat_h2(a.minv[r1 * groups + gi]);
-#pragma unroll
-            for (int u = 0; u < F::NT; ++u) {
-                const half8v b = i == 0 ? load_b<XF16>(xp + sp * F::SPAN + 8 * u) : half8v{};
-                acc[0] = mfma16(dq<BITS>(q0, u, s0, m0), b, acc[0]);
-                acc[1] = mfma16(dq<BITS>(q1, u, s1, m1), b, acc[1]);
-            }
-        }
-        const float c = coef[m * a.A + s];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) out[rt][r] = fmaf(c, acc[rt][r], out[rt][r]);
-    }
-    if (i == 0)
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            const int64_t n = c0 + 16 * rt + 4 * g;
-            if (n < a.N) store4(yrow + n, out[rt]);
-        }
 }
 
 // y[m, n] = sum_a coef[m, a] * partial[m * A + a, n] in slot order (fmaf), rounded once; NaN for a token with an
