@@ -230,7 +230,7 @@ def main():
         "metric": METRIC, "value": round(dec_tps, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dec_ms, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
-        "math": "bf16 activations; Q4/Q8 codes dequantized to f16 in registers; f16 MFMA, FP32 accumulation; "
+        "math": "bf16 activations; Q4/Q8 codes as exact bf16 integers; bf16 MFMA, per-group scale/min on the FP32 accumulator; "
                 "router logits FP32",
         "data": "synthetic (seeded on the device; independent weights per layer)",
         "config": {"workload": "cfg2: decode 16 tokens (2 slots x (1 + 7 MTP)), H3072 E512 top-10 + shared Q8 g64, "
