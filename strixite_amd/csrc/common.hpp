@@ -73,9 +73,8 @@ __device__ __forceinline__ float qnan() { return __uint_as_float(0x7fc00000u); }
 // rounded on the weight side; activations stay bf16 (full range).
 //
 // Q4: the bf16 bits 0x4300 | n are exactly 128 + n (n < 16), so a byte shuffle with the constant 0x43 turns a
-// masked dword into bf16 pairs; the offset is folded into the min: m' = m - 128 s. The pairs come out as
-//   [k0, k2, k4, k6, k1, k3, k5, k7]
-// of the dword's 8 codes (even nibbles, then odd), and the activations are shuffled to the same order.
+// masked dword into bf16 pairs; the offset is folded into the min: m' = m - 128 s. Two more shuffles interleave the
+// even (low) and odd (high) nibbles first, so the 8 codes of a dword come out in natural k order.
 // Q8: codes 0..255 are exact in bf16 (8 significant bits): byte -> f32 (v_cvt_f32_ubyte) -> high half; natural order.
 
 typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
@@ -88,15 +87,11 @@ __device__ __forceinline__ bf16x8v as_bf16x8(const Frag &f) { return __builtin_b
 
 __device__ __forceinline__ Frag q4_codes_to_bf16(uint32_t w) {
     const uint32_t t = w & 0x0F0F0F0Fu, u = (w >> 4) & 0x0F0F0F0Fu, c = 0x43434343u;
-    // perm(S0 = c, S1 = t, sel): selector 0..3 picks t's bytes, 4..7 c's
-    return Frag{{__builtin_amdgcn_perm(c, t, 0x04010400u), __builtin_amdgcn_perm(c, t, 0x04030402u),
-                 __builtin_amdgcn_perm(c, u, 0x04010400u), __builtin_amdgcn_perm(c, u, 0x04030402u)}};
-}
-
-// 8 natural-order bf16 activations -> the Q4 slot order [k0, k2, k4, k6, k1, k3, k5, k7]
-__device__ __forceinline__ Frag q4_order(const uint4 &v) {
-    return Frag{{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
-                 __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)}};
+    // perm(S0, S1, sel): selector bytes 0..3 pick S1's bytes, 4..7 S0's. t holds the even k of the 4 bytes, u the odd:
+    // interleave them to k0..k3 and k4..k7, then widen each code byte n to the bf16 0x43nn = 128 + n
+    const uint32_t m0 = __builtin_amdgcn_perm(u, t, 0x05010400u), m1 = __builtin_amdgcn_perm(u, t, 0x07030602u);
+    return Frag{{__builtin_amdgcn_perm(c, m0, 0x04010400u), __builtin_amdgcn_perm(c, m0, 0x04030402u),
+                 __builtin_amdgcn_perm(c, m1, 0x04010400u), __builtin_amdgcn_perm(c, m1, 0x04030402u)}};
 }
 
 __device__ __forceinline__ uint32_t hi16_pair(float a, float b) {

@@ -14,14 +14,18 @@
 // served layout: q4g128, q8g64).
 #include "common.hpp"
 
+#include <algorithm>
 #include <type_traits>
+#include <utility>
 
 namespace strix::kernels {
 
 namespace route {
-// route.hip's workspace layout, as the expert kernels read it (header, offsets, slots, 16-slot tile tables)
-__device__ __forceinline__ int64_t t16_bucket_at(int64_t S, int64_t E) { return 4 + E + 2 + S; }
-__device__ __forceinline__ int64_t t16_start_at(int64_t S, int64_t E) { return t16_bucket_at(S, E) + S / 16 + E + 2; }
+// route.hip's workspace layout as the expert kernels read it: header [4], offsets [E + 2], slots [S], then the
+// 16-slot tile records
+__host__ __device__ __forceinline__ int64_t slots_at(int64_t E) { return 4 + E + 2; }
+__host__ __device__ __forceinline__ int64_t t16_rec_at(int64_t S, int64_t E) { return (4 + E + 2 + S + 3) / 4 * 4; }
+constexpr int kRec16 = 20;  // ints per tile record: {bucket, first index into slots, rows, 0, slot[16], -1 past rows}
 }  // namespace route
 
 namespace {
@@ -45,6 +49,7 @@ struct GemmArgs {
     const uint16_t *scale, *minv;
     int64_t N;          // weight rows per expert
     int64_t K, G, E, A, M;
+    int64_t S;          // GROUPED: slots (M * A)
     const int32_t *ws;  // GROUPED: the grouping workspace
     const int32_t *ids; // PERSLOT: ids [M, A]
     void *y;            // output rows, stride ldy elements
@@ -71,191 +76,447 @@ template <int BITS> __device__ __forceinline__ Frag b_frag(const uint4 &c, int u
     if constexpr (BITS == 4) return q4_codes_to_bf16(u == 0 ? c.x : u == 1 ? c.y : u == 2 ? c.z : c.w);
     else return u == 0 ? q8_codes_to_bf16(c.x, c.y) : q8_codes_to_bf16(c.z, c.w);
 }
-template <int BITS> __device__ __forceinline__ Frag a_frag(const uint4 &v) {
-    if constexpr (BITS == 4) return q4_order(v);
-    else return Frag{{v.x, v.y, v.z, v.w}};
-}
-
-// The token tile of this block and its expert. Token j of the tile (j < 16) is slot(j), -1 past the tile's rows.
-struct Tile {
-    int64_t expert;
-    bool nan;   // invalid ids: outputs are NaN
-    int rows;
-    int64_t st;  // GROUPED: first index into slots[]; DENSE: first token; PERSLOT: the slot
-};
-
-template <int MODE>
-__device__ __forceinline__ bool get_tile(const GemmArgs &a, Tile &t) {
-    if constexpr (MODE == GROUPED) {
-        const int64_t S = a.ws[1], E = a.ws[2];
-        const int64_t tile = blockIdx.y;
-        if (tile >= a.ws[0]) return false;
-        const int32_t bucket = a.ws[route::t16_bucket_at(S, E) + tile], st = a.ws[route::t16_start_at(S, E) + tile];
-        const int32_t end = a.ws[4 + bucket + 1];
-        t.rows = end - st < 16 ? end - st : 16;
-        t.expert = bucket;
-        t.nan = bucket >= a.E;
-        t.st = st;
-    } else if constexpr (MODE == DENSE) {
-        const int64_t m0 = (int64_t)blockIdx.y * 16;
-        t.expert = 0;
-        t.nan = false;
-        t.rows = a.M - m0 < 16 ? (int)(a.M - m0) : 16;
-        t.st = m0;
-    } else {
-        const int64_t slot = blockIdx.y;
-        const int32_t id = a.ids[slot];
-        t.nan = id < 0 || id >= a.E;
-        t.expert = t.nan ? 0 : id;
-        t.rows = 1;
-        t.st = slot;
-        if (t.nan && blockIdx.x == 0 && threadIdx.x == 0 && atomicCAS(&a.err[0], 0u, 1u) == 0u) {
-            a.err[1] = (uint32_t)id;
-            a.err[2] = (uint32_t)slot;
-        }
-    }
-    return true;
-}
-
-template <int MODE> __device__ __forceinline__ int64_t slot_of(const GemmArgs &a, const Tile &t, int j) {
-    if (j >= t.rows) return -1;
-    if constexpr (MODE == GROUPED) return a.ws[4 + a.ws[2] + 2 + t.st + j];
-    else return t.st + j;
-}
+// both code formats decode to natural k order: the activations enter the MFMA as loaded
+template <int BITS> __device__ __forceinline__ Frag a_frag(const uint4 &v) { return Frag{{v.x, v.y, v.z, v.w}}; }
 
 template <typename T> __device__ __forceinline__ void store1(T *p, float v);
 template <> __device__ __forceinline__ void store1<uint16_t>(uint16_t *p, float v) { *p = f32_to_bf16(v); }
 template <> __device__ __forceinline__ void store1<float>(float *p, float v) { *p = v; }
-// h as f16 bits of its bf16 rounding (the reference's h_f16 form)
-__device__ __forceinline__ void store1_hf16(uint16_t *p, float v) {
-    *p = __builtin_bit_cast(uint16_t, (_Float16)bf16_round(v));
-}
 
-// One 16-token x (2 x 16)-row wave tile over all of K: returns acc[rt][r] = token 4g + r, weight column (lane % 16)
-// of tile rt.
-template <int BITS, bool XF16>
-__device__ __forceinline__ void wave_gemm(const GemmArgs &a, const uint16_t *xrow, const int64_t (&tile_row)[2],
-                                          float4v (&acc)[2]) {
+// One 16-token x RT 16-row wave tile over the K steps [s0, s1): acc[rt][r] = token 4g + r, weight column
+// (lane % 16) of tile rt. Loads run two K steps ahead of the math.
+template <int BITS, int RT, bool XF16>
+__device__ __forceinline__ void wave_gemm(const GemmArgs &a, const uint16_t *xrow, const int64_t (&tile_row)[RT],
+                                          int64_t s0, int64_t s1, float4v (&acc)[RT]) {
     using F = QFmt<BITS>;
     const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
     const int64_t row_bytes = a.K * BITS / 8, groups = a.K / a.G;
-    const uint8_t *qp[2];
-    const uint16_t *sp[2], *mp[2];
+    const uint8_t *qp[RT];
+    const uint16_t *sp[RT], *mp[RT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
         const int64_t r = tile_row[rt] + j;
         qp[rt] = a.q + r * row_bytes + g * 16;
         sp[rt] = a.scale + r * groups;
         mp[rt] = a.minv + r * groups;
+        acc[rt] = float4v{0, 0, 0, 0};
     }
     const uint16_t *xp = xrow ? xrow + g * F::CPL : nullptr;
-    acc[0] = float4v{0, 0, 0, 0};
-    acc[1] = float4v{0, 0, 0, 0};
-    const int64_t spans = a.K / F::SPAN;
-    // software pipeline: span s + 1's loads are in flight during span s's math
-    uint4 cq[2], xv[F::NT];
-    uint16_t cs[2], cm[2];
-    auto fetch = [&](int64_t s) {
+    struct Buf {
+        uint4 q[RT], x[F::NT];
+        uint16_t s[RT], m[RT];
+    };
+    auto fetch = [&](int64_t s, Buf &b) {
         const int64_t gi = s * F::SPAN / a.G;
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            cq[rt] = ld16(qp[rt] + s * 64);
-            cs[rt] = sp[rt][gi];
-            cm[rt] = mp[rt][gi];
+        for (int rt = 0; rt < RT; ++rt) {
+            b.q[rt] = ld16(qp[rt] + s * 64);
+            b.s[rt] = sp[rt][gi];
+            b.m[rt] = mp[rt][gi];
         }
 #pragma unroll
-        for (int u = 0; u < F::NT; ++u) xv[u] = xp ? ld16(xp + s * F::SPAN + 8 * u) : make_uint4(0, 0, 0, 0);
+        for (int u = 0; u < F::NT; ++u) b.x[u] = xp ? ld16(xp + s * F::SPAN + 8 * u) : make_uint4(0, 0, 0, 0);
     };
-    fetch(0);
-    for (int64_t s = 0; s < spans; ++s) {
-        const uint4 q0 = cq[0], q1 = cq[1];
-        float sc[2], mn[2];
+    // one K step: consume b, refill it with step s_next (if any) before the MFMAs
+    auto step = [&](Buf &b, int64_t s_next) {
+        uint4 q[RT];
+        float sc[RT], mn[RT];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            sc[rt] = bf16_to_f32(cs[rt]);
-            mn[rt] = BITS == 4 ? bf16_to_f32(cm[rt]) - 128.0f * sc[rt] : bf16_to_f32(cm[rt]);
+        for (int rt = 0; rt < RT; ++rt) {
+            q[rt] = b.q[rt];
+            sc[rt] = bf16_to_f32(b.s[rt]);
+            mn[rt] = BITS == 4 ? bf16_to_f32(b.m[rt]) - 128.0f * sc[rt] : bf16_to_f32(b.m[rt]);
         }
         Frag af[F::NT];
         float xs = 0.f;
 #pragma unroll
         for (int u = 0; u < F::NT; ++u) {
-            const uint4 v = XF16 ? f16x8_to_bf16x8(xv[u]) : xv[u];
+            const uint4 v = XF16 ? f16x8_to_bf16x8(b.x[u]) : b.x[u];
             af[u] = a_frag<BITS>(v);
             xs = frag_sum(v, xs);
         }
-        if (s + 1 < spans) fetch(s + 1);
-        float4v d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
+        if (s_next < s1) fetch(s_next, b);
+        float4v d[RT];
 #pragma unroll
-        for (int u = 0; u < F::NT; ++u) {
-            d0 = mfma_bf16(af[u], b_frag<BITS>(q0, u), d0);
-            d1 = mfma_bf16(af[u], b_frag<BITS>(q1, u), d1);
-        }
-        // the span's activation sum per token: over the 4 lane groups, then to the lanes holding tokens 4g..4g+3
+        for (int rt = 0; rt < RT; ++rt) d[rt] = float4v{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < F::NT; ++u)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) d[rt] = mfma_bf16(af[u], b_frag<BITS>(q[rt], u), d[rt]);
+        // the step's activation sum per token: over the 4 lane groups, then to the lanes holding tokens 4g..4g+3
         xs += __shfl_xor(xs, 16, kWave);
         xs += __shfl_xor(xs, 32, kWave);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const float xr = __shfl(xs, 4 * g + r, kWave);
-            acc[0][r] = fmaf(sc[0], d0[r], fmaf(mn[0], xr, acc[0][r]));
-            acc[1][r] = fmaf(sc[1], d1[r], fmaf(mn[1], xr, acc[1][r]));
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) acc[rt][r] = fmaf(sc[rt], d[rt][r], fmaf(mn[rt], xr, acc[rt][r]));
         }
+    };
+    Buf b0, b1;
+    if (s0 < s1) fetch(s0, b0);
+    if (s0 + 1 < s1) fetch(s0 + 1, b1);
+    for (int64_t s = s0; s < s1; s += 2) {
+        step(b0, s + 2);
+        if (s + 1 < s1) step(b1, s + 3);
     }
 }
 
-// Grid: x over weight-row blocks (kWaves waves x 32 rows, or x 16 SwiGLU columns), y over token tiles.
-template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
-__global__ void __launch_bounds__(kThreads) expert_gemm_kernel(GemmArgs a) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int g = lane / 16, j = lane % 16;
-    Tile t;
-    if (!get_tile<MODE>(a, t)) return;  // uniform per block; no barrier in this kernel
-    const int64_t I = a.N / 2;
-    int64_t tile_row[2];
-    int64_t c0;  // SwiGLU: first h column; else first output row (within the expert)
-    if constexpr (EPI == EPI_SWIGLU) {
-        c0 = ((int64_t)blockIdx.x * kWaves + wave) * 16;
-        if (c0 >= I) return;
-        tile_row[0] = t.expert * a.N + c0;
-        tile_row[1] = t.expert * a.N + I + c0;
+// ---- the persistent streaming kernel ----------------------------------------------------------------------------
+// Work items are (token tile, column block). SwiGLU (gate_up): a whole block takes an item - one 16-column pair, 16
+// gate + 16 up rows - and ks of its 4 waves split K, meeting in LDS at the end of the item. Otherwise each wave takes
+// its own items of 4 row tiles (64 rows) over all of K. Blocks (or waves) loop over items; each wave streams its K
+// steps item after item with the codes and scales two steps ahead across item boundaries, the activations one step
+// ahead, and the next item's tile record a whole item ahead, so the HBM stream does not stop between items.
+//
+// All loads are raw buffer loads: the tensor base is a uniform resource, the lane's row a 32-bit offset fixed per
+// item, and the K step a uniform offset, so the K loop spends no vector instructions on addresses. A lane with no
+// token gets an offset past the activation buffer's end, and the hardware returns zeros.
+// The per-step activation sums (the min term) come from one more MFMA against an all-ones B operand: its D rows are
+// the token sums, already in the lanes that hold those tokens' outputs.
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// The RT weight tiles of an item lie at fixed row distances from the first (SwiGLU: two gate tiles, 16 rows apart,
+// and the matching up tiles N / 2 rows on; otherwise 16 rows apart), so a lane keeps one code and one scale offset per item and the tiles'
+// distances travel in the uniform offset operand. A tile past the expert's last row reads the next expert's rows or,
+// past the buffer's end, zeros; its outputs are not stored.
+template <int RT> struct Item {
+    uint32_t qoff;      // this lane's code row (first tile row + j) byte offset, + its 16-byte lane group
+    // Scales and mins are read as the aligned dword holding the wanted bf16 (a 16-bit load would be widened or
+    // repacked in registers where the prefetch ring wraps, which waits for it). Element (row + tile rows) * groups + gi
+    // of the first tile: tile rows are a multiple of 16, so its parity is (row * groups + gi) & 1 = par ^ (gi & 1).
+    uint32_t soff;      // byte offset of this lane's row, rounded down to a dword: 2 * (row * groups) - 2 par
+    uint32_t par;       // (row * groups) & 1
+    uint32_t xoff;      // this lane's activation row (token j) byte offset + lane group; past the end if none
+    int32_t my;         // output row of token j (lanes j of every lane group hold it); -1 past the tile
+    int32_t c0;         // first output column (SwiGLU: first h column)
+    bool valid, nan;
+};
+
+// What an item needs from memory, loaded a whole item before its offsets are computed: its expert and the lane's
+// token slot (grouped tiles: from the tile record {bucket, first, rows, 0, slot[16]}; per-slot items: the id).
+struct RawItem {
+    int32_t expert, my;
+};
+
+template <int MODE>
+__device__ __forceinline__ RawItem load_raw(const GemmArgs &a, int64_t item, int64_t n_tiles, int64_t col_blocks) {
+    const int j = threadIdx.x % 16;
+    uint32_t tile = (uint32_t)item / (uint32_t)col_blocks;
+    tile = tile < (uint32_t)n_tiles ? tile : (uint32_t)n_tiles - 1;  // past the end: any record, item invalid
+    RawItem r;
+    if constexpr (MODE == GROUPED) {
+        const int32_t *rec = a.ws + route::t16_rec_at(a.S, a.E) + route::kRec16 * (int64_t)tile;
+        r.expert = rec[0];
+        r.my = rec[4 + j];
+    } else if constexpr (MODE == DENSE) {
+        const int32_t st = (int32_t)tile * 16, rows = a.M - st < 16 ? (int32_t)(a.M - st) : 16;
+        r.expert = 0;
+        r.my = j < rows ? st + j : -1;
     } else {
-        c0 = ((int64_t)blockIdx.x * kWaves + wave) * 32;
-        if (c0 >= a.N) return;
-        tile_row[0] = t.expert * a.N + c0;
-        tile_row[1] = t.expert * a.N + (c0 + 16 < a.N ? c0 + 16 : c0);  // a.N % 16 == 0: the tile exists or is skipped
+        r.expert = a.ids[tile];
+        r.my = j == 0 ? (int32_t)tile : -1;
     }
-    // output rows of this lane's tokens 4g + r
-    int64_t orow[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) orow[r] = slot_of<MODE>(a, t, 4 * g + r);
-    float4v acc[2];
-    if (t.nan) {
-        acc[0] = acc[1] = float4v{qnan(), qnan(), qnan(), qnan()};
-    } else {
-        const int64_t my = slot_of<MODE>(a, t, j);  // this lane's A row (token j)
-        const uint16_t *xrow = my < 0 ? nullptr : a.x + (XROW_DIV ? my / a.A : my) * a.K;
-        wave_gemm<BITS, XF16>(a, xrow, tile_row, acc);
-    }
-    if constexpr (EPI == EPI_SWIGLU) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (orow[r] >= 0) {
-                uint16_t *h = static_cast<uint16_t *>(a.y) + orow[r] * a.ldy + c0 + j;
-                const float v = t.nan ? qnan() : silu(acc[0][r]) * acc[1][r];
-                if constexpr (HF16) store1_hf16(h, v);
-                else store1(h, v);
-            }
-    } else {
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            const int64_t n = c0 + 16 * rt + j;
-            if (rt == 1 && c0 + 16 >= a.N) break;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (orow[r] >= 0) {
-                    if constexpr (EPI == EPI_F32) store1(static_cast<float *>(a.y) + orow[r] * a.ldy + n, acc[rt][r]);
-                    else store1(static_cast<uint16_t *>(a.y) + orow[r] * a.ldy + n, acc[rt][r]);
-                }
+    return r;
+}
+
+template <int BITS, int MODE, bool SWI, int RT, bool XROW_DIV>
+__device__ __forceinline__ Item<RT> make_item(const GemmArgs &a, const RawItem &raw, int64_t item, int64_t n_items,
+                                              int64_t col_blocks, bool report, uint32_t x_bytes) {
+    const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
+    Item<RT> it;
+    it.valid = item < n_items;
+    const uint32_t tile = (uint32_t)item / (uint32_t)col_blocks, cb = (uint32_t)item % (uint32_t)col_blocks;
+    const int32_t id = __builtin_amdgcn_readfirstlane(raw.expert);
+    it.nan = MODE != DENSE && (id < 0 || id >= a.E);
+    const uint32_t expert = it.nan ? 0u : (uint32_t)id;
+    if constexpr (MODE == PERSLOT) {
+        if (it.nan && it.valid && report && cb == 0 && lane == 0 && atomicCAS(&a.err[0], 0u, 1u) == 0u) {
+            a.err[1] = (uint32_t)id;
+            a.err[2] = tile;
         }
+    }
+    it.xoff = raw.my >= 0 ? ((XROW_DIV ? (uint32_t)raw.my / (uint32_t)a.A : (uint32_t)raw.my) * (uint32_t)a.K +
+                             g * QFmt<BITS>::CPL) * 2
+                          : x_bytes;
+    it.my = raw.my;
+    it.c0 = (int32_t)(cb * 16 * (SWI ? RT / 2 : RT));
+    const uint32_t row = expert * (uint32_t)a.N + it.c0 + j;
+    it.qoff = row * (uint32_t)(a.K * BITS / 8) + g * 16;
+    const uint32_t e = row * (uint32_t)(a.K / a.G);
+    it.par = e & 1u;
+    it.soff = (e - it.par) * 2;
+    return it;
+}
+
+template <int RT> struct Codes {
+    uint4 q[RT];
+    uint32_t s[RT], m[RT];  // the dwords holding the bf16 scale and min
+};
+
+// Barrier for the LDS reduction only: waits for this wave's LDS traffic, not for its outstanding global prefetches
+// (__syncthreads would also wait for every load in flight and drain the stream).
+// The wave's own LDS writes are complete once lgkmcnt reaches 0; a release fence would also wait for the loads that
+// write the activation ring into LDS (vmcnt), which the reduction does not read.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // no compiler reordering of LDS accesses across the barrier
+    __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0); vmcnt and expcnt left at their maxima
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Prefetch depth of the K-step stream: while step q is consumed, the codes of step q + D (registers, into the slot
+// step q frees) and the activations of step q + D - 1 (LDS, loaded there directly, into the slot step q - 1 freed) are
+// issued, activations first. The compiler waits for loads in issue order; waiting for step q's activations then
+// leaves D - 1 steps of codes in flight. Items run in whole trips of D steps (the ring positions repeat).
+template <bool SWI> constexpr int ring_depth() { return SWI ? 3 : 4; }
+// weight tiles per wave (SwiGLU: 2 gate + 2 up) and the occupancy the kernel is built for (waves per SIMD)
+template <bool SWI> constexpr int wave_tiles() { return SWI ? 4 : 2; }
+template <bool SWI> constexpr int waves_per_simd() { return SWI ? 2 : 3; }
+
+// 16 bytes a lane from a buffer straight into LDS: lane i's bytes land at dst + i (dst is wave-uniform)
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint4 *dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)dst, 16, voff, soff, 0, 0);
+}
+
+// The wave's uniform stream parameters.
+template <int RT> struct Stream {
+    __amdgpu_buffer_rsrc_t rq, rs, rm, rx;
+    uint32_t q_bytes, s_bytes, x_bytes;
+    uint32_t dq[RT], dsm[RT];  // byte distance of tile rt from the first tile: codes, scales
+    int s0, spw, spe, gsh;     // first K step, steps per item, steps per item rounded to whole trips, log2 G
+};
+
+// Step t of cur (t >= spe: step t - spe of nxt; t < 2 spe since spe >= D; past the real steps: no source).
+template <int RT>
+__device__ __forceinline__ int step_source(const Stream<RT> &st, const Item<RT> &nxt, int t, bool &in_cur,
+                                           bool &in_nxt) {
+    in_cur = t < st.spw;
+    in_nxt = !in_cur & (t >= st.spe) & (t - st.spe < st.spw) & nxt.valid;
+    return st.s0 + (in_cur ? t : in_nxt ? t - st.spe : 0);
+}
+
+// Every step issues the same loads - with no source, at offsets past the buffers' ends, which read zeros -, so no
+// branch changes the compiler's wait counts.
+template <int BITS, int RT>
+__device__ __forceinline__ void fetch_x(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt, int t,
+                                        uint4 *xs) {
+    bool in_cur, in_nxt;
+    const int s = step_source(st, nxt, t, in_cur, in_nxt);
+    const uint32_t xo = in_cur ? cur.xoff : in_nxt ? nxt.xoff : st.x_bytes;
+#pragma unroll
+    for (int u = 0; u < QFmt<BITS>::NT; ++u)
+        lds_load16(st.rx, xs + u * kWave, xo, (uint32_t)(s * QFmt<BITS>::SPAN + 8 * u) * 2);
+}
+
+template <int BITS, int RT>
+__device__ __forceinline__ void fetch_codes(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt, int t,
+                                            Codes<RT> &c) {
+    bool in_cur, in_nxt;
+    const int s = step_source(st, nxt, t, in_cur, in_nxt);
+    // group gi = s * SPAN / G: the dword holding element 2k and 2k + 1 lies at 4k, one dword further for an odd
+    // gi when the row's parity is odd
+    const uint32_t gi = (uint32_t)((s * QFmt<BITS>::SPAN) >> st.gsh), g1 = gi & 1u;
+    const uint32_t goff = (gi - g1) * 2;
+    const uint32_t qo = in_cur ? cur.qoff : in_nxt ? nxt.qoff : st.q_bytes;
+    const uint32_t so = in_cur ? cur.soff + 4 * (cur.par & g1) : in_nxt ? nxt.soff + 4 * (nxt.par & g1) : st.s_bytes;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        c.q[rt] = bld16(st.rq, qo, (uint32_t)s * 64 + st.dq[rt]);
+        c.s[rt] = bld4(st.rs, so, goff + st.dsm[rt]);
+        c.m[rt] = bld4(st.rm, so, goff + st.dsm[rt]);
+    }
+}
+
+// One K step of cur from ring position q % D (codes cb, activations xs); the activations of step q + D - 1 go to
+// xfree (the slot of step q - 1), the codes of step q + D to cb once consumed.
+template <int BITS, int RT, bool XF16, int D>
+__device__ __forceinline__ void stream_step(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt,
+                                            Codes<RT> &cb, const uint4 *xs, uint4 *xfree, int q,
+                                            float4v (&acc)[RT], int lane) {
+    constexpr int NT = QFmt<BITS>::NT;
+    const Frag ones{{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}};
+    Frag af[NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        const uint4 v = xs[u * kWave + lane];
+        af[u] = a_frag<BITS>(XF16 ? f16x8_to_bf16x8(v) : v);
+    }
+    fetch_x<BITS, RT>(st, cur, nxt, q + D - 1, xfree);
+    float4v d[RT], dx = {0, 0, 0, 0};
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) d[rt] = float4v{0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) d[rt] = mfma_bf16(af[u], b_frag<BITS>(cb.q[rt], u), d[rt]);
+        dx = mfma_bf16(af[u], ones, dx);
+        __builtin_amdgcn_sched_barrier(0);  // decode each group's codes just before its MFMAs (register pressure)
+    }
+    // the wanted bf16 is the dword's high half when (row * groups + gi) is odd: shuffle it to the high half
+    const uint32_t gi = (uint32_t)(((st.s0 + q) * QFmt<BITS>::SPAN) >> st.gsh);
+    // perm(0, w, sel): selector bytes 0..3 pick w's bytes, 0x0C gives zero
+    const uint32_t sel = (cur.par ^ (gi & 1u)) ? 0x03020C0Cu : 0x01000C0Cu;
+    float sc[RT], mn[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        sc[rt] = __uint_as_float(__builtin_amdgcn_perm(0u, cb.s[rt], sel));
+        const float m = __uint_as_float(__builtin_amdgcn_perm(0u, cb.m[rt], sel));
+        mn[rt] = BITS == 4 ? fmaf(-128.0f, sc[rt], m) : m;
+    }
+    fetch_codes<BITS, RT>(st, cur, nxt, q + D, cb);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt][r] = fmaf(sc[rt], d[rt][r], fmaf(mn[rt], dx[r], acc[rt][r]));
+}
+
+// Ring positions I..D-1 of one trip, expanded at compile time (the slots are fixed registers and LDS arrays).
+template <int BITS, int RT, bool XF16, int D, int I>
+__device__ __forceinline__ void stream_trip(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt,
+                                            Codes<RT> (&c)[D], uint4 *(&xr)[D], int q, float4v (&acc)[RT],
+                                            int lane) {
+    if constexpr (I < D) {
+        stream_step<BITS, RT, XF16, D>(st, cur, nxt, c[I], xr[I], xr[(I + D - 1) % D], q + I, acc, lane);
+        __builtin_amdgcn_sched_barrier(0);  // no interleaving of steps: it only raises register pressure
+        stream_trip<BITS, RT, XF16, D, I + 1>(st, cur, nxt, c, xr, q, acc, lane);
+    }
+}
+
+template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<EPI == EPI_SWIGLU>())))
+    expert_stream_kernel(GemmArgs a, int64_t tiles_bound, int64_t col_blocks, int ks, uint32_t q_bytes,
+                         uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
+    using F = QFmt<BITS>;
+    constexpr bool SWI = EPI == EPI_SWIGLU;
+    constexpr int RT = wave_tiles<SWI>();
+    constexpr int KS = SWI ? kWaves : 1;  // most waves of a block sharing an item (SwiGLU: the block's ks waves)
+    constexpr int D = ring_depth<SWI>();
+    // partial sums of waves 1..ks-1, double-buffered by item parity so one barrier per item suffices
+    __shared__ float4v red[KS > 1 ? 2 * (KS - 1) * RT * kWave : 1];
+    // the activation ring, one array per slot (separate objects let the compiler wait for each slot's loads alone):
+    // [wave][MFMA u][lane] 16 bytes, written by the buffer-to-LDS loads in lane order
+    __shared__ uint4 xr0[kWaves][F::NT][kWave], xr1[kWaves][F::NT][kWave], xr2[kWaves][F::NT][kWave],
+        xr3[D > 3 ? kWaves : 1][F::NT][kWave];
+    static_assert(D == 3 || D == 4, "one activation array per ring slot");
+    // the wave index is uniform across the wave: say so, so the K-step offsets stay scalar
+    const int lane = threadIdx.x % kWave, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int j = lane % 16;
+    int64_t n_tiles = tiles_bound;
+    if constexpr (MODE == GROUPED) n_tiles = a.ws[0] < tiles_bound ? a.ws[0] : tiles_bound;
+    const int64_t n_items = n_tiles * col_blocks;
+    const int64_t first = SWI ? (int64_t)blockIdx.x : (int64_t)blockIdx.x * kWaves + wave;
+    const int64_t stride = SWI ? (int64_t)gridDim.x : (int64_t)gridDim.x * kWaves;
+    if (first >= n_items) return;  // SwiGLU: uniform per block, before any barrier
+    const bool report = wave == 0;
+
+    Stream<RT> st;
+    st.rq = rsrc(a.q, q_bytes), st.rs = rsrc(a.scale, s_bytes), st.rm = rsrc(a.minv, s_bytes);
+    st.rx = rsrc(a.x, x_bytes);
+    st.q_bytes = q_bytes, st.s_bytes = s_bytes, st.x_bytes = x_bytes;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const uint32_t rows = SWI ? 16u * (rt % 2) + (uint32_t)(rt / 2) * (uint32_t)(a.N / 2) : 16u * rt;
+        st.dq[rt] = rows * (uint32_t)(a.K * BITS / 8);
+        st.dsm[rt] = rows * (uint32_t)(a.K / a.G) * 2;
+    }
+    const int spans = (int)(a.K / F::SPAN);
+    // K steps [s0, s0 + spw) of this wave per item (SwiGLU: K split over the block's ks waves, ks <= spans); items
+    // take spe = spw rounded up to whole trips, a step past spw loads zeros and adds nothing
+    st.s0 = KS > 1 ? spans * wave / ks : 0;
+    st.spw = KS > 1 ? spans * (wave + 1) / ks - st.s0 : spans;
+    st.spe = (st.spw + D - 1) / D * D;
+    st.gsh = a.G == 128 ? 7 : 6;
+    const __amdgpu_buffer_rsrc_t ry = rsrc(a.y, y_bytes);
+
+    // three items in flight: cur (streaming), nxt (offsets ready, its first steps prefetched), raw (loads issued)
+    Item<RT> cur = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, load_raw<MODE>(a, first, n_tiles, col_blocks), first,
+                                                            n_items, col_blocks, report, x_bytes);
+    Item<RT> nxt = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, load_raw<MODE>(a, first + stride, n_tiles, col_blocks),
+                                                            first + stride, n_items, col_blocks, report, x_bytes);
+    RawItem raw = load_raw<MODE>(a, first + 2 * stride, n_tiles, col_blocks);
+    float4v acc[RT];
+    Codes<RT> c[D];
+    uint4 *xr[D];
+    xr[0] = &xr0[wave][0][0], xr[1] = &xr1[wave][0][0], xr[2] = &xr2[wave][0][0];
+    if constexpr (D > 3) xr[3] = &xr3[wave][0][0];
+#pragma unroll
+    for (int t = 0; t < D; ++t) {
+        if (t < D - 1) fetch_x<BITS, RT>(st, cur, nxt, t, xr[t]);
+        fetch_codes<BITS, RT>(st, cur, nxt, t, c[t]);
+    }
+    int parity = 0;
+    for (int64_t item = first; item < n_items; item += stride) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt] = float4v{0, 0, 0, 0};
+        int q = 0;
+        do {  // spe >= D: at least one trip (the wait counts after the loop rely on its loads)
+            stream_trip<BITS, RT, XF16, D, 0>(st, cur, nxt, c, xr, q, acc, lane);
+            q += D;
+        } while (q < st.spe);
+        // the item's end: K parts meet (SwiGLU), outputs stored
+        if constexpr (KS > 1) {
+            float4v *rb = red + parity * (KS - 1) * RT * kWave;
+            if (wave > 0)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) rb[((wave - 1) * RT + rt) * kWave + lane] = acc[rt];
+            lds_barrier();
+            if (wave == 0)
+                for (int w = 1; w < ks; ++w)
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) acc[rt] += rb[((w - 1) * RT + rt) * kWave + lane];
+            parity ^= 1;
+        }
+        if (wave == 0 || KS == 1) {
+            // output rows of tokens 4g + r, from the lanes j = 4g + r that hold them
+            const int g = lane / 16;
+            int32_t orow[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) orow[r] = __shfl(cur.my, 4 * g + r, kWave);
+            if constexpr (SWI) {
+#pragma unroll
+                for (int t = 0; t < RT / 2; ++t) {  // h columns c0 + 16 t + j: gate tile t, up tile RT / 2 + t
+                    if (cur.c0 + 16 * t >= a.N / 2) break;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (orow[r] >= 0) {
+                            const float v = cur.nan ? qnan() : silu(acc[t][r]) * acc[RT / 2 + t][r];
+                            // HF16: h as f16 bits of its bf16 rounding (the reference's h_f16 form)
+                            const uint16_t bits =
+                                HF16 ? __builtin_bit_cast(uint16_t, (_Float16)bf16_round(v)) : f32_to_bf16(v);
+                            __builtin_amdgcn_raw_buffer_store_b16(
+                                bits, ry, ((uint32_t)orow[r] * (uint32_t)a.ldy + cur.c0 + 16 * t + j) * 2, 0, 0);
+                        }
+                }
+            } else {
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    if (cur.c0 + 16 * rt >= a.N) break;
+                    const uint32_t n = cur.c0 + 16 * rt + j;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (orow[r] >= 0) {
+                            const float v = cur.nan ? qnan() : acc[rt][r];
+                            const uint32_t e = (uint32_t)orow[r] * (uint32_t)a.ldy + n;
+                            if constexpr (EPI == EPI_F32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, e * 4, 0, 0);
+                            else __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), ry, e * 2, 0, 0);
+                        }
+                }
+            }
+        }
+        cur = nxt;
+        nxt = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, raw, item + 2 * stride, n_items, col_blocks, report, x_bytes);
+        raw = load_raw<MODE>(a, item + 3 * stride, n_tiles, col_blocks);
     }
 }
 
@@ -287,7 +548,8 @@ __global__ void __launch_bounds__(kThreads) perslot_combine_kernel(GemmArgs a, c
             const int64_t e = a.ids[m * a.A + s];
             const int64_t tile_row[2] = {e * a.N + c0, e * a.N + (c0 + 16 < a.N ? c0 + 16 : c0)};
             float4v acc[2];
-            wave_gemm<BITS, XF16>(a, j == 0 ? a.x + (m * a.A + s) * a.K : nullptr, tile_row, acc);
+            wave_gemm<BITS, 2, XF16>(a, j == 0 ? a.x + (m * a.A + s) * a.K : nullptr, tile_row, 0,
+                                     a.K / QFmt<BITS>::SPAN, acc);
             const float c = coef[m * a.A + s];
             out[0] = fmaf(c, acc[0][0], out[0]);
             out[1] = fmaf(c, acc[1][0], out[1]);
@@ -409,12 +671,56 @@ void check_view(const char *fn, const QV &w, int64_t E) {
     STRIX_CHECK(reinterpret_cast<uintptr_t>(w.q) % 16 == 0, fn, ": code array must be 16-byte aligned");
 }
 
+int device_cus() {
+    static int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 256;
+        return n > 0 ? n : 256;
+    }();
+    return cus;
+}
+
+// Persistent grid: as many blocks as fit on the device at once (capped by the items), each looping over items.
 template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
-void launch_gemm(const GemmArgs &a, int64_t tiles, hipStream_t stream) {
-    const int64_t cols = EPI == EPI_SWIGLU ? a.N / 2 : a.N, per_block = EPI == EPI_SWIGLU ? 16 * kWaves : 32 * kWaves;
-    STRIX_CHECK(tiles <= 65535 * 64, "expert kernels: ", tiles, " token tiles exceed the grid");
-    dim3 grid((unsigned)((cols + per_block - 1) / per_block), (unsigned)tiles), block(kThreads);
-    expert_gemm_kernel<BITS, MODE, EPI, XF16, XROW_DIV, HF16><<<grid, block, 0, stream>>>(a);
+void launch_gemm(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
+    constexpr bool SWI = EPI == EPI_SWIGLU;
+    constexpr int RT = wave_tiles<SWI>();
+    const int64_t spans = a.K / QFmt<BITS>::SPAN;
+    // SwiGLU: K split over ks = 1..4 waves (the block), preferring an even split into whole ring trips and then
+    // the most waves; otherwise one wave per item over all of K
+    int ks = 1;
+    if constexpr (SWI) {
+        int64_t best = -1;
+        for (int k = 1; k <= kWaves && k <= spans; ++k) {
+            const bool whole = spans % k == 0 && (spans / k) % ring_depth<SWI>() == 0;
+            const int64_t score = (whole ? 16 : 0) + k;
+            if (score > best) best = score, ks = k;
+        }
+    }
+    const int threads = SWI ? ks * kWave : kThreads;
+    const int64_t col_blocks = SWI ? (a.N / 2 + 16 * RT / 2 - 1) / (16 * RT / 2) : (a.N + 16 * RT - 1) / (16 * RT);
+    const int64_t items = tiles_bound * col_blocks, per_block = SWI ? 1 : kWaves;
+    auto kernel = expert_stream_kernel<BITS, MODE, EPI, XF16, XROW_DIV, HF16>;
+    static int occ[kWaves + 1] = {};
+    if (occ[threads / kWave] == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1) n = 1;
+        occ[threads / kWave] = n;
+    }
+    const int64_t want = (items + per_block - 1) / per_block, cap = (int64_t)device_cus() * occ[threads / kWave];
+    const int64_t blocks = std::max<int64_t>(1, std::min(want, cap));
+    // 32-bit buffer offsets: the weight view and the activations must each stay below 2 GiB
+    const int64_t q_bytes = a.N * a.E * a.K * BITS / 8, s_bytes = a.N * a.E * (a.K / a.G) * 2;
+    const int64_t x_rows = MODE == GROUPED ? (XROW_DIV ? a.S / a.A : a.S) : MODE == DENSE ? a.M : (XROW_DIV ? a.M : a.M * a.A);
+    const int64_t x_bytes = x_rows * a.K * 2;
+    const int64_t y_rows = MODE == GROUPED ? a.S : MODE == DENSE ? a.M : a.M * a.A;
+    const int64_t y_bytes = y_rows * a.ldy * (EPI == EPI_F32 ? 4 : 2);
+    STRIX_CHECK(q_bytes < (1ll << 31) && s_bytes < (1ll << 31) && x_bytes < (1ll << 31) && y_bytes < (1ll << 31),
+                "expert kernels: weight (", q_bytes, " B), activation (", x_bytes, " B) or output (", y_bytes,
+                " B) tensor at or above 2 GiB (32-bit buffer offsets)");
+    kernel<<<(unsigned)blocks, threads, 0, stream>>>(a, tiles_bound, col_blocks, ks, (uint32_t)q_bytes,
+                                                      (uint32_t)s_bytes, (uint32_t)x_bytes, (uint32_t)y_bytes);
 }
 
 template <int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
@@ -440,13 +746,15 @@ void check_grouped(const char *fn, const void *x, const QV &w, int64_t E, const 
     STRIX_CHECK(E <= kMoeMaxExperts, fn, ": E = ", E, " > ", kMoeMaxExperts);
     STRIX_CHECK(M >= 1 && A >= 1 && A <= 64 && A <= E && M * A <= kMoeMaxSlots, fn, ": M = ", M, " tokens x A = ", A,
                 " slots (A 1..min(64, E = ", E, "), M*A <= ", kMoeMaxSlots, ")");
+    STRIX_CHECK(reinterpret_cast<uintptr_t>(ws) % 16 == 0, fn, ": workspace must be 16-byte aligned");
     STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, A, E), fn, ": workspace of ", ws_bytes, " bytes, needs ",
                 moe_route_workspace_bytes(M, A, E), " for M = ", M, ", A = ", A, ", E = ", E);
     STRIX_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0, fn, ": input must be 16-byte aligned");
     STRIX_CHECK(disjoint(y, y_bytes, x, x_rows * w.K * 2), fn, ": output overlaps the input");
 }
 
-int64_t grouped_tiles(int64_t M, int64_t A, int64_t E) { return M * A / 16 + E + 2; }
+// every tile holds at least one slot, and the tables hold at most S / 16 + E + 2 of them
+int64_t grouped_tiles(int64_t M, int64_t A, int64_t E) { return std::min(M * A, M * A / 16 + E + 2); }
 
 template <typename V>
 void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E, const void *ws, size_t ws_bytes,
@@ -457,7 +765,7 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
     STRIX_CHECK(I % 16 == 0, fn, ": gate_up has ", N, " rows an expert; I = N / 2 must be a multiple of 16");
     STRIX_CHECK(reinterpret_cast<uintptr_t>(h) % 8 == 0, fn, ": h must be 8-byte aligned");
     GemmArgs a = make_args(w, E, x, h, I);
-    a.A = A, a.ws = static_cast<const int32_t *>(ws);
+    a.A = A, a.ws = static_cast<const int32_t *>(ws), a.S = M * A;
     const int64_t tiles = grouped_tiles(M, A, E);
     if (h_f16) launch_bits<GROUPED, EPI_SWIGLU, false, true, true>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_SWIGLU, false, true, false>(w.bits, a, tiles, stream);
@@ -504,7 +812,7 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
         STRIX_CHECK(disjoint(y, M * N * 2, shared->s, M * N * 2), fn, ": shared s overlaps y");
     }
     GemmArgs a = make_args(w, E, h, partial, N);
-    a.A = A, a.ws = static_cast<const int32_t *>(ws);
+    a.A = A, a.ws = static_cast<const int32_t *>(ws), a.S = M * A;
     const int64_t tiles = grouped_tiles(M, A, E);
     if (h_f16) launch_bits<GROUPED, EPI_F32, true, false, false>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_F32, false, false, false>(w.bits, a, tiles, stream);
@@ -533,7 +841,7 @@ void linear_q4_experts_gather_grouped(const void *x, const Q4DeviceView &w, int6
     check_grouped(fn, x, v, E, ws, ws_bytes, M, A, y, act, M * A * N * 2, M);
     STRIX_CHECK(reinterpret_cast<uintptr_t>(y) % 8 == 0, fn, ": y must be 8-byte aligned");
     GemmArgs a = make_args(v, E, x, y, N);
-    a.A = A, a.ws = static_cast<const int32_t *>(ws);
+    a.A = A, a.ws = static_cast<const int32_t *>(ws), a.S = M * A;
     launch_gemm<4, GROUPED, EPI_BF16, false, true, false>(a, grouped_tiles(M, A, E), stream);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E);
 }
@@ -764,7 +1072,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         const QV dv = q8 ? qv(dn8) : qv(w.down);
         check_view(fn, dv, E);
         GemmArgs a = make_args(dv, E, h, partial, H);
-        a.A = k, a.ws = static_cast<const int32_t *>(route);
+        a.A = k, a.ws = static_cast<const int32_t *>(route), a.S = M * k;
         if (q8) launch_gemm<8, GROUPED, EPI_F32, true, false, false>(a, grouped_tiles(M, k, E), stream);
         else launch_gemm<4, GROUPED, EPI_F32, true, false, false>(a, grouped_tiles(M, k, E), stream);
     }

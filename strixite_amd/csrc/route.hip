@@ -9,6 +9,7 @@
 // as three launches (chunk histograms, scan, placement) through the workspace.
 #include "common.hpp"
 
+#include <algorithm>
 #include <climits>
 
 namespace strix::kernels {
@@ -20,24 +21,26 @@ constexpr int kChunk = 256;          // slots per wave chunk
 constexpr int kSmallWaves = 16;      // the one-block path: 1024 threads
 constexpr int kTileRows = 16;        // slots per tile of the grouped expert kernels
 constexpr int kWideRows = 64;        // slots per wide tile (kept for the large-M kernels)
+constexpr int kRec16 = 4 + kTileRows; // ints per 16-slot tile record
 
 struct Layout {
     int64_t S, E, T16, T64, nch;
     __host__ __device__ int64_t offsets() const { return 4; }
     __host__ __device__ int64_t slots() const { return offsets() + E + 2; }
-    __host__ __device__ int64_t t16_bucket() const { return slots() + S; }
-    __host__ __device__ int64_t t16_start() const { return t16_bucket() + T16; }
-    __host__ __device__ int64_t t64_bucket() const { return t16_start() + T16; }
-    __host__ __device__ int64_t t64_start() const { return t64_bucket() + T64; }
-    __host__ __device__ int64_t hist() const { return t64_start() + T64; }        // [nch][E + 1]
+    // 16-slot tile records {bucket, first index into slots, rows, 0, slot[16] (-1 past rows)}: everything an
+    // expert kernel needs about a tile in independent loads; 64-slot tiles {bucket, first index, rows, 0}
+    __host__ __device__ int64_t t16_rec() const { return (slots() + S + 3) / 4 * 4; }
+    __host__ __device__ int64_t t64_rec() const { return t16_rec() + kRec16 * T16; }
+    __host__ __device__ int64_t hist() const { return t64_rec() + 4 * T64; }       // [nch][E + 1]
     __host__ __device__ int64_t bad() const { return hist() + nch * (E + 1); }    // [nch]
     __host__ __device__ int64_t ints() const { return bad() + nch; }
 };
 
 inline Layout layout(int64_t M, int64_t A, int64_t E) {
     const int64_t S = M * A;
-    // sum over buckets of ceil(count / R) <= S / R + (E + 1)
-    return {S, E, S / kTileRows + E + 2, S / kWideRows + E + 2, (S + kChunk - 1) / kChunk};
+    // sum over buckets of ceil(count / R) <= min(S, S / R + (E + 1)): a tile holds at least one slot
+    const int64_t t16 = std::min(S, S / kTileRows + E + 2), t64 = std::min(S, S / kWideRows + E + 2);
+    return {S, E, t16, t64, (S + kChunk - 1) / kChunk};
 }
 
 }  // namespace route
@@ -132,8 +135,22 @@ __device__ void write_bucket(int t, int cnt, const int (&pre)[3], int32_t *ws, c
     int32_t *offsets = ws + L.offsets();
     offsets[t] = pre[0];
     const int n16 = (cnt + kTileRows - 1) / kTileRows, n64 = (cnt + kWideRows - 1) / kWideRows;
-    for (int i = 0; i < n16; ++i) ws[L.t16_bucket() + pre[1] + i] = t, ws[L.t16_start() + pre[1] + i] = pre[0] + i * kTileRows;
-    for (int i = 0; i < n64; ++i) ws[L.t64_bucket() + pre[2] + i] = t, ws[L.t64_start() + pre[2] + i] = pre[0] + i * kWideRows;
+    for (int i = 0; i < n16; ++i)
+        *reinterpret_cast<int4 *>(ws + L.t16_rec() + kRec16 * (pre[1] + i)) =
+            make_int4(t, pre[0] + i * kTileRows, min(kTileRows, cnt - i * kTileRows), 0);
+    for (int i = 0; i < n64; ++i)
+        *reinterpret_cast<int4 *>(ws + L.t64_rec() + 4 * (pre[2] + i)) =
+            make_int4(t, pre[0] + i * kWideRows, min(kWideRows, cnt - i * kWideRows), 0);
+}
+
+// After placement: each 16-slot tile record gets its slots (-1 past its rows). Threads t, t + nthreads, ... of the
+// caller copy entries [t, n_tiles * 16).
+__device__ void fill_tile_slots(int32_t *ws, const Layout &L, int64_t n_tiles, int64_t t, int64_t nthreads) {
+    for (int64_t i = t; i < n_tiles * kTileRows; i += nthreads) {
+        int32_t *rec = ws + L.t16_rec() + kRec16 * (i / kTileRows);
+        const int jj = (int)(i % kTileRows);
+        rec[4 + jj] = jj < rec[2] ? ws[L.slots() + rec[1] + jj] : -1;
+    }
 }
 
 __device__ void write_header(int32_t *ws, const Layout &L, const int (&tot)[3]) {
@@ -189,6 +206,8 @@ __global__ void __launch_bounds__(1024) route_small_kernel(const int32_t *ids, L
     }
     __syncthreads();
     if (s0 < L.S) chunk_place(ids, s0, s1, E, nbits, h, ws + L.slots());
+    __syncthreads();
+    fill_tile_slots(ws, L, tot[1], threadIdx.x, blockDim.x);
 }
 
 // ---- larger S: chunk histograms, one scan block, placement ----------------------------------------------------------
@@ -252,6 +271,10 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave) route_place_kernel(con
     chunk_place(ids, s0, s1, E, nbits, c, ws + L.slots());
 }
 
+__global__ void __launch_bounds__(256) route_tiles_kernel(Layout L, int32_t *ws) {
+    fill_tile_slots(ws, L, ws[0], (int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x);
+}
+
 }  // namespace
 
 size_t moe_route_workspace_bytes(int64_t M, int64_t A, int64_t E) {
@@ -271,6 +294,7 @@ void moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void 
     STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, A, E), fn, ": workspace of ", ws_bytes, " bytes, needs ",
                 moe_route_workspace_bytes(M, A, E));
     STRIX_CHECK(disjoint(ids, M * A * 4, ws, (int64_t)ws_bytes), fn, ": ids overlaps the workspace");
+    STRIX_CHECK(reinterpret_cast<uintptr_t>(ws) % 16 == 0, fn, ": workspace must be 16-byte aligned");
     const Layout L = route::layout(M, A, E);
     int nbits = 0;
     while ((1ll << nbits) <= E) ++nbits;  // buckets 0..E
@@ -284,6 +308,8 @@ void moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void 
         route_hist_kernel<<<blocks, kWavesPerBlock * kWave, lds, stream>>>(ids, L, nbits, w);
         route_scan_kernel<<<1, 1024, 0, stream>>>(ids, L, w, err);
         route_place_kernel<<<blocks, kWavesPerBlock * kWave, lds, stream>>>(ids, L, nbits, w);
+        const int64_t tb = (L.T16 * kTileRows + 255) / 256;
+        route_tiles_kernel<<<(unsigned)(tb < 4096 ? tb : 4096), 256, 0, stream>>>(L, w);
     }
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E);
 }

@@ -18,50 +18,73 @@ constexpr int kWave = 64;
 constexpr int kThreads = 256;
 
 // ---- router projection ----------------------------------------------------------------------------------------
-// One wave per output row n, MR token rows a block. Lane l owns the 8-element chunks c = l, l + 64, ...: its
-// partial is an fmaf chain over them (chunk order, then element order), then a butterfly over the 64 lanes. The
-// order depends on nothing but K, so every M, grid and launch gives the same bits (oracle: orc_router_logits).
-// VEC: K % 8 == 0 and 16-byte aligned x / w rows - 16-byte loads; else element loads, the same arithmetic.
+// One wave per (output row n, group of MR token rows); a block is RB rows x TG token groups (RB * TG = 4 waves), so
+// the waves sharing a weight row share it through L1. Lane l owns the 8-element chunks c = l, l + 64, ...: its
+// partial is an fmaf chain over them (chunk order, then element order), then a butterfly over the 64 lanes. The order
+// depends on nothing but K, so every M, grid and launch gives the same bits (oracle: orc_router_logits).
+// A lane's weight chunks are loaded in batches of NB before the token loop. VEC: K % 8 == 0 and 16-byte aligned x / w
+// rows - 16-byte loads; else element loads, the same arithmetic.
 template <typename TY, int MR, bool VEC>
 __global__ void __launch_bounds__(kThreads)
-    router_rows_kernel(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K) {
+    router_rows_kernel(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K, int TG) {
+    constexpr int NB = 8;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int64_t n = (int64_t)blockIdx.x * (kThreads / kWave) + wave;
-    const int64_t m0 = (int64_t)blockIdx.y * MR;
-    if (n >= N) return;  // no barrier in this kernel
+    const int RB = (kThreads / kWave) / TG;
+    const int64_t n = (int64_t)blockIdx.x * RB + wave / TG;
+    const int64_t m0 = ((int64_t)blockIdx.y * TG + wave % TG) * MR;
+    if (n >= N || m0 >= M) return;  // no barrier in this kernel
     const int rows = (int)(M - m0 < MR ? M - m0 : MR);
     float acc[MR];
 #pragma unroll
     for (int r = 0; r < MR; ++r) acc[r] = 0.f;
     const int64_t chunks = (K + 7) / 8;
     const uint16_t *wr = w + n * K;
-    for (int64_t c = lane; c < chunks; c += kWave) {
-        float wv[8];
-        if constexpr (VEC) {
-            const uint4 u = *reinterpret_cast<const uint4 *>(wr + c * 8);
-            const uint32_t d[4] = {u.x, u.y, u.z, u.w};
+    for (int64_t cb = lane; cb < chunks; cb += (int64_t)NB * kWave) {
+        uint4 wu[NB];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) wv[2 * i] = __uint_as_float(d[i] << 16), wv[2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
-        } else {
+        for (int b = 0; b < NB; ++b) {
+            const int64_t c = cb + (int64_t)b * kWave;
+            if constexpr (VEC) {
+                wu[b] = c < chunks ? *reinterpret_cast<const uint4 *>(wr + c * 8) : make_uint4(0, 0, 0, 0);
+            } else {
+                uint16_t e[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) wv[i] = c * 8 + i < K ? bf16_to_f32(wr[c * 8 + i]) : 0.f;
+                for (int i = 0; i < 8; ++i) e[i] = c * 8 + i < K ? wr[c * 8 + i] : 0;
+                wu[b] = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16, e[4] | (uint32_t)e[5] << 16,
+                                   e[6] | (uint32_t)e[7] << 16);
+            }
         }
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
             if (r < rows) {
                 const uint16_t *xr = x + (m0 + r) * K;
-                float xv[8];
-                if constexpr (VEC) {
-                    const uint4 u = *reinterpret_cast<const uint4 *>(xr + c * 8);
-                    const uint32_t d[4] = {u.x, u.y, u.z, u.w};
+                uint4 xu[NB];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) xv[2 * i] = __uint_as_float(d[i] << 16), xv[2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+                for (int b = 0; b < NB; ++b) {
+                    const int64_t c = cb + (int64_t)b * kWave;
+                    if constexpr (VEC) {
+                        xu[b] = c < chunks ? *reinterpret_cast<const uint4 *>(xr + c * 8) : make_uint4(0, 0, 0, 0);
+                    } else {
+                        uint16_t e[8];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) acc[r] = fmaf(xv[i], wv[i], acc[r]);
-                } else {
+                        for (int i = 0; i < 8; ++i) e[i] = c * 8 + i < K ? xr[c * 8 + i] : 0;
+                        xu[b] = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                                           e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+                    }
+                }
 #pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        if (c * 8 + i < K) acc[r] = fmaf(bf16_to_f32(xr[c * 8 + i]), wv[i], acc[r]);
+                for (int b = 0; b < NB; ++b) {
+                    const int64_t c = cb + (int64_t)b * kWave;
+                    if (c >= chunks) break;
+                    const uint32_t wd[4] = {wu[b].x, wu[b].y, wu[b].z, wu[b].w};
+                    const uint32_t xd[4] = {xu[b].x, xu[b].y, xu[b].z, xu[b].w};
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        if (!VEC && c * 8 + i >= K) break;
+                        const float xv = __uint_as_float(i % 2 ? xd[i / 2] & 0xffff0000u : xd[i / 2] << 16);
+                        const float wv = __uint_as_float(i % 2 ? wd[i / 2] & 0xffff0000u : wd[i / 2] << 16);
+                        acc[r] = fmaf(xv, wv, acc[r]);
+                    }
                 }
             }
         }
@@ -83,17 +106,18 @@ template <typename TY>
 void launch_router_rows(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K,
                         hipStream_t stream) {
     const bool vec = K % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
-    const unsigned bx = (unsigned)((N + kThreads / kWave - 1) / (kThreads / kWave));
     auto go = [&](auto mr) {
         constexpr int MR = decltype(mr)::value;
-        const int64_t by = (M + MR - 1) / MR;
+        const int64_t groups = (M + MR - 1) / MR;
+        const int TG = groups >= 4 ? 4 : groups >= 2 ? 2 : 1, RB = 4 / TG;
+        const int64_t by = (groups + TG - 1) / TG;
         STRIX_CHECK(by <= 65535, "linear_bf16w: M = ", M, " needs ", by, " row blocks, grid.y holds 65535");
-        dim3 grid(bx, (unsigned)by), block(kThreads);
-        if (vec) router_rows_kernel<TY, MR, true><<<grid, block, 0, stream>>>(x, w, y, M, N, K);
-        else router_rows_kernel<TY, MR, false><<<grid, block, 0, stream>>>(x, w, y, M, N, K);
+        dim3 grid((unsigned)((N + RB - 1) / RB), (unsigned)by), block(kThreads);
+        if (vec) router_rows_kernel<TY, MR, true><<<grid, block, 0, stream>>>(x, w, y, M, N, K, TG);
+        else router_rows_kernel<TY, MR, false><<<grid, block, 0, stream>>>(x, w, y, M, N, K, TG);
     };
     if (M == 1) go(std::integral_constant<int, 1>{});
-    else if (M <= 4) go(std::integral_constant<int, 4>{});
+    else if (M <= 64) go(std::integral_constant<int, 4>{});
     else go(std::integral_constant<int, 16>{});
 }
 
