@@ -200,6 +200,7 @@ template <int RT> struct Item {
     uint32_t xoff;      // this lane's activation row (token j) byte offset + lane group; past the end if none
     int32_t my;         // output row of token j (lanes j of every lane group hold it); -1 past the tile
     int32_t c0;         // first output column (SwiGLU: first h column)
+    uint32_t expert;    // the expert whose rows the item reads (0 for an invalid id)
     bool valid, nan;
 };
 
@@ -240,6 +241,7 @@ __device__ __forceinline__ Item<RT> make_item(const GemmArgs &a, const RawItem &
     const int32_t id = __builtin_amdgcn_readfirstlane(raw.expert);
     it.nan = MODE != DENSE && (id < 0 || id >= a.E);
     const uint32_t expert = it.nan ? 0u : (uint32_t)id;
+    it.expert = expert;
     if constexpr (MODE == PERSLOT) {
         if (it.nan && it.valid && report && cb == 0 && lane == 0 && atomicCAS(&a.err[0], 0u, 1u) == 0u) {
             a.err[1] = (uint32_t)id;
@@ -259,9 +261,9 @@ __device__ __forceinline__ Item<RT> make_item(const GemmArgs &a, const RawItem &
     return it;
 }
 
-template <int RT> struct Codes {
+template <int RT, bool SST> struct Codes {
     uint4 q[RT];
-    uint32_t s[RT], m[RT];  // the dwords holding the bf16 scale and min
+    uint32_t s[SST ? 1 : RT], m[SST ? 1 : RT];  // the dwords holding the bf16 scale and min (unless staged in LDS)
 };
 
 // Barrier for the LDS reduction only: waits for this wave's LDS traffic, not for its outstanding global prefetches
@@ -295,6 +297,7 @@ template <int RT> struct Stream {
     uint32_t q_bytes, s_bytes, x_bytes;
     uint32_t dq[RT], dsm[RT];  // byte distance of tile rt from the first tile: codes, scales
     int s0, spw, spe, gsh;     // first K step, steps per item, steps per item rounded to whole trips, log2 G
+    uint32_t groups;           // quantization groups a row
 };
 
 // Step t of cur (t >= spe: step t - spe of nxt; t < 2 spe since spe >= D; past the real steps: no source).
@@ -319,9 +322,9 @@ __device__ __forceinline__ void fetch_x(const Stream<RT> &st, const Item<RT> &cu
         lds_load16(st.rx, xs + u * kWave, xo, (uint32_t)(s * QFmt<BITS>::SPAN + 8 * u) * 2);
 }
 
-template <int BITS, int RT>
+template <int BITS, int RT, bool SST>
 __device__ __forceinline__ void fetch_codes(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt, int t,
-                                            Codes<RT> &c) {
+                                            Codes<RT, SST> &c) {
     bool in_cur, in_nxt;
     const int s = step_source(st, nxt, t, in_cur, in_nxt);
     // group gi = s * SPAN / G: the dword holding element 2k and 2k + 1 lies at 4k, one dword further for an odd
@@ -333,17 +336,19 @@ __device__ __forceinline__ void fetch_codes(const Stream<RT> &st, const Item<RT>
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         c.q[rt] = bld16(st.rq, qo, (uint32_t)s * 64 + st.dq[rt]);
-        c.s[rt] = bld4(st.rs, so, goff + st.dsm[rt]);
-        c.m[rt] = bld4(st.rm, so, goff + st.dsm[rt]);
+        if constexpr (!SST) {
+            c.s[rt] = bld4(st.rs, so, goff + st.dsm[rt]);
+            c.m[rt] = bld4(st.rm, so, goff + st.dsm[rt]);
+        }
     }
 }
 
 // One K step of cur from ring position q % D (codes cb, activations xs); the activations of step q + D - 1 go to
 // xfree (the slot of step q - 1), the codes of step q + D to cb once consumed.
-template <int BITS, int RT, bool XF16, int D>
+template <int BITS, int RT, bool XF16, int D, bool SST>
 __device__ __forceinline__ void stream_step(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt,
-                                            Codes<RT> &cb, const uint4 *xs, uint4 *xfree, int q,
-                                            float4v (&acc)[RT], int lane) {
+                                            Codes<RT, SST> &cb, const uint4 *xs, uint4 *xfree, int q,
+                                            float4v (&acc)[RT], int lane, const uint16_t *sl) {
     constexpr int NT = QFmt<BITS>::NT;
     const Frag ones{{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}};
     Frag af[NT];
@@ -363,18 +368,31 @@ __device__ __forceinline__ void stream_step(const Stream<RT> &st, const Item<RT>
         dx = mfma_bf16(af[u], ones, dx);
         __builtin_amdgcn_sched_barrier(0);  // decode each group's codes just before its MFMAs (register pressure)
     }
-    // the wanted bf16 is the dword's high half when (row * groups + gi) is odd: shuffle it to the high half
     const uint32_t gi = (uint32_t)(((st.s0 + q) * QFmt<BITS>::SPAN) >> st.gsh);
-    // perm(0, w, sel): selector bytes 0..3 pick w's bytes, 0x0C gives zero
-    const uint32_t sel = (cur.par ^ (gi & 1u)) ? 0x03020C0Cu : 0x01000C0Cu;
     float sc[RT], mn[RT];
+    if constexpr (SST) {
+        // staged in LDS as [group][scale, min][tile][row]: sl points at this lane's row of group 0. A padding step
+        // (q >= spw) has zero codes and activations but must still read finite values: its group is clamped.
+        const uint32_t gl = gi < st.groups ? gi : st.groups - 1;
+        const uint16_t *g = sl + gl * (2 * RT * 16);
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        sc[rt] = __uint_as_float(__builtin_amdgcn_perm(0u, cb.s[rt], sel));
-        const float m = __uint_as_float(__builtin_amdgcn_perm(0u, cb.m[rt], sel));
-        mn[rt] = BITS == 4 ? fmaf(-128.0f, sc[rt], m) : m;
+        for (int rt = 0; rt < RT; ++rt) {
+            sc[rt] = __uint_as_float((uint32_t)g[rt * 16] << 16);
+            const float m = __uint_as_float((uint32_t)g[(RT + rt) * 16] << 16);
+            mn[rt] = BITS == 4 ? fmaf(-128.0f, sc[rt], m) : m;
+        }
+    } else {
+        // the wanted bf16 is the dword's high half when (row * groups + gi) is odd: shuffle it to the high half
+        // (perm(0, w, sel): selector bytes 0..3 pick w's bytes, 0x0C gives zero)
+        const uint32_t sel = (cur.par ^ (gi & 1u)) ? 0x03020C0Cu : 0x01000C0Cu;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            sc[rt] = __uint_as_float(__builtin_amdgcn_perm(0u, cb.s[rt], sel));
+            const float m = __uint_as_float(__builtin_amdgcn_perm(0u, cb.m[rt], sel));
+            mn[rt] = BITS == 4 ? fmaf(-128.0f, sc[rt], m) : m;
+        }
     }
-    fetch_codes<BITS, RT>(st, cur, nxt, q + D, cb);
+    fetch_codes<BITS, RT, SST>(st, cur, nxt, q + D, cb);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -382,18 +400,58 @@ __device__ __forceinline__ void stream_step(const Stream<RT> &st, const Item<RT>
 }
 
 // Ring positions I..D-1 of one trip, expanded at compile time (the slots are fixed registers and LDS arrays).
-template <int BITS, int RT, bool XF16, int D, int I>
+template <int BITS, int RT, bool XF16, int D, bool SST, int I>
 __device__ __forceinline__ void stream_trip(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt,
-                                            Codes<RT> (&c)[D], uint4 *(&xr)[D], int q, float4v (&acc)[RT],
-                                            int lane) {
+                                            Codes<RT, SST> (&c)[D], uint4 *(&xr)[D], int q, float4v (&acc)[RT],
+                                            int lane, const uint16_t *sl) {
     if constexpr (I < D) {
-        stream_step<BITS, RT, XF16, D>(st, cur, nxt, c[I], xr[I], xr[(I + D - 1) % D], q + I, acc, lane);
+        stream_step<BITS, RT, XF16, D, SST>(st, cur, nxt, c[I], xr[I], xr[(I + D - 1) % D], q + I, acc, lane, sl);
         __builtin_amdgcn_sched_barrier(0);  // no interleaving of steps: it only raises register pressure
-        stream_trip<BITS, RT, XF16, D, I + 1>(st, cur, nxt, c, xr, q, acc, lane);
+        stream_trip<BITS, RT, XF16, D, SST, I + 1>(st, cur, nxt, c, xr, q, acc, lane, sl);
     }
 }
 
-template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
+// Scale staging (SwiGLU, SST): an item's scales and mins - for each tile rt its 16 rows x groups bf16, contiguous in
+// memory - are read by the block's ks waves as dwords one item ahead, held in registers, and written to LDS at the
+// previous item's end transposed to [group][scale, min][tile][row], so a K step reads its 2 RT values from LDS
+// instead of 2 RT scattered 16-row requests. kStageMax dwords a lane.
+constexpr int kStageMax = 8;
+template <int RT> struct Stage {
+    uint32_t v[kStageMax];
+};
+// dwords this lane holds for an item: tensor t's RT * 8 * groups dwords, lane tid takes tid + k * nthr
+template <int RT>
+__device__ __forceinline__ void stage_load(const Stream<RT> &st, const GemmArgs &a, const Item<RT> &it, int tid,
+                                           int nthr, int groups, Stage<RT> &sg) {
+    const int per = RT * 8 * groups;               // dwords a tensor
+    const uint32_t base = (it.expert * (uint32_t)a.N + (uint32_t)it.c0) * (uint32_t)groups * 2;  // first tile row, bytes
+#pragma unroll
+    for (int k = 0; k < kStageMax; ++k) {
+        const int d = tid + (k >> 1) * nthr;       // even k: scales, odd k: mins
+        const int rt = d / (8 * groups), w = d % (8 * groups);
+        const uint32_t rows = (uint32_t)(rt % 2) * 16u + (uint32_t)(rt / 2) * (uint32_t)(a.N / 2);
+        const uint32_t off = d < per ? (rows * (uint32_t)groups + 2u * (uint32_t)w) * 2 : st.s_bytes;
+        sg.v[k] = bld4(k % 2 ? st.rm : st.rs, off, base);
+    }
+}
+template <int RT>
+__device__ __forceinline__ void stage_store(const Stage<RT> &sg, int tid, int nthr, int groups, uint16_t *buf) {
+    const int per = RT * 8 * groups;
+#pragma unroll
+    for (int k = 0; k < kStageMax; ++k) {
+        const int d = tid + (k >> 1) * nthr, t = k % 2;
+        if (d < per) {
+            const int rt = d / (8 * groups), w = d % (8 * groups);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int e = 2 * w + h, row = e / groups, gi = e % groups;
+                buf[((gi * 2 + t) * RT + rt) * 16 + row] = (uint16_t)(h ? sg.v[k] >> 16 : sg.v[k] & 0xFFFFu);
+            }
+        }
+    }
+}
+
+template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<EPI == EPI_SWIGLU>())))
     expert_stream_kernel(GemmArgs a, int64_t tiles_bound, int64_t col_blocks, int ks, uint32_t q_bytes,
                          uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
@@ -402,8 +460,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     constexpr int RT = wave_tiles<SWI>();
     constexpr int KS = SWI ? kWaves : 1;  // most waves of a block sharing an item (SwiGLU: the block's ks waves)
     constexpr int D = ring_depth<SWI>();
-    // partial sums of waves 1..ks-1, double-buffered by item parity so one barrier per item suffices
-    __shared__ float4v red[KS > 1 ? 2 * (KS - 1) * RT * kWave : 1];
+    // partial sums of waves 1..ks-1
+    __shared__ float4v red[KS > 1 ? (KS - 1) * RT * kWave : 1];
+    // SST: the staged scales, two item buffers of 2 * RT * 16 * groups bf16 (dynamic LDS)
+    extern __shared__ uint16_t stage_lds[];
+    static_assert(!SST || SWI, "scale staging rides on the SwiGLU block's per-item barrier");
     // the activation ring, one array per slot (separate objects let the compiler wait for each slot's loads alone):
     // [wave][MFMA u][lane] 16 bytes, written by the buffer-to-LDS loads in lane order
     __shared__ uint4 xr0[kWaves][F::NT][kWave], xr1[kWaves][F::NT][kWave], xr2[kWaves][F::NT][kWave],
@@ -437,6 +498,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     st.spw = KS > 1 ? spans * (wave + 1) / ks - st.s0 : spans;
     st.spe = (st.spw + D - 1) / D * D;
     st.gsh = a.G == 128 ? 7 : 6;
+    st.groups = (uint32_t)(a.K / a.G);
     const __amdgpu_buffer_rsrc_t ry = rsrc(a.y, y_bytes);
 
     // three items in flight: cur (streaming), nxt (offsets ready, its first steps prefetched), raw (loads issued)
@@ -445,15 +507,25 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     Item<RT> nxt = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, load_raw<MODE>(a, first + stride, n_tiles, col_blocks),
                                                             first + stride, n_items, col_blocks, report, x_bytes);
     RawItem raw = load_raw<MODE>(a, first + 2 * stride, n_tiles, col_blocks);
+    const int groups = (int)(a.K / a.G), tid = wave * kWave + lane, nthr = ks * kWave;
+    const int sbuf = 2 * RT * 16 * groups;  // bf16 per stage buffer
+    Stage<RT> sg;
+    if constexpr (SST) {  // cur's scales into buffer 0, nxt's into registers
+        stage_load(st, a, cur, tid, nthr, groups, sg);
+        stage_store(sg, tid, nthr, groups, stage_lds);
+        stage_load(st, a, nxt, tid, nthr, groups, sg);
+        lds_barrier();
+    }
+    const uint16_t *sl = stage_lds + j;  // this lane's row in the current buffer
     float4v acc[RT];
-    Codes<RT> c[D];
+    Codes<RT, SST> c[D];
     uint4 *xr[D];
     xr[0] = &xr0[wave][0][0], xr[1] = &xr1[wave][0][0], xr[2] = &xr2[wave][0][0];
     if constexpr (D > 3) xr[3] = &xr3[wave][0][0];
 #pragma unroll
     for (int t = 0; t < D; ++t) {
         if (t < D - 1) fetch_x<BITS, RT>(st, cur, nxt, t, xr[t]);
-        fetch_codes<BITS, RT>(st, cur, nxt, t, c[t]);
+        fetch_codes<BITS, RT, SST>(st, cur, nxt, t, c[t]);
     }
     int parity = 0;
     for (int64_t item = first; item < n_items; item += stride) {
@@ -461,21 +533,25 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
         for (int rt = 0; rt < RT; ++rt) acc[rt] = float4v{0, 0, 0, 0};
         int q = 0;
         do {  // spe >= D: at least one trip (the wait counts after the loop rely on its loads)
-            stream_trip<BITS, RT, XF16, D, 0>(st, cur, nxt, c, xr, q, acc, lane);
+            stream_trip<BITS, RT, XF16, D, SST, 0>(st, cur, nxt, c, xr, q, acc, lane, sl);
             q += D;
         } while (q < st.spe);
         // the item's end: K parts meet (SwiGLU), outputs stored
         if constexpr (KS > 1) {
-            float4v *rb = red + parity * (KS - 1) * RT * kWave;
+            // nxt's scales to the other stage buffer (no wave reads it: its last readers passed the previous item's
+            // barriers), the K parts to wave 0; the second barrier keeps red until wave 0 has read it
+            if constexpr (SST) stage_store(sg, tid, nthr, groups, stage_lds + (parity ^ 1) * sbuf);
             if (wave > 0)
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt) rb[((wave - 1) * RT + rt) * kWave + lane] = acc[rt];
+                for (int rt = 0; rt < RT; ++rt) red[((wave - 1) * RT + rt) * kWave + lane] = acc[rt];
             lds_barrier();
             if (wave == 0)
                 for (int w = 1; w < ks; ++w)
 #pragma unroll
-                    for (int rt = 0; rt < RT; ++rt) acc[rt] += rb[((w - 1) * RT + rt) * kWave + lane];
+                    for (int rt = 0; rt < RT; ++rt) acc[rt] += red[((w - 1) * RT + rt) * kWave + lane];
+            lds_barrier();
             parity ^= 1;
+            if constexpr (SST) sl = stage_lds + parity * sbuf + j;
         }
         if (wave == 0 || KS == 1) {
             // output rows of tokens 4g + r, from the lanes j = 4g + r that hold them
@@ -517,6 +593,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
         cur = nxt;
         nxt = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, raw, item + 2 * stride, n_items, col_blocks, report, x_bytes);
         raw = load_raw<MODE>(a, item + 3 * stride, n_tiles, col_blocks);
+        if constexpr (SST) stage_load(st, a, nxt, tid, nthr, groups, sg);
     }
 }
 
@@ -682,33 +759,33 @@ int device_cus() {
 }
 
 // Persistent grid: as many blocks as fit on the device at once (capped by the items), each looping over items.
-template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
-void launch_gemm(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
+// SwiGLU: K split over ks = 1..4 waves (the block), preferring an even split into whole ring trips of D steps and
+// then the most waves
+int swiglu_ks(int64_t spans, int D) {
+    int ks = 1;
+    int64_t best = -1;
+    for (int k = 1; k <= kWaves && k <= spans; ++k) {
+        const bool whole = spans % k == 0 && (spans / k) % D == 0;
+        const int64_t score = (whole ? 16 : 0) + k;
+        if (score > best) best = score, ks = k;
+    }
+    return ks;
+}
+
+template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST>
+void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
     constexpr bool SWI = EPI == EPI_SWIGLU;
     constexpr int RT = wave_tiles<SWI>();
     const int64_t spans = a.K / QFmt<BITS>::SPAN;
-    // SwiGLU: K split over ks = 1..4 waves (the block), preferring an even split into whole ring trips and then
-    // the most waves; otherwise one wave per item over all of K
-    int ks = 1;
-    if constexpr (SWI) {
-        int64_t best = -1;
-        for (int k = 1; k <= kWaves && k <= spans; ++k) {
-            const bool whole = spans % k == 0 && (spans / k) % ring_depth<SWI>() == 0;
-            const int64_t score = (whole ? 16 : 0) + k;
-            if (score > best) best = score, ks = k;
-        }
-    }
+    const int ks = SWI ? swiglu_ks(spans, ring_depth<SWI>()) : 1;  // otherwise one wave per item over all of K
+    const size_t lds = SST ? (size_t)2 * 2 * RT * 16 * (a.K / a.G) * 2 : 0;
     const int threads = SWI ? ks * kWave : kThreads;
     const int64_t col_blocks = SWI ? (a.N / 2 + 16 * RT / 2 - 1) / (16 * RT / 2) : (a.N + 16 * RT - 1) / (16 * RT);
     const int64_t items = tiles_bound * col_blocks, per_block = SWI ? 1 : kWaves;
-    auto kernel = expert_stream_kernel<BITS, MODE, EPI, XF16, XROW_DIV, HF16>;
-    static int occ[kWaves + 1] = {};
-    if (occ[threads / kWave] == 0) {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n < 1) n = 1;
-        occ[threads / kWave] = n;
-    }
-    const int64_t want = (items + per_block - 1) / per_block, cap = (int64_t)device_cus() * occ[threads / kWave];
+    auto kernel = expert_stream_kernel<BITS, MODE, EPI, XF16, XROW_DIV, HF16, SST>;
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, lds) != hipSuccess || occ < 1) occ = 1;
+    const int64_t want = (items + per_block - 1) / per_block, cap = (int64_t)device_cus() * occ;
     const int64_t blocks = std::max<int64_t>(1, std::min(want, cap));
     // 32-bit buffer offsets: the weight view and the activations must each stay below 2 GiB
     const int64_t q_bytes = a.N * a.E * a.K * BITS / 8, s_bytes = a.N * a.E * (a.K / a.G) * 2;
@@ -719,8 +796,20 @@ void launch_gemm(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
     STRIX_CHECK(q_bytes < (1ll << 31) && s_bytes < (1ll << 31) && x_bytes < (1ll << 31) && y_bytes < (1ll << 31),
                 "expert kernels: weight (", q_bytes, " B), activation (", x_bytes, " B) or output (", y_bytes,
                 " B) tensor at or above 2 GiB (32-bit buffer offsets)");
-    kernel<<<(unsigned)blocks, threads, 0, stream>>>(a, tiles_bound, col_blocks, ks, (uint32_t)q_bytes,
+    kernel<<<(unsigned)blocks, threads, lds, stream>>>(a, tiles_bound, col_blocks, ks, (uint32_t)q_bytes,
                                                       (uint32_t)s_bytes, (uint32_t)x_bytes, (uint32_t)y_bytes);
+}
+
+template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
+void launch_gemm(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
+    if constexpr (EPI == EPI_SWIGLU) {
+        // scale staging when an item's scales fit kStageMax dwords a lane of the block
+        const int ks = swiglu_ks(a.K / QFmt<BITS>::SPAN, ring_depth<true>());
+        const int64_t dwords = 2 * wave_tiles<true>() * 8 * (a.K / a.G);
+        if ((dwords + 2 * ks * kWave - 1) / (2 * ks * kWave) * 2 <= kStageMax)
+            return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, true>(a, tiles_bound, stream);
+    }
+    launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, false>(a, tiles_bound, stream);
 }
 
 template <int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
