@@ -133,11 +133,11 @@ def main():
 
     # dominant decode kernel: the grouped gate_up + SwiGLU over the layer's own routing, timed alone
     routes = [moe.moe_group_routes(outs[l]["ids"], E)[0] for l in range(nl)]
-    hbuf = [torch.empty((Md * K_TOP, I), dtype=torch.float16, device=dev) for _ in range(nl)]
+    hbuf = [torch.empty((Md * K_TOP, I), dtype=torch.bfloat16, device=dev) for _ in range(nl)]
     torch.cuda.synchronize()
 
     def gu_launch(l):
-        moe.experts_gather_grouped_swiglu(xs[l], layers[l].gate_up, E, routes[l], Md, K_TOP, h_f16=True, h=hbuf[l])
+        moe.experts_gather_grouped_swiglu(xs[l], layers[l].gate_up, E, routes[l], Md, K_TOP, h=hbuf[l])
 
     for i in range(args.warmup):
         gu_launch(i % nl)
@@ -178,14 +178,13 @@ def main():
         cnt = np.bincount(pouts[0]["ids"].cpu().numpy().ravel(), minlength=E)
         # dominant prefill kernel: the grouped gate_up + SwiGLU
         proutes = [moe.moe_group_routes(pouts[l]["ids"], E)[0] for l in range(nl)]
-        ph = torch.empty((Mp * K_TOP, I), dtype=torch.float16, device=dev)
-        moe.experts_gather_grouped_swiglu(xp, players[0].gate_up, E, proutes[0], Mp, K_TOP, h_f16=True, h=ph)
+        ph = torch.empty((Mp * K_TOP, I), dtype=torch.bfloat16, device=dev)
+        moe.experts_gather_grouped_swiglu(xp, players[0].gate_up, E, proutes[0], Mp, K_TOP, h=ph)
         torch.cuda.synchronize()
         preps = 2 * nl
         ev0.record()
         for i in range(preps):
-            moe.experts_gather_grouped_swiglu(xp, players[i % nl].gate_up, E, proutes[i % nl], Mp, K_TOP, h_f16=True,
-                                              h=ph)
+            moe.experts_gather_grouped_swiglu(xp, players[i % nl].gate_up, E, proutes[i % nl], Mp, K_TOP, h=ph)
         ev1.record()
         torch.cuda.synchronize()
         pgu_us = ev0.elapsed_time(ev1) / preps * 1e3

@@ -411,16 +411,16 @@ __device__ __forceinline__ void stream_trip(const Stream<RT> &st, const Item<RT>
     }
 }
 
-// Scale staging (SwiGLU, SST): an item's scales and mins - for each tile rt its 16 rows x groups bf16, contiguous in
-// memory - are read by the block's ks waves as dwords one item ahead, held in registers, and written to LDS at the
-// previous item's end transposed to [group][scale, min][tile][row], so a K step reads its 2 RT values from LDS
-// instead of 2 RT scattered 16-row requests. kStageMax dwords a lane.
+// Scale staging (SST): an item's scales and mins - for each tile rt its 16 rows x groups bf16, contiguous in memory -
+// are read as dwords one item ahead (SwiGLU: by the block's ks waves together; otherwise by the item's wave), held in
+// registers, and written to LDS at the previous item's end transposed to [group][scale, min][tile][row], so a K step
+// reads its 2 RT values from LDS instead of 2 RT scattered 16-row requests. kStageMax dwords a lane.
 constexpr int kStageMax = 8;
 template <int RT> struct Stage {
     uint32_t v[kStageMax];
 };
 // dwords this lane holds for an item: tensor t's RT * 8 * groups dwords, lane tid takes tid + k * nthr
-template <int RT>
+template <int RT, bool SWI>
 __device__ __forceinline__ void stage_load(const Stream<RT> &st, const GemmArgs &a, const Item<RT> &it, int tid,
                                            int nthr, int groups, Stage<RT> &sg) {
     const int per = RT * 8 * groups;               // dwords a tensor
@@ -429,7 +429,7 @@ __device__ __forceinline__ void stage_load(const Stream<RT> &st, const GemmArgs 
     for (int k = 0; k < kStageMax; ++k) {
         const int d = tid + (k >> 1) * nthr;       // even k: scales, odd k: mins
         const int rt = d / (8 * groups), w = d % (8 * groups);
-        const uint32_t rows = (uint32_t)(rt % 2) * 16u + (uint32_t)(rt / 2) * (uint32_t)(a.N / 2);
+        const uint32_t rows = SWI ? (uint32_t)(rt % 2) * 16u + (uint32_t)(rt / 2) * (uint32_t)(a.N / 2) : 16u * rt;
         const uint32_t off = d < per ? (rows * (uint32_t)groups + 2u * (uint32_t)w) * 2 : st.s_bytes;
         sg.v[k] = bld4(k % 2 ? st.rm : st.rs, off, base);
     }
@@ -463,8 +463,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     // partial sums of waves 1..ks-1
     __shared__ float4v red[KS > 1 ? (KS - 1) * RT * kWave : 1];
     // SST: the staged scales, two item buffers of 2 * RT * 16 * groups bf16 (dynamic LDS)
+    // (SwiGLU: one pair for the block, written behind the per-item barrier; otherwise one buffer a wave, which only
+    // that wave reads, so program order suffices)
     extern __shared__ uint16_t stage_lds[];
-    static_assert(!SST || SWI, "scale staging rides on the SwiGLU block's per-item barrier");
     // the activation ring, one array per slot (separate objects let the compiler wait for each slot's loads alone):
     // [wave][MFMA u][lane] 16 bytes, written by the buffer-to-LDS loads in lane order
     __shared__ uint4 xr0[kWaves][F::NT][kWave], xr1[kWaves][F::NT][kWave], xr2[kWaves][F::NT][kWave],
@@ -507,16 +508,17 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     Item<RT> nxt = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, load_raw<MODE>(a, first + stride, n_tiles, col_blocks),
                                                             first + stride, n_items, col_blocks, report, x_bytes);
     RawItem raw = load_raw<MODE>(a, first + 2 * stride, n_tiles, col_blocks);
-    const int groups = (int)(a.K / a.G), tid = wave * kWave + lane, nthr = ks * kWave;
+    const int groups = (int)(a.K / a.G), tid = SWI ? wave * kWave + lane : lane, nthr = SWI ? ks * kWave : kWave;
     const int sbuf = 2 * RT * 16 * groups;  // bf16 per stage buffer
+    uint16_t *const sown = stage_lds + (SWI ? 0 : wave * sbuf);  // SwiGLU: the block's pair; otherwise this wave's
     Stage<RT> sg;
-    if constexpr (SST) {  // cur's scales into buffer 0, nxt's into registers
-        stage_load(st, a, cur, tid, nthr, groups, sg);
-        stage_store(sg, tid, nthr, groups, stage_lds);
-        stage_load(st, a, nxt, tid, nthr, groups, sg);
-        lds_barrier();
+    if constexpr (SST) {  // cur's scales into the (first) buffer, nxt's into registers
+        stage_load<RT, SWI>(st, a, cur, tid, nthr, groups, sg);
+        stage_store(sg, tid, nthr, groups, sown);
+        stage_load<RT, SWI>(st, a, nxt, tid, nthr, groups, sg);
+        if constexpr (SWI) lds_barrier();
     }
-    const uint16_t *sl = stage_lds + j;  // this lane's row in the current buffer
+    const uint16_t *sl = sown + j;  // this lane's row in the current buffer
     float4v acc[RT];
     Codes<RT, SST> c[D];
     uint4 *xr[D];
@@ -553,6 +555,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
             parity ^= 1;
             if constexpr (SST) sl = stage_lds + parity * sbuf + j;
         }
+        if constexpr (SST && !SWI) stage_store(sg, tid, nthr, groups, sown);  // program order: reads of cur are done
         if (wave == 0 || KS == 1) {
             // output rows of tokens 4g + r, from the lanes j = 4g + r that hold them
             const int g = lane / 16;
@@ -593,7 +596,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
         cur = nxt;
         nxt = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, raw, item + 2 * stride, n_items, col_blocks, report, x_bytes);
         raw = load_raw<MODE>(a, item + 3 * stride, n_tiles, col_blocks);
-        if constexpr (SST) stage_load(st, a, nxt, tid, nthr, groups, sg);
+        if constexpr (SST) stage_load<RT, SWI>(st, a, nxt, tid, nthr, groups, sg);
     }
 }
 
@@ -778,7 +781,8 @@ void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
     constexpr int RT = wave_tiles<SWI>();
     const int64_t spans = a.K / QFmt<BITS>::SPAN;
     const int ks = SWI ? swiglu_ks(spans, ring_depth<SWI>()) : 1;  // otherwise one wave per item over all of K
-    const size_t lds = SST ? (size_t)2 * 2 * RT * 16 * (a.K / a.G) * 2 : 0;
+    // SwiGLU: two stage buffers for the block; otherwise one a wave
+    const size_t lds = SST ? (size_t)(SWI ? 2 : kWaves) * 2 * RT * 16 * (a.K / a.G) * 2 : 0;
     const int threads = SWI ? ks * kWave : kThreads;
     const int64_t col_blocks = SWI ? (a.N / 2 + 16 * RT / 2 - 1) / (16 * RT / 2) : (a.N + 16 * RT - 1) / (16 * RT);
     const int64_t items = tiles_bound * col_blocks, per_block = SWI ? 1 : kWaves;
@@ -802,13 +806,12 @@ void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
 
 template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
 void launch_gemm(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
-    if constexpr (EPI == EPI_SWIGLU) {
-        // scale staging when an item's scales fit kStageMax dwords a lane of the block
-        const int ks = swiglu_ks(a.K / QFmt<BITS>::SPAN, ring_depth<true>());
-        const int64_t dwords = 2 * wave_tiles<true>() * 8 * (a.K / a.G);
-        if ((dwords + 2 * ks * kWave - 1) / (2 * ks * kWave) * 2 <= kStageMax)
-            return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, true>(a, tiles_bound, stream);
-    }
+    // scale staging when an item's scales fit kStageMax dwords a lane of the item's waves
+    constexpr bool SWI = EPI == EPI_SWIGLU;
+    const int lanes = (SWI ? swiglu_ks(a.K / QFmt<BITS>::SPAN, ring_depth<true>()) : 1) * kWave;
+    const int64_t per_tensor = wave_tiles<SWI>() * 8 * (a.K / a.G);  // dwords
+    if ((per_tensor + lanes - 1) / lanes * 2 <= kStageMax)
+        return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, true>(a, tiles_bound, stream);
     launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, false>(a, tiles_bound, stream);
 }
 
@@ -1142,8 +1145,9 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     const bool q8 = w.gate_up_bits == 8;
     const Q8DeviceView gu8{w.gate_up.q, w.gate_up.scale, w.gate_up.minv, w.gate_up.N, w.gate_up.K, w.gate_up.G};
     const Q8DeviceView dn8{w.down.q, w.down.scale, w.down.minv, w.down.N, w.down.K, w.down.G};
-    if (q8) linear_q8_experts_gather_grouped_swiglu(x, gu8, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, true);
-    else linear_q4_experts_gather_grouped_swiglu(x, w.gate_up, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, true);
+    // h in bf16: the oracle's rounding of silu(g) * u, with bf16's range (the f16 form is the reference API's option)
+    if (q8) linear_q8_experts_gather_grouped_swiglu(x, gu8, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
+    else linear_q4_experts_gather_grouped_swiglu(x, w.gate_up, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
     // shared expert (dense Q8): gate_up + SwiGLU -> sh_h, down -> sh_s
     if (w.has_shared) {
         const QV gv = qv(w.sh_gate_up), dv = qv(w.sh_down);
@@ -1162,8 +1166,8 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         check_view(fn, dv, E);
         GemmArgs a = make_args(dv, E, h, partial, H);
         a.A = k, a.ws = static_cast<const int32_t *>(route), a.S = M * k;
-        if (q8) launch_gemm<8, GROUPED, EPI_F32, true, false, false>(a, grouped_tiles(M, k, E), stream);
-        else launch_gemm<4, GROUPED, EPI_F32, true, false, false>(a, grouped_tiles(M, k, E), stream);
+        if (q8) launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream);
+        else launch_gemm<4, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream);
     }
     const MoeSharedAdd sh{sh_s, lg + E, ld, (uint32_t)E, err_router};
     combine_reduce(partial, ids, coef, M, k, E, H, static_cast<uint16_t *>(y), w.has_shared ? &sh : nullptr,
