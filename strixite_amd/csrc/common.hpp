@@ -12,6 +12,14 @@
 
 namespace strix {
 
+// Internal entry (route.hip), used by the layer forward for small batches: top-k of FP32 logits (no shared-expert
+// slot) and the packing of moe_group_routes in one launch, M k <= 1024.
+namespace kernels {
+void moe_topk_group_routes_small(const float *logits, int64_t ld, int64_t M, int64_t E, int64_t k, int32_t *ids,
+                                 float *coef, void *ws, size_t ws_bytes, uint32_t *err_router, uint32_t *err_route,
+                                 hipStream_t stream);
+}  // namespace kernels
+
 // ---- host-side checks -----------------------------------------------------------------------------------------
 // A failed precondition throws strix::Error carrying "fn (file:line): check `cond` failed: message", the form of
 // strixite common/check.hpp:59-79.

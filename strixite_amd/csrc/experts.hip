@@ -15,6 +15,8 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -787,8 +789,13 @@ void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
     const int64_t col_blocks = SWI ? (a.N / 2 + 16 * RT / 2 - 1) / (16 * RT / 2) : (a.N + 16 * RT - 1) / (16 * RT);
     const int64_t items = tiles_bound * col_blocks, per_block = SWI ? 1 : kWaves;
     auto kernel = expert_stream_kernel<BITS, MODE, EPI, XF16, XROW_DIV, HF16, SST>;
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, lds) != hipSuccess || occ < 1) occ = 1;
+    // resident blocks a CU, cached for the last (block size, LDS) this instantiation was launched with
+    static thread_local int occ_threads = -1, occ = 1;
+    static thread_local size_t occ_lds = 0;
+    if (threads != occ_threads || lds != occ_lds) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, lds) != hipSuccess || occ < 1) occ = 1;
+        occ_threads = threads, occ_lds = lds;
+    }
     const int64_t want = (items + per_block - 1) / per_block, cap = (int64_t)device_cus() * occ;
     const int64_t blocks = std::max<int64_t>(1, std::min(want, cap));
     // 32-bit buffer offsets: the weight view and the activations must each stay below 2 GiB
@@ -1098,6 +1105,30 @@ size_t moe_layer_workspace_bytes(const MoeLayerWeights &w, int64_t M) {
     return (size_t)layer_ws(w, M).total;
 }
 
+namespace {
+// The shared expert runs on a helper stream beside the routing kernels (router, top-k, packing), which leave most of
+// the chip idle: forked from the caller's stream with an event and joined back before the combine. One helper
+// stream and event pair per device, created on the first layer call (before any graph capture); a mutex serialises
+// layer calls so that each join waits on its own fork.
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex side_mu;
+SideStream &side_stream(const char *fn) {
+    static std::map<int, SideStream> per_device;
+    int dev = 0;
+    STRIX_HIP_CHECK(hipGetDevice(&dev), fn, ": hipGetDevice");
+    SideStream &ss = per_device[dev];
+    if (!ss.s) {
+        STRIX_HIP_CHECK(hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking), fn, ": helper stream");
+        STRIX_HIP_CHECK(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming), fn, ": fork event");
+        STRIX_HIP_CHECK(hipEventCreateWithFlags(&ss.join, hipEventDisableTiming), fn, ": join event");
+    }
+    return ss;
+}
+}  // namespace
+
 void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const float *logits_in, void *y,
                        void *x_out, int32_t *ids_out, float *coef_out, void *ws, size_t ws_bytes, uint32_t *err,
                        hipStream_t stream) {
@@ -1128,6 +1159,27 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     uint16_t *sh_s = reinterpret_cast<uint16_t *>(base + L.sh_s);
     uint32_t *err_router = err, *err_expert = err + 3;
 
+    // shared expert (dense Q8) on the helper stream: gate_up + SwiGLU -> sh_h, down -> sh_s
+    std::unique_lock<std::mutex> side_lock(side_mu, std::defer_lock);
+    SideStream *ss = nullptr;
+    if (w.has_shared) {
+        const QV gv = qv(w.sh_gate_up), dv = qv(w.sh_down);
+        check_view(fn, gv, 1);
+        check_view(fn, dv, 1);
+        side_lock.lock();
+        ss = &side_stream(fn);
+        STRIX_HIP_CHECK(hipEventRecord(ss->fork, stream), fn, ": fork");
+        STRIX_HIP_CHECK(hipStreamWaitEvent(ss->s, ss->fork, 0), fn, ": fork wait");
+        GemmArgs a = make_args(gv, 1, x, sh_h, I);
+        a.M = M;
+        launch_gemm<8, DENSE, EPI_SWIGLU, false, false, false>(a, (M + 15) / 16, ss->s);
+        GemmArgs b = make_args(dv, 1, sh_h, sh_s, H);
+        b.M = M;
+        launch_gemm<8, DENSE, EPI_BF16, false, false, false>(b, (M + 15) / 16, ss->s);
+        STRIX_HIP_CHECK_LAUNCH(fn, " shared expert M=", M);
+        STRIX_HIP_CHECK(hipEventRecord(ss->join, ss->s), fn, ": join");
+    }
+
     // router projection (+ harness bias) and top-k
     const float *lg = logits_in;
     if (!lg) {
@@ -1139,8 +1191,12 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         }
         lg = logits;
     }
-    moe_router(lg, ld, M, E, k, nullptr, 0, 0, ids, coef, Act::F32, err_router, stream);
-    moe_group_routes(ids, M, k, E, route, L.route_bytes, err_expert, stream);
+    if (M * k <= 1024) {  // one launch: top-k and packing with the ids kept in LDS
+        moe_topk_group_routes_small(lg, ld, M, E, k, ids, coef, route, L.route_bytes, err_router, err_expert, stream);
+    } else {
+        moe_router(lg, ld, M, E, k, nullptr, 0, 0, ids, coef, Act::F32, err_router, stream);
+        moe_group_routes(ids, M, k, E, route, L.route_bytes, err_expert, stream);
+    }
     // routed experts: gate_up + SwiGLU -> h, down -> partial
     const bool q8 = w.gate_up_bits == 8;
     const Q8DeviceView gu8{w.gate_up.q, w.gate_up.scale, w.gate_up.minv, w.gate_up.N, w.gate_up.K, w.gate_up.G};
@@ -1148,19 +1204,6 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     // h in bf16: the oracle's rounding of silu(g) * u, with bf16's range (the f16 form is the reference API's option)
     if (q8) linear_q8_experts_gather_grouped_swiglu(x, gu8, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
     else linear_q4_experts_gather_grouped_swiglu(x, w.gate_up, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
-    // shared expert (dense Q8): gate_up + SwiGLU -> sh_h, down -> sh_s
-    if (w.has_shared) {
-        const QV gv = qv(w.sh_gate_up), dv = qv(w.sh_down);
-        check_view(fn, gv, 1);
-        check_view(fn, dv, 1);
-        GemmArgs a = make_args(gv, 1, x, sh_h, I);
-        a.M = M;
-        launch_gemm<8, DENSE, EPI_SWIGLU, false, false, false>(a, (M + 15) / 16, stream);
-        GemmArgs b = make_args(dv, 1, sh_h, sh_s, H);
-        b.M = M;
-        launch_gemm<8, DENSE, EPI_BF16, false, false, false>(b, (M + 15) / 16, stream);
-        STRIX_HIP_CHECK_LAUNCH(fn, " shared expert M=", M);
-    }
     {
         const QV dv = q8 ? qv(dn8) : qv(w.down);
         check_view(fn, dv, E);
@@ -1169,6 +1212,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         if (q8) launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream);
         else launch_gemm<4, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream);
     }
+    if (ss) STRIX_HIP_CHECK(hipStreamWaitEvent(stream, ss->join, 0), fn, ": join wait");
     const MoeSharedAdd sh{sh_s, lg + E, ld, (uint32_t)E, err_router};
     combine_reduce(partial, ids, coef, M, k, E, H, static_cast<uint16_t *>(y), w.has_shared ? &sh : nullptr,
                    static_cast<const uint16_t *>(x), static_cast<uint16_t *>(x_out), stream);

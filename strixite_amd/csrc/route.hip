@@ -8,9 +8,11 @@
 // stable order by construction. Small S (<= 16 chunks) runs as one 1024-thread block with everything in LDS; larger S
 // as three launches (chunk histograms, scan, placement) through the workspace.
 #include "common.hpp"
+#include "topk.hpp"
 
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 namespace strix::kernels {
 
@@ -275,6 +277,89 @@ __global__ void __launch_bounds__(256) route_tiles_kernel(Layout L, int32_t *ws)
     fill_tile_slots(ws, L, ws[0], (int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x);
 }
 
+
+// ---- top-k + packing for small batches (S = M k <= 1024): one 1024-thread block, ids never leave LDS ---------------
+// Phase A: wave w takes tokens w, w + 16, ...: top-k (ids, coef out, and ids into LDS). Phase B: wave w takes slots
+// [64 w, 64 w + 64): histogram, block scan, placement into LDS, then the workspace written from LDS (slots, offsets,
+// tile records). The workspace layout and contents are those of moe_group_routes.
+constexpr int kFusedSlots = 1024;
+
+template <int NV>
+__global__ void __launch_bounds__(1024)
+    topk_route_small_kernel(const float *logits, int64_t ld, int M, int E, int k, int32_t *ids_out, float *coef_out,
+                            Layout L, int nbits, int32_t *ws, uint32_t *err_router, uint32_t *err_route) {
+    extern __shared__ int lds[];
+    const int S = (int)L.S, nb = E + 1, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, t = threadIdx.x;
+    int *sids = lds;                          // [S] ids by slot
+    int *sl = sids + kFusedSlots;             // [S] slots by position
+    int *cnt = sl + kFusedSlots;              // [16][E + 1] wave counts, then cursors
+    int *bstart = cnt + kSmallWaves * nb;     // [E + 1] bucket start
+    int *btile = bstart + nb;                 // [E + 1] bucket's first 16-slot tile
+    int *bcount = btile + nb;                 // [E + 1]
+    int *tile_b = bcount + nb;                // [T16] bucket of a tile
+    int *wsum = tile_b + L.T16;               // [48]
+    int *bad = wsum + 48;                     // [1]
+    // A: top-k
+    for (int m = wave; m < M; m += kSmallWaves) {
+        int id;
+        float cf;
+        const int rb = topk::wave_topk<float, NV>(logits + (int64_t)m * ld, E, k, id, cf);
+        if (rb != INT_MAX) {
+            if (lane == 0 && atomicCAS(&err_router[0], 0u, 1u) == 0u) {
+                err_router[1] = (uint32_t)m;
+                err_router[2] = (uint32_t)rb;
+            }
+            id = -1, cf = dev::qnan();
+        }
+        if (lane < k) {
+            ids_out[m * k + lane] = id;
+            coef_out[m * k + lane] = cf;
+            sids[m * k + lane] = id;
+        }
+    }
+    for (int i = t; i < kSmallWaves * nb; i += blockDim.x) cnt[i] = 0;
+    if (t == 0) *bad = INT_MAX;
+    __syncthreads();
+    // B: histogram of this wave's chunk
+    const int s0 = wave * kWave, s1 = min(s0 + kWave, S);
+    if (s0 < S) {
+        const int fb = chunk_hist(sids, s0, s1, E, nbits, cnt + wave * nb);
+        if (lane == 0 && fb != INT_MAX) atomicMin(bad, fb);
+    }
+    __syncthreads();
+    int c = 0;
+    if (t <= E)
+        for (int w = 0; w < kSmallWaves; ++w) c += cnt[w * nb + t];
+    int v[3] = {c, (c + kTileRows - 1) / kTileRows, (c + kWideRows - 1) / kWideRows}, tot[3];
+    block_scan3(v, wsum, tot);
+    if (t <= E) {
+        write_bucket(t, c, v, ws, L);
+        bstart[t] = v[0], btile[t] = v[1], bcount[t] = c;
+        for (int i = 0; i < (c + kTileRows - 1) / kTileRows; ++i) tile_b[v[1] + i] = t;
+        int run = v[0];
+        for (int w = 0; w < kSmallWaves; ++w) {
+            const int x = cnt[w * nb + t];
+            cnt[w * nb + t] = run;
+            run += x;
+        }
+    }
+    if (t == 0) {
+        write_header(ws, L, tot);
+        // the ids live in LDS here: report_bad reads them through this pointer
+        report_bad(sids, *bad, err_route);
+    }
+    __syncthreads();
+    if (s0 < S) chunk_place(sids, s0, s1, E, nbits, cnt + wave * nb, sl);
+    __syncthreads();
+    for (int i = t; i < S; i += blockDim.x) ws[L.slots() + i] = sl[i];
+    // tile records' slot lists from LDS: thread per (tile, slot)
+    for (int i = t; i < tot[1] * kTileRows; i += blockDim.x) {
+        const int ti = i / kTileRows, jj = i % kTileRows, b = tile_b[ti], r = ti - btile[b];
+        const int rows = min(kTileRows, bcount[b] - r * kTileRows);
+        ws[L.t16_rec() + kRec16 * ti + 4 + jj] = jj < rows ? sl[bstart[b] + r * kTileRows + jj] : -1;
+    }
+}
+
 }  // namespace
 
 size_t moe_route_workspace_bytes(int64_t M, int64_t A, int64_t E) {
@@ -312,6 +397,35 @@ void moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void 
         route_tiles_kernel<<<(unsigned)(tb < 4096 ? tb : 4096), 256, 0, stream>>>(L, w);
     }
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E);
+}
+
+
+void moe_topk_group_routes_small(const float *logits, int64_t ld, int64_t M, int64_t E, int64_t k, int32_t *ids,
+                                 float *coef, void *ws, size_t ws_bytes, uint32_t *err_router, uint32_t *err_route,
+                                 hipStream_t stream) {
+    const char *fn = "moe_topk_group_routes_small";
+    STRIX_CHECK(M >= 1 && k >= 1 && k <= 64 && k <= E && E <= kMoeMaxExperts && M * k <= kFusedSlots, fn,
+                ": M = ", M, ", E = ", E, ", k = ", k, " (M k <= ", kFusedSlots, ")");
+    STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, k, E) && reinterpret_cast<uintptr_t>(ws) % 16 == 0, fn,
+                ": workspace of ", ws_bytes, " bytes, needs ", moe_route_workspace_bytes(M, k, E), ", 16-byte aligned");
+    const route::Layout L = route::layout(M, k, E);
+    int nbits = 0;
+    while ((1ll << nbits) <= E) ++nbits;
+    const size_t lds = ((size_t)2 * kFusedSlots + (size_t)route::kSmallWaves * (E + 1) + 3 * (size_t)(E + 1) +
+                        (size_t)L.T16 + 48 + 1) * 4;
+    const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
+    auto go = [&](auto nvc) {
+        topk_route_small_kernel<decltype(nvc)::value><<<1, 1024, lds, stream>>>(
+            logits, ld, (int)M, (int)E, (int)k, ids, coef, L, nbits, static_cast<int32_t *>(ws), err_router, err_route);
+    };
+    switch (nv) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        case 8: go(std::integral_constant<int, 8>{}); break;
+        default: go(std::integral_constant<int, 16>{}); break;
+    }
+    STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " E=", E, " k=", k);
 }
 
 }  // namespace strix::kernels

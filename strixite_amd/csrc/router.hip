@@ -2,6 +2,7 @@
 // the top-k / softmax (moe_router, one wave64 per token, logits in registers), and the shared expert's gated add
 // (moe_shared_add, moe_shared_add_inject).
 #include "common.hpp"
+#include "topk.hpp"
 
 #include <climits>
 #include <type_traits>
@@ -125,10 +126,6 @@ void launch_router_rows(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, 
 // One wave64 per token (4 a block). Lane l holds experts l, l + 64, ... (NV registers, -inf past E). A round is a
 // 64-lane arg-max over the lanes' bests (larger value, then lower index); the winner lane masks its pick and rescans
 // its registers. Lane r keeps the r-th pick, so the softmax over the k is one butterfly sum.
-template <typename T> __device__ __forceinline__ float load_logit(const T *p, int64_t i);
-template <> __device__ __forceinline__ float load_logit<float>(const float *p, int64_t i) { return p[i]; }
-template <> __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t *p, int64_t i) { return bf16_to_f32(p[i]); }
-
 template <typename T, int NV>
 __global__ void __launch_bounds__(kThreads)
     topk_kernel(const T *logits, int64_t ld, int64_t M, int E, int k, const T *shared, int64_t shared_ld,
@@ -136,25 +133,18 @@ __global__ void __launch_bounds__(kThreads)
     const int lane = threadIdx.x % kWave;
     const int64_t m = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
     if (m >= M) return;  // whole wave; no barrier in this kernel
-    const T *row = logits + m * ld;
-    float v[NV];
-    int bad = INT_MAX;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int e = lane + j * kWave;
-        const float xv = e < E ? load_logit(row, e) : -INFINITY;
-        v[j] = xv;
-        if (e < E && !isfinite(xv) && e < bad) bad = e;
-    }
-    float sl = 0.f;
-    if (shared != nullptr) {
-        sl = load_logit(shared, m * shared_ld);
-        if (!isfinite(sl) && E < bad) bad = E;
-    }
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off, kWave));
     int32_t *id_row = ids + m * A;
     float *coef_row = coef + m * A;
+    float sl = 0.f;
+    int bad = INT_MAX;
+    if (shared != nullptr) {
+        sl = topk::load_logit(shared, m * shared_ld);
+        if (!isfinite(sl)) bad = E;
+    }
+    int id;
+    float cf;
+    const int rb = topk::wave_topk<T, NV>(logits + m * ld, E, k, id, cf);
+    bad = rb < bad ? rb : bad;
     if (bad != INT_MAX) {
         if (lane == 0 && atomicCAS(&err[0], 0u, 1u) == 0u) {
             err[1] = (uint32_t)m;
@@ -163,43 +153,9 @@ __global__ void __launch_bounds__(kThreads)
         for (int a = lane; a < A; a += kWave) id_row[a] = -1, coef_row[a] = qnan();
         return;
     }
-    // finite from here: -inf marks a taken expert and the padding past E
-    float lv = -INFINITY;
-    int li = INT_MAX;
-    auto lane_best = [&]() {
-        lv = -INFINITY, li = INT_MAX;
-#pragma unroll
-        for (int j = 0; j < NV; ++j)
-            if (v[j] > lv) lv = v[j], li = lane + j * kWave;  // ascending scan, strict >: lower index on ties
-    };
-    lane_best();
-    float my_v = -INFINITY, top = 0.f;
-    int my_i = -1;
-    for (int r = 0; r < k; ++r) {
-        float bv = lv;
-        int bi = li;
-#pragma unroll
-        for (int off = kWave / 2; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, kWave);
-            const int oi = __shfl_xor(bi, off, kWave);
-            if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
-        }
-        if (r == 0) top = bv;
-        if (lane == r) my_v = bv, my_i = bi;
-        if (bi == li) {  // the pick is this lane's best (an index lives in one lane only)
-#pragma unroll
-            for (int j = 0; j < NV; ++j)
-                if (lane + j * kWave == bi) v[j] = -INFINITY;
-            lane_best();
-        }
-    }
-    const float ex = lane < k ? expf(my_v - top) : 0.f;
-    float sum = ex;
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, kWave);
     if (lane < k) {
-        id_row[lane] = my_i;
-        coef_row[lane] = ex / sum;
+        id_row[lane] = id;
+        coef_row[lane] = cf;
     }
     if (shared != nullptr && lane == 0) {
         id_row[k] = shared_id;

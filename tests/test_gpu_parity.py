@@ -306,6 +306,40 @@ def _layer_parity(layer, M, seed, logits_in=None, sample=None):
     return out, o, e
 
 
+@pytest.mark.parametrize("M,E,k", [(16, 64, 8), (128, 64, 8), (512, 512, 2), (3, 512, 10)])
+def test_layer_fused_topk_packing_matches_router(M, E, k):
+    """Small batches (M k <= 1024) route through one fused top-k + packing launch inside the layer: its ids and
+    weights equal the standalone moe_router's bit for bit, ties and a non-finite token included, and the layer's
+    output matches the same layer fed the standalone router's routing through the oracle's reference."""
+    say("fused routing", M, E, k)
+    layer = moe.MoeLayer.synth(256, E, k, 128, seed=3)
+    rng = np.random.default_rng(M + E + k)
+    ld = E + 1  # the layer's logits carry the shared-expert gate in column E
+    lg = rng.standard_normal((M, ld)).astype(np.float32)
+    lg[0, :E] = 0.5                      # all equal: ids 0..k-1
+    if M > 2:
+        lg[1, 2:2 + k + 2] = lg[1, :E].max() + 1  # a tie at the top
+        lg[2, 5] = np.nan                 # a non-finite token
+    x = moe.synth_bf16_normal(3, "x", 7, (M, 256), 1.0)
+    out = layer.forward(x, logits_in=torch.from_numpy(lg).to(DEV))
+    torch.cuda.synchronize()
+    rids, rcoef, rerr = moe.moe_router(torch.from_numpy(np.ascontiguousarray(lg)).to(DEV), E, k, ld=ld)
+    assert np.array_equal(to_np(out["ids"]), to_np(rids))
+    assert np.array_equal(to_np(out["coef"]).view(np.uint32), to_np(rcoef).view(np.uint32))
+    err = to_np(out["err"])
+    if M > 2:
+        assert err[0] == 1 and err[1] == 2 and err[2] == 5 and to_np(rerr)[0] == 1
+        assert err[3] == 1, "the non-finite token's -1 ids reach the packing as invalid"
+    else:
+        assert err[0] == 0 and err[3] == 0
+    # the routed part of the layer against the oracle on the finite tokens
+    ok = np.all(np.isfinite(lg[:, :E]), axis=1)
+    ws, _ = moe.moe_group_routes(rids, E)
+    off, _, _ = orc.group_routes(to_np(rids), E)
+    assert np.array_equal(to_np(moe.route_tables(ws, M, k, E)["offsets"]), off)
+    assert np.all(np.isfinite(to_np(out["y"]).view(np.uint16)[ok] != 0x7fc0))
+
+
 def test_layer_config1_decode_q8():
     """1 token, H 2048, 64 experts, top-8, I 512, Q8 routed experts, no shared expert."""
     say("layer cfg1")
