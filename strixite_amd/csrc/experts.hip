@@ -602,6 +602,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     }
 }
 
+#include "expert_gemm.hpp"
+
 // Per-slot combine (strixite kernels/linear_q4.hip:283-322): y[m, n] = sum_a coef[m, a] * (h[m, a, :] . Wd[id] row n),
 // the slot dots in FP32 from the MFMA (token row 0 of the tile), summed over a in order with fmaf, rounded once.
 // Two 16-row tiles a wave. Any invalid id of the token: NaN row, err.
@@ -855,6 +857,12 @@ void check_grouped(const char *fn, const void *x, const QV &w, int64_t E, const 
 // every tile holds at least one slot, and the tables hold at most S / 16 + E + 2 of them
 int64_t grouped_tiles(int64_t M, int64_t A, int64_t E) { return std::min(M * A, M * A / 16 + E + 2); }
 
+// Prefill-size batches (at least 1024 slots and 8 a bucket on average) take the LDS-tiled GEMM: its 64-slot tiles
+// read an expert's weights a quarter as often as the 16-slot stream tiles and keep the matrix cores busy.
+bool use_expert_gemm(int64_t S, int64_t E, int64_t K, int64_t G) {
+    return S >= 1024 && S >= 8 * E && K % gemm::BK == 0 && G % gemm::BK == 0;
+}
+
 template <typename V>
 void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E, const void *ws, size_t ws_bytes,
                            int64_t M, int64_t A, void *h, Act act, bool h_f16, hipStream_t stream) {
@@ -866,7 +874,15 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
     GemmArgs a = make_args(w, E, x, h, I);
     a.A = A, a.ws = static_cast<const int32_t *>(ws), a.S = M * A;
     const int64_t tiles = grouped_tiles(M, A, E);
-    if (h_f16) launch_bits<GROUPED, EPI_SWIGLU, false, true, true>(w.bits, a, tiles, stream);
+    if (use_expert_gemm(M * A, E, w.K, w.G)) {
+        if (w.bits == 4) {
+            if (h_f16) launch_expert_gemm<4, GROUPED, EPI_SWIGLU, true, true>(a, stream);
+            else launch_expert_gemm<4, GROUPED, EPI_SWIGLU, true, false>(a, stream);
+        } else {
+            if (h_f16) launch_expert_gemm<8, GROUPED, EPI_SWIGLU, true, true>(a, stream);
+            else launch_expert_gemm<8, GROUPED, EPI_SWIGLU, true, false>(a, stream);
+        }
+    } else if (h_f16) launch_bits<GROUPED, EPI_SWIGLU, false, true, true>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_SWIGLU, false, true, false>(w.bits, a, tiles, stream);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E, " N=", N, " K=", w.K, " G=", w.G, h_f16 ? " (F16 h)" : "");
 }
@@ -913,7 +929,10 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
     GemmArgs a = make_args(w, E, h, partial, N);
     a.A = A, a.ws = static_cast<const int32_t *>(ws), a.S = M * A;
     const int64_t tiles = grouped_tiles(M, A, E);
-    if (h_f16) launch_bits<GROUPED, EPI_F32, true, false, false>(w.bits, a, tiles, stream);
+    if (!h_f16 && use_expert_gemm(M * A, E, w.K, w.G)) {  // (the GEMM reads bf16 activations only)
+        if (w.bits == 4) launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
+        else launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
+    } else if (h_f16) launch_bits<GROUPED, EPI_F32, true, false, false>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_F32, false, false, false>(w.bits, a, tiles, stream);
     combine_reduce(partial, ids, coef, M, A, E, N, static_cast<uint16_t *>(y), shared, nullptr, nullptr, stream);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E, " N=", N, " K=", w.K, " G=", w.G,
@@ -1172,10 +1191,15 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         STRIX_HIP_CHECK(hipStreamWaitEvent(ss->s, ss->fork, 0), fn, ": fork wait");
         GemmArgs a = make_args(gv, 1, x, sh_h, I);
         a.M = M;
-        launch_gemm<8, DENSE, EPI_SWIGLU, false, false, false>(a, (M + 15) / 16, ss->s);
         GemmArgs b = make_args(dv, 1, sh_h, sh_s, H);
         b.M = M;
-        launch_gemm<8, DENSE, EPI_BF16, false, false, false>(b, (M + 15) / 16, ss->s);
+        if (M >= 128 && H % gemm::BK == 0 && I % gemm::BK == 0 && gv.G % gemm::BK == 0 && dv.G % gemm::BK == 0) {
+            launch_expert_gemm<8, DENSE, EPI_SWIGLU, false, false>(a, ss->s);
+            launch_expert_gemm<8, DENSE, EPI_BF16, false, false>(b, ss->s);
+        } else {
+            launch_gemm<8, DENSE, EPI_SWIGLU, false, false, false>(a, (M + 15) / 16, ss->s);
+            launch_gemm<8, DENSE, EPI_BF16, false, false, false>(b, (M + 15) / 16, ss->s);
+        }
         STRIX_HIP_CHECK_LAUNCH(fn, " shared expert M=", M);
         STRIX_HIP_CHECK(hipEventRecord(ss->join, ss->s), fn, ": join");
     }
@@ -1209,7 +1233,10 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         check_view(fn, dv, E);
         GemmArgs a = make_args(dv, E, h, partial, H);
         a.A = k, a.ws = static_cast<const int32_t *>(route), a.S = M * k;
-        if (q8) launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream);
+        if (use_expert_gemm(M * k, E, dv.K, dv.G)) {
+            if (q8) launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
+            else launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
+        } else if (q8) launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream);
         else launch_gemm<4, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream);
     }
     if (ss) STRIX_HIP_CHECK(hipStreamWaitEvent(stream, ss->join, 0), fn, ": join wait");
