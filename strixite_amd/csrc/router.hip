@@ -103,6 +103,68 @@ __global__ void __launch_bounds__(kThreads)
             }
 }
 
+// Register-tiled form for larger M (same arithmetic, same bits): a wave computes 8 tokens x 8 output rows, so each
+// loaded chunk feeds 8 fmaf chains; lane l still owns chunks l, l + 64, ... of every pair. The 64 pairs' lane
+// partials then meet in a reduce-scatter along the same butterfly (offsets 32 .. 1): at offset o a lane keeps half of
+// its pairs - the upper half when bit o of its lane is set - and adds the partner's partials of that half, own +
+// partner as in the butterfly. Lane l ends with pair l. A block is 4 waves on the same 8 tokens (32 rows).
+constexpr int kTT = 8, kTE = 8;
+template <typename TY>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+    router_tile_kernel(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int64_t n0 = ((int64_t)blockIdx.x * (kThreads / kWave) + wave) * kTE, m0 = (int64_t)blockIdx.y * kTT;
+    if (n0 >= N) return;  // no barrier in this kernel
+    float v[kTT * kTE];
+#pragma unroll
+    for (int p = 0; p < kTT * kTE; ++p) v[p] = 0.f;
+    const int64_t chunks = K / 8;
+    for (int64_t c = lane; c < chunks; c += kWave) {
+        uint4 wu[kTE];
+#pragma unroll
+        for (int e = 0; e < kTE; ++e)
+            wu[e] = n0 + e < N ? *reinterpret_cast<const uint4 *>(w + (n0 + e) * K + c * 8) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < kTT; ++t) {
+            const uint4 xu = m0 + t < M ? *reinterpret_cast<const uint4 *>(x + (m0 + t) * K + c * 8) : make_uint4(0, 0, 0, 0);
+            const uint32_t xd[4] = {xu.x, xu.y, xu.z, xu.w};
+#pragma unroll
+            for (int e = 0; e < kTE; ++e) {
+                const uint32_t wd[4] = {wu[e].x, wu[e].y, wu[e].z, wu[e].w};
+                float a = v[t * kTE + e];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float xv = __uint_as_float(i % 2 ? xd[i / 2] & 0xffff0000u : xd[i / 2] << 16);
+                    const float wv = __uint_as_float(i % 2 ? wd[i / 2] & 0xffff0000u : wd[i / 2] << 16);
+                    a = fmaf(xv, wv, a);
+                }
+                v[t * kTE + e] = a;
+            }
+        }
+    }
+    // reduce-scatter along the butterfly: n live pairs halve at each offset
+#pragma unroll
+    for (int lvl = 0; lvl < 6; ++lvl) {
+        const int o = kWave / 2 >> lvl, n = kTT * kTE >> lvl;
+        const bool up = lane & o;
+#pragma unroll
+        for (int i = 0; i < n / 2; ++i) {
+            const float send = up ? v[i] : v[n / 2 + i];
+            const float keep = up ? v[n / 2 + i] : v[i];
+            v[i] = keep + __shfl_xor(send, o, kWave);
+        }
+    }
+    constexpr int PL = kTT * kTE / kWave;  // pairs a lane ends with
+#pragma unroll
+    for (int h = 0; h < PL; ++h) {
+        const int p = PL * lane + h, t = p / kTE, e = p % kTE;
+        if (m0 + t < M && n0 + e < N) {
+            if constexpr (std::is_same_v<TY, float>) y[(m0 + t) * N + n0 + e] = v[h];
+            else y[(m0 + t) * N + n0 + e] = f32_to_bf16(v[h]);
+        }
+    }
+}
+
 template <typename TY>
 void launch_router_rows(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K,
                         hipStream_t stream) {
@@ -117,7 +179,13 @@ void launch_router_rows(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, 
         if (vec) router_rows_kernel<TY, MR, true><<<grid, block, 0, stream>>>(x, w, y, M, N, K, TG);
         else router_rows_kernel<TY, MR, false><<<grid, block, 0, stream>>>(x, w, y, M, N, K, TG);
     };
-    if (M == 1) go(std::integral_constant<int, 1>{});
+    if (M >= 256 && vec) {
+        const int64_t by = (M + kTT - 1) / kTT;
+        STRIX_CHECK(by <= 65535, "linear_bf16w: M = ", M, " needs ", by, " token blocks, grid.y holds 65535");
+        const int64_t per_block = kTE * (kThreads / kWave);
+        dim3 grid((unsigned)((N + per_block - 1) / per_block), (unsigned)by), block(kThreads);
+        router_tile_kernel<TY><<<grid, block, 0, stream>>>(x, w, y, M, N, K);
+    } else if (M == 1) go(std::integral_constant<int, 1>{});
     else if (M <= 64) go(std::integral_constant<int, 4>{});
     else go(std::integral_constant<int, 16>{});
 }
