@@ -20,14 +20,15 @@ constexpr int BM = 64, BN = 256, BK = 64;
 constexpr int LDA = BK + 8;  // bf16 per LDS activation row: 144 bytes, so 16 consecutive rows start on distinct bank quads
 constexpr int kThreads = 256;
 constexpr int PF = 2;        // chunks in flight in registers
-constexpr int GW = 8;        // groups a scale window
+constexpr int GW = 8;        // groups a min-term window (two K steps of the tail MFMAs)
+constexpr int kMaxGroups = 48;  // a weight row's scales and mins staged whole in LDS (2 blocks a CU up to 48 groups)
+// u16 per staged row: the groups rounded up to GW, plus 2 - an odd number of dwords, so 16 consecutive rows fall in
+// distinct banks
+__host__ __device__ constexpr int table_stride(int groups) { return (groups + GW - 1) / GW * GW + 2; }
 
 template <int BITS> struct Chunk {
     uint4 a[2];                                   // activation pieces: rows t / 8 and t / 8 + 32, 8 bf16 at (t % 8) * 8
     typename std::conditional<BITS == 4, uint2, uint4>::type q[4];  // the lane's 16 codes of each of its 4 row tiles
-};
-struct Window {  // one weight row's scales and mins for GW groups (raw bf16)
-    uint4 s, m;
 };
 }  // namespace gemm
 
@@ -38,8 +39,9 @@ __global__ void __launch_bounds__(gemm::kThreads) __attribute__((amdgpu_waves_pe
     using namespace gemm;
     constexpr bool SWI = EPI == EPI_SWIGLU;
     __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDA];
-    __shared__ float sc[2][GW][BN], mn[2][GW][BN];  // scale windows (double buffered): scale, m' per group and row
+    extern __shared__ uint16_t stable[];  // raw bf16 scales [BN][stride], then mins [BN][stride]
     __shared__ int32_t orow[BM];
+    __shared__ float xsum[2][GW][BM];  // token sums per group of the last two windows (wave w: tokens 16 w ..)
     const int tid = threadIdx.x, lane = tid % kWave, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int j = lane % 16, g = lane / 16;
 
@@ -94,12 +96,15 @@ __global__ void __launch_bounds__(gemm::kThreads) __attribute__((amdgpu_waves_pe
     for (int u = 0; u < 4; ++u) qoff[u] = wrow_of(brow[u] + j) * (K * BITS / 8) + g * (16 * BITS / 8);
     // the scale row this thread stages into the windows
     const uint32_t srow = wrow_of(tid) * groups;
-    const bool wide = groups % GW == 0;  // 16-byte aligned windows
-
-    auto load = [&](int c, Chunk<BITS> &ch) __attribute__((always_inline)) {
+    const int stride = table_stride((int)groups);
+    uint16_t *tsc = stable, *tmn = stable + BN * stride;
+    auto load_a = [&](int c, Chunk<BITS> &ch) __attribute__((always_inline)) {
         const bool live = c < chunks;
 #pragma unroll
         for (int i = 0; i < 2; ++i) ch.a[i] = bld16(rx, live ? xoff[i] : x_bytes, (uint32_t)c * BK * 2);
+    };
+    auto load_q = [&](int c, Chunk<BITS> &ch) __attribute__((always_inline)) {
+        const bool live = c < chunks;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const uint32_t o = live ? qoff[u] : q_bytes, co = (uint32_t)c * (BK * BITS / 8);
@@ -107,128 +112,148 @@ __global__ void __launch_bounds__(gemm::kThreads) __attribute__((amdgpu_waves_pe
             else ch.q[u] = bld16(rq, o, co);
         }
     };
-    auto load_window = [&](int w, Window &win) __attribute__((always_inline)) {
-        const uint32_t g0 = (uint32_t)w * GW;
-        if (wide) {
-            const uint32_t o = g0 < groups ? (srow + g0) * 2 : s_bytes;
-            win.s = bld16(rs, o, 0);
-            win.m = bld16(rm, o, 0);
-        } else {
-            uint32_t sv[GW], mv[GW];
-#pragma unroll
-            for (int e = 0; e < GW; ++e) {
-                const uint32_t o = g0 + e < groups ? (srow + g0 + e) * 2 : s_bytes;
-                sv[e] = __builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0);
-                mv[e] = __builtin_amdgcn_raw_buffer_load_b16(rm, o, 0, 0);
-            }
-            win.s = make_uint4(sv[0] | sv[1] << 16, sv[2] | sv[3] << 16, sv[4] | sv[5] << 16, sv[6] | sv[7] << 16);
-            win.m = make_uint4(mv[0] | mv[1] << 16, mv[2] | mv[3] << 16, mv[4] | mv[5] << 16, mv[6] | mv[7] << 16);
-        }
-    };
-    auto store_window = [&](int w, const Window &win) __attribute__((always_inline)) {
-        const uint32_t sw[4] = {win.s.x, win.s.y, win.s.z, win.s.w}, mw[4] = {win.m.x, win.m.y, win.m.z, win.m.w};
-#pragma unroll
-        for (int e = 0; e < GW; ++e) {
-            const float s = __uint_as_float(e % 2 ? sw[e / 2] & 0xFFFF0000u : sw[e / 2] << 16);
-            const float m = __uint_as_float(e % 2 ? mw[e / 2] & 0xFFFF0000u : mw[e / 2] << 16);
-            sc[w & 1][e][tid] = s;
-            mn[w & 1][e][tid] = BITS == 4 ? fmaf(-128.0f, s, m) : m;
-        }
-    };
-
-    float4v acc[4][4], d[4][4], dx[4];  // d, dx: the open group's partials
+    // d: the open group's partials; sx: the token sums of tile `wave` over the open group, lane (j, g) holding token
+    // 16 wave + j (all 4 registers alike: the sums come out of an MFMA with the all-ones matrix as A); each wave
+    // publishes its tile's sums in xsum for every wave's min-term tail
+    float4v acc[4][4], d[4][4], sx = float4v{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        dx[i] = float4v{0, 0, 0, 0};
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc[i][u] = d[i][u] = float4v{0, 0, 0, 0};
     }
     const Frag ones{{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}};
-    Window win;
-    load_window(0, win);
-    store_window(0, win);
-    if (groups > GW) load_window(1, win);
+    // the block's scale table: thread t stages weight row t (groups at and past `groups` read as zero)
+    if (groups % GW == 0) {
+        uint32_t *ts = reinterpret_cast<uint32_t *>(tsc + tid * stride), *tm = reinterpret_cast<uint32_t *>(tmn + tid * stride);
+        for (int q = 0; q < (int)groups / GW; ++q) {
+            const uint4 vs = bld16(rs, srow * 2, 16 * q), vm = bld16(rm, srow * 2, 16 * q);
+            ts[4 * q] = vs.x, ts[4 * q + 1] = vs.y, ts[4 * q + 2] = vs.z, ts[4 * q + 3] = vs.w;
+            tm[4 * q] = vm.x, tm[4 * q + 1] = vm.y, tm[4 * q + 2] = vm.z, tm[4 * q + 3] = vm.w;
+        }
+    } else {
+        for (int e = 0; e < (int)groups; ++e) {
+            tsc[tid * stride + e] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (srow + e) * 2, 0, 0);
+            tmn[tid * stride + e] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rm, (srow + e) * 2, 0, 0);
+        }
+    }
+    for (int e = (int)groups; e < stride; ++e) tsc[tid * stride + e] = tmn[tid * stride + e] = 0;
+    for (int e = tid; e < 2 * GW * BM; e += gemm::kThreads) (&xsum[0][0][0])[e] = 0.0f;
+
+    // a window's min terms, sum over its groups of (m - 128 s) * sum(x) (Q8: m * sum(x)), on the matrix cores: each
+    // K step takes 4 groups, lane g's 8 entries one group's, A = [hi, mid, lo, 0] x 2 (the exact bf16 split of the
+    // token's sum), B = [m, m, m, 0, s', s', s', 0] with s' = -128 s exact in bf16 (Q8: 0); each product is exact
+    auto tail = [&](int w) __attribute__((always_inline)) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            Frag ap[4], bp[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float v = xsum[w & 1][4 * st + g][16 * i + j];
+                const float hi = __uint_as_float(__float_as_uint(v) & 0xFFFF0000u), r = v - hi;
+                const float mid = __uint_as_float(__float_as_uint(r) & 0xFFFF0000u), lo = r - mid;
+                const uint32_t d0 = __builtin_amdgcn_perm(__float_as_uint(mid), __float_as_uint(hi), 0x07060302u);
+                const uint32_t d1 = __float_as_uint(lo) >> 16;
+                ap[i] = Frag{{d0, d1, d0, d1}};
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = (brow[u] + j) * stride + GW * w + 4 * st + g;
+                const uint32_t m = tmn[e];
+                uint32_t sp = 0;
+                if constexpr (BITS == 4) sp = __float_as_uint(-128.0f * __uint_as_float((uint32_t)tsc[e] << 16)) >> 16;
+                bp[u] = Frag{{m | m << 16, m, sp | sp << 16, sp}};
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc[i][u] = mfma_bf16(ap[i], bp[u], acc[i][u]);
+        }
+    };
 
     // one chunk: activations -> LDS, prefetch chunk c + PF into the same registers, MFMAs, rescale at a group's end
     auto run = [&](int c, Chunk<BITS> &ch) __attribute__((always_inline)) {
         const int gi = c / cpg;
-        const bool opens = c % cpg == 0, closes = G1 || c % cpg == cpg - 1;
+        const bool closes = G1 || c % cpg == cpg - 1;
         uint16_t *as = As[c & 1];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             *reinterpret_cast<uint4 *>(&as[(tid / 8 + 32 * i) * LDA + (tid % 8) * 8]) = ch.a[i];
-        // the next window goes to LDS mid-window (its buffer's last reader closed GW / 2 groups ago)
-        if (opens && gi % GW == GW / 2 && gi + GW / 2 < (int)groups) {
-            store_window(gi / GW + 1, win);
-            if (gi + GW / 2 + GW < (int)groups) load_window(gi / GW + 2, win);
-        }
-        __syncthreads();  // this chunk's activations (and a stored window) are visible; the previous chunk is read
-        // codes of this chunk -> bf16 B fragments, then the prefetch reuses the registers
-        Frag bq[2][4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if constexpr (BITS == 4) {
-                bq[0][u] = q4_codes_to_bf16(ch.q[u].x);
-                bq[1][u] = q4_codes_to_bf16(ch.q[u].y);
-            } else {
-                bq[0][u] = q8_codes_to_bf16(ch.q[u].x, ch.q[u].y);
-                bq[1][u] = q8_codes_to_bf16(ch.q[u].z, ch.q[u].w);
-            }
-        }
-        load(c + PF, ch);
+        load_a(c + PF, ch);
+        __syncthreads();  // this chunk's activations (and at the first, the scale table) are visible
+        // the previous window's min terms, now that all its token sums are visible
+        if (c % cpg == 0 && gi % GW == 0 && gi > 0 && gi < (int)groups) tail(gi / GW - 1);
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ++ks) {
+            // this K step's codes -> bf16 B fragments; after the last, the prefetch reuses the code registers
+            Frag bq[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if constexpr (BITS == 4) bq[u] = q4_codes_to_bf16(ks == 0 ? ch.q[u].x : ch.q[u].y);
+                else bq[u] = ks == 0 ? q8_codes_to_bf16(ch.q[u].x, ch.q[u].y) : q8_codes_to_bf16(ch.q[u].z, ch.q[u].w);
+            }
+            if (ks == BK / 32 - 1) load_q(c + PF, ch);
             Frag af[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint4 v = *reinterpret_cast<const uint4 *>(&as[(16 * i + j) * LDA + 16 * g + 8 * ks]);
                 af[i] = Frag{{v.x, v.y, v.z, v.w}};
             }
+            const uint4 vw = *reinterpret_cast<const uint4 *>(&as[(16 * wave + j) * LDA + 16 * g + 8 * ks]);
+            const Frag aw{{vw.x, vw.y, vw.z, vw.w}};
             // one chunk a group: its first K step starts the partials from zero (an inline operand, no clearing)
             if (G1 && ks == 0) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) d[i][u] = mfma_bf16(af[i], bq[ks][u], float4v{0, 0, 0, 0});
-                    dx[i] = mfma_bf16(af[i], ones, float4v{0, 0, 0, 0});
-                }
+                    for (int u = 0; u < 4; ++u) d[i][u] = mfma_bf16(af[i], bq[u], float4v{0, 0, 0, 0});
+                sx = mfma_bf16(ones, aw, float4v{0, 0, 0, 0});
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) d[i][u] = mfma_bf16(af[i], bq[ks][u], d[i][u]);
-                    dx[i] = mfma_bf16(af[i], ones, dx[i]);
-                }
+                    for (int u = 0; u < 4; ++u) d[i][u] = mfma_bf16(af[i], bq[u], d[i][u]);
+                sx = mfma_bf16(ones, aw, sx);
             }
         }
         if (closes) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const float s = sc[(gi / GW) & 1][gi % GW][brow[u] + j], m = mn[(gi / GW) & 1][gi % GW][brow[u] + j];
+                const float s = __uint_as_float((uint32_t)tsc[(brow[u] + j) * stride + gi] << 16);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[i][u][r] = fmaf(s, d[i][u][r], fmaf(m, dx[i][r], acc[i][u][r]));
+                    for (int r = 0; r < 4; ++r) acc[i][u][r] = fmaf(s, d[i][u][r], acc[i][u][r]);
             }
+            // this wave's tile of the group's token sums, for the window's tail
+            xsum[(gi / GW) & 1][gi % GW][16 * wave + j] = sx[0];
             if constexpr (!G1) {
+                sx = float4v{0, 0, 0, 0};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    dx[i] = float4v{0, 0, 0, 0};
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int u = 0; u < 4; ++u) d[i][u] = float4v{0, 0, 0, 0};
-                }
             }
+
         }
     };
 
     Chunk<BITS> ch[PF];
+    // in the loop's own order (the scheduler kept out), so entering the loop waits no more than a trip does
 #pragma unroll
-    for (int p = 0; p < PF; ++p) load(p, ch[p]);
+    for (int p = 0; p < PF; ++p) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_a(p, ch[p]);
+        __builtin_amdgcn_sched_barrier(0);
+        load_q(p, ch[p]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // whole trips: a chunk past K loads zeros and adds exactly 0 (its codes meet zero activations, its scales are 0)
     for (int c = 0; c < chunks; c += PF) {
 #pragma unroll
-        for (int p = 0; p < PF; ++p)
-            if (p == 0 || c + p < chunks) run(c + p, ch[p]);
+        for (int p = 0; p < PF; ++p) run(c + p, ch[p]);
     }
+    __syncthreads();
+    tail(((int)groups - 1) / GW);
 
     // epilogue: output rows are the tile's slots (dense: tokens)
 #pragma unroll
@@ -270,7 +295,8 @@ template <int BITS, int MODE, int EPI, bool XROW_DIV, bool HF16>
 void launch_expert_gemm(const GemmArgs &a, hipStream_t stream) {
     using namespace gemm;
     constexpr bool SWI = EPI == EPI_SWIGLU;
-    STRIX_CHECK(a.K % BK == 0 && a.G % BK == 0, "expert gemm: K = ", a.K, " and G = ", a.G, " must be multiples of ", BK);
+    STRIX_CHECK(a.K % BK == 0 && a.G % BK == 0 && a.K / a.G <= kMaxGroups, "expert gemm: K = ", a.K, " and G = ", a.G,
+                " must be multiples of ", BK, " with at most ", kMaxGroups, " groups");
     const int64_t tiles_bound = MODE == GROUPED ? std::min(a.S, a.S / BM + a.E + 2) : (a.M + BM - 1) / BM;
     const int64_t col_blocks = SWI ? (a.N / 2 + BN / 2 - 1) / (BN / 2) : (a.N + BN - 1) / BN;
     const int64_t q_bytes = a.N * a.E * a.K * BITS / 8, s_bytes = a.N * a.E * (a.K / a.G) * 2;
@@ -286,6 +312,7 @@ void launch_expert_gemm(const GemmArgs &a, hipStream_t stream) {
     // a group of one chunk (G == 64, the formats' group size) has its own kernel: no partial clearing
     auto kern = a.G == BK ? expert_gemm_kernel<BITS, MODE, EPI, XROW_DIV, HF16, true>
                           : expert_gemm_kernel<BITS, MODE, EPI, XROW_DIV, HF16, false>;
-    kern<<<(unsigned)blocks, gemm::kThreads, 0, stream>>>(a, tiles_bound, rec64, (uint32_t)q_bytes, (uint32_t)s_bytes,
+    const size_t lds = (size_t)2 * BN * table_stride((int)(a.K / a.G)) * 2;
+    kern<<<(unsigned)blocks, gemm::kThreads, lds, stream>>>(a, tiles_bound, rec64, (uint32_t)q_bytes, (uint32_t)s_bytes,
                                                           (uint32_t)x_bytes, (uint32_t)y_bytes);
 }

@@ -865,7 +865,7 @@ int64_t grouped_tiles(int64_t M, int64_t A, int64_t E) { return std::min(M * A, 
 // Prefill-size batches (at least 1024 slots and 8 a bucket on average) take the LDS-tiled GEMM: its 64-slot tiles
 // read an expert's weights a quarter as often as the 16-slot stream tiles and keep the matrix cores busy.
 bool use_expert_gemm(int64_t S, int64_t E, int64_t K, int64_t G) {
-    return S >= 1024 && S >= 8 * E && K % gemm::BK == 0 && G % gemm::BK == 0;
+    return S >= 1024 && S >= 8 * E && K % gemm::BK == 0 && G % gemm::BK == 0 && K / G <= gemm::kMaxGroups;
 }
 
 template <typename V>
