@@ -6,7 +6,7 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libstrixite_moe.so")
+LIB_PATH = os.environ.get("STRIX_MOE_LIB") or os.path.join(HERE, "libstrixite_moe.so")
 
 _p, _i64, _i32, _u32, _u64, _f32, _int, _sz = (C.c_void_p, C.c_int64, C.c_int32, C.c_uint32, C.c_uint64, C.c_float,
                                                C.c_int, C.c_size_t)

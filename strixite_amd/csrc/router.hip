@@ -191,15 +191,17 @@ void launch_router_rows(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, 
 }
 
 // ---- top-k ----------------------------------------------------------------------------------------------------
-// One wave64 per token (4 a block). Lane l holds experts l, l + 64, ... (NV registers, -inf past E). A round is a
-// 64-lane arg-max over the lanes' bests (larger value, then lower index); the winner lane masks its pick and rescans
-// its registers. Lane r keeps the r-th pick, so the softmax over the k is one butterfly sum.
+// One wave64 per token: a block of 4 waves, or of 1 wave for small batches (the rounds are VALU-bound, so tokens that
+// share a CU share its 4 SIMDs; a decode batch spread one token a CU finishes several times sooner). Lane l holds
+// experts l, l + 64, ... (NV registers, -inf past E). A round is a 64-lane arg-max over the lanes' bests (larger
+// value, then lower index); the winner lane masks its pick and rescans its registers. Lane r keeps the r-th pick, so
+// the softmax over the k is one butterfly sum.
 template <typename T, int NV>
 __global__ void __launch_bounds__(kThreads)
     topk_kernel(const T *logits, int64_t ld, int64_t M, int E, int k, const T *shared, int64_t shared_ld,
                 int32_t shared_id, int32_t *ids, float *coef, int A, uint32_t *err) {
     const int lane = threadIdx.x % kWave;
-    const int64_t m = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+    const int64_t m = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
     if (m >= M) return;  // whole wave; no barrier in this kernel
     int32_t *id_row = ids + m * A;
     float *coef_row = coef + m * A;
@@ -314,7 +316,8 @@ void moe_router(const void *logits, int64_t ld, int64_t M, int64_t E, int64_t k,
     STRIX_CHECK((const void *)ids != (const void *)coef, "moe_router: ids and coef are the same buffer");
     STRIX_CHECK(act == Act::F32 || act == Act::BF16, "moe_router: unsupported logit dtype ", (int)act);
     const int A = (int)k + (shared_logit != nullptr ? 1 : 0);
-    dim3 grid((unsigned)((M + 3) / 4)), block(kThreads);
+    const unsigned per_block = M <= 1024 ? 1 : kThreads / kWave;  // tokens a block
+    dim3 grid((unsigned)((M + per_block - 1) / per_block)), block(per_block * kWave);
     const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
     auto go = [&](auto tag, auto nvc) {
         using T = decltype(tag);

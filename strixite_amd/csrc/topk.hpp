@@ -2,9 +2,9 @@
 // selected logits, ties to the lower expert index), shared by the standalone top-k kernel and the fused small-batch
 // top-k + packing kernel.
 //
-// A round is one wave argmax of (value, index): four DPP steps leave every lane with its 16-lane row's winner
-// (quad swaps, then the half-row and row mirrors), and the four row winners meet through readlane. No LDS round trips,
-// so k rounds cost a few hundred cycles each instead of the microseconds of a shuffle butterfly.
+// A round is one wave max over order-preserving integer keys: four DPP max steps leave every lane with its 16-lane
+// row's maximum (quad swaps, then the half-row and row mirrors), and the four row maxima meet through readlane; a
+// ballot names the lane that holds it. No LDS round trips and no value/index pair compares.
 #pragma once
 
 #include "common.hpp"
@@ -21,74 +21,88 @@ template <> __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t
     return dev::bf16_to_f32(p[i]);
 }
 
-__device__ __forceinline__ bool better(float ov, int oi, float v, int i) { return ov > v || (ov == v && oi < i); }
-
-template <int CTRL> __device__ __forceinline__ void dpp_step(float &v, int &i) {
-    const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-    const int oi = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false);
-    if (better(ov, oi, v, i)) v = ov, i = oi;
+// Order-preserving key of a finite float: larger value <-> larger unsigned key; -0 and +0 share a key (they compare
+// equal, so they tie and the lower index wins); 0 is below every finite value's key and marks a taken expert or the
+// padding past E.
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t b = f == 0.0f ? 0u : __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : b | 0x80000000u;
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? k & 0x7fffffffu : ~k);
 }
 
-// every lane gets the wave's best (value, index)
-__device__ __forceinline__ void wave_argmax(float &v, int &i) {
-    dpp_step<0xB1>(v, i);   // quad_perm [1, 0, 3, 2]
-    dpp_step<0x4E>(v, i);   // quad_perm [2, 3, 0, 1]
-    dpp_step<0x141>(v, i);  // row_half_mirror
-    dpp_step<0x140>(v, i);  // row_mirror
-    float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    int bi = __builtin_amdgcn_readlane(i, 0);
-#pragma unroll
-    for (int r = 1; r < 4; ++r) {
-        const float ov = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * r));
-        const int oi = __builtin_amdgcn_readlane(i, 16 * r);
-        if (better(ov, oi, bv, bi)) bv = ov, bi = oi;
-    }
-    v = bv, i = bi;
+// every lane gets the wave's largest unsigned value: row-local DPP max steps, then the four row results
+template <bool MIN> __device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v) {
+    auto step = [&](uint32_t o) __attribute__((always_inline)) { v = MIN ? (o < v ? o : v) : (o > v ? o : v); };
+    step((uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm [1, 0, 3, 2]
+    step((uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm [2, 3, 0, 1]
+    step((uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    step((uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+    const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    const uint32_t a = MIN ? (r0 < r1 ? r0 : r1) : (r0 > r1 ? r0 : r1);
+    const uint32_t b = MIN ? (r2 < r3 ? r2 : r3) : (r2 > r3 ? r2 : r3);
+    return MIN ? (a < b ? a : b) : (a > b ? a : b);
 }
 
 // Top-k of row[0, E) (E <= 64 NV). Returns the smallest index of a non-finite logit, or INT_MAX; when none, lanes
 // a < k hold the a-th pick (id) and its softmax weight over the k picks (coef).
+// A round: the wave max of the lanes' best keys; the lanes holding it (a ballot) - one, or on an exact tie the one
+// whose best index is lowest; that lane marks its pick taken and rescans its NV keys (ascending, strict: the lowest
+// index among its equal keys).
 template <typename T, int NV>
 __device__ __forceinline__ int wave_topk(const T *row, int E, int k, int &id, float &coef) {
     const int lane = threadIdx.x % kWave;
-    float v[NV];
+    uint32_t key[NV];
+    bool fin = true;
     int bad = INT_MAX;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int e = lane + j * kWave;
-        const float xv = e < E ? load_logit(row, e) : -INFINITY;
-        v[j] = xv;
-        if (e < E && !isfinite(xv) && e < bad) bad = e;
+        const float xv = e < E ? load_logit(row, e) : 0.0f;
+        const bool f = isfinite(xv);
+        if (e < E && !f && e < bad) bad = e;
+        fin = fin && f;
+        key[j] = e < E && f ? order_key(xv) : 0u;
     }
+    if (__ballot(!fin) != 0) {  // rare: the smallest bad index
 #pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off, kWave));
-    if (bad != INT_MAX) return bad;
-    // finite from here: -inf marks a taken expert and the padding past E
-    float lv = -INFINITY;
-    int li = INT_MAX;
+        for (int off = kWave / 2; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off, kWave));
+        return bad;
+    }
+    uint32_t lk = 0;
+    int lj = 0;
     auto lane_best = [&]() __attribute__((always_inline)) {
-        lv = -INFINITY, li = INT_MAX;
+        lk = 0, lj = 0;
 #pragma unroll
         for (int j = 0; j < NV; ++j)
-            if (v[j] > lv) lv = v[j], li = lane + j * kWave;  // ascending scan, strict >: lower index on ties
+            if (key[j] > lk) lk = key[j], lj = j;  // ascending scan, strict >: lower index on ties
     };
     lane_best();
-    float my_v = -INFINITY, top = 0.f;
+    uint32_t my_k = 0, top = 0;
     id = -1;
     for (int r = 0; r < k; ++r) {
-        float bv = lv;
-        int bi = li;
-        wave_argmax(bv, bi);
-        if (r == 0) top = bv;
-        if (lane == r) my_v = bv, id = bi;
-        if (bi == li) {  // the pick is this lane's best (an index lives in one lane only)
+        const uint32_t best = wave_reduce_u32<false>(lk);
+        const uint64_t holders = __ballot(lk == best);
+        int win;
+        if ((holders & (holders - 1)) == 0) {
+            win = __builtin_ctzll(holders);
+        } else {  // several lanes hold the best value: the lowest expert index wins
+            const uint32_t mine = lk == best ? (uint32_t)(lane + lj * kWave) : 0xffffffffu;
+            win = (int)(wave_reduce_u32<true>(mine) % kWave);
+        }
+        const int wj = __builtin_amdgcn_readlane(lj, win);
+        if (r == 0) top = best;
+        if (lane == r) my_k = best, id = win + wj * kWave;
+        if (lane == win) {
 #pragma unroll
             for (int j = 0; j < NV; ++j)
-                if (lane + j * kWave == bi) v[j] = -INFINITY;
+                if (j == wj) key[j] = 0u;
             lane_best();
         }
     }
-    const float ex = lane < k ? expf(my_v - top) : 0.f;
+    const float ex = lane < k ? expf(key_value(my_k) - key_value(top)) : 0.f;
     float sum = ex;
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, kWave);

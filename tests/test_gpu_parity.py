@@ -74,6 +74,10 @@ def test_moe_router_matches_oracle(E, k):
     lg[5, :] = 0.25  # all equal: ids 0..k-1
     lg[6, 3:9] = lg[6, :E].max() + 1  # a tie at the top
     lg[7, : E // 2] = lg[7, E // 2: 2 * (E // 2)]  # pairwise ties everywhere
+    lg[8, :] = 0.0
+    lg[8, 1::2] = -0.0  # -0 and +0 compare equal: the lower index wins
+    lg[9, :] = -1.0
+    lg[9, E - 1] = lg[9, E // 2] = 3.0  # a tie between far-apart experts
     ids, coef, err = moe.moe_router(torch.from_numpy(lg).to(DEV), E, k, ld=E + 3)
     rids, rcoef, rerr = orc.topk(lg, E, k)
     assert np.array_equal(to_np(ids), rids)
