@@ -653,64 +653,126 @@ __global__ void __launch_bounds__(kThreads) perslot_combine_kernel(GemmArgs a, c
     }
 }
 
+constexpr int kSharedParts = 8;  // most K parts of the split-K dense projection
+
+// Dense projection of at most 16 tokens (the shared expert at decode sizes), split over K so that hundreds of waves
+// stream its rows at once: wave (tile, part) computes rows tile * 16 .. + 15 over K steps [part * spp, (part + 1) *
+// spp) for all tokens and writes its FP32 sums to part[part][m][n]; dense_parts_finish adds the parts in order.
+template <int BITS>
+__global__ void __launch_bounds__(kThreads) dense_parts_kernel(GemmArgs a, int spp, int parts, float *part) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int g = lane / 16, j = lane % 16;
+    const int64_t w = (int64_t)blockIdx.x * kWaves + wave, tiles = a.N / 16;
+    if (w >= tiles * parts) return;  // no barrier in this kernel
+    const int64_t tile = w / parts, pt = w % parts;
+    const int64_t spans = a.K / QFmt<BITS>::SPAN, s0 = pt * spp, s1 = s0 + spp < spans ? s0 + spp : spans;
+    const int64_t tile_row[1] = {tile * 16};
+    float4v acc[1];
+    wave_gemm<BITS, 1, false>(a, j < a.M ? a.x + j * a.K : nullptr, tile_row, s0, s1, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (4 * g + r < a.M) part[(pt * a.M + 4 * g + r) * a.N + tile * 16 + j] = acc[0][r];
+}
+
+// SWI: h[m, c] = bf16(silu(g) * u) with g, u the in-order sums of the parts of rows c and I + c (I = N / 2); otherwise
+// y[m, n] = bf16(sum). One thread an output.
+template <bool SWI>
+__global__ void __launch_bounds__(kThreads) dense_parts_finish(const float *part, int parts, int64_t M, int64_t N,
+                                                               uint16_t *y) {
+    const int64_t no = SWI ? N / 2 : N, i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= M * no) return;
+    const int64_t m = i / no, c = i % no;
+    float g[kSharedParts], u[kSharedParts];
+#pragma unroll
+    for (int p = 0; p < kSharedParts; ++p)
+        if (p < parts) {
+            g[p] = part[(p * M + m) * N + c];
+            if constexpr (SWI) u[p] = part[(p * M + m) * N + no + c];
+        }
+    float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+    for (int p = 0; p < kSharedParts; ++p)
+        if (p < parts) {
+            v0 += g[p];
+            if constexpr (SWI) v1 += u[p];
+        }
+    y[m * no + c] = f32_to_bf16(SWI ? silu(v0) * v1 : v0);
+}
+
 // y[m, n] = sum_a coef[m, a] * partial[m * A + a, n] in slot order (fmaf), rounded once; NaN for a token with an
 // invalid id. SH: y = stored(sum) + sigmoid(gl) * s (strixite kernels/moe_grouped.hip:948-985). RES: x_out = stored(x + y).
-// 8 columns a thread (N % 8 == 0).
+// 4 columns a thread (N % 4 == 0); every slot's partials are loaded before the ordered sum, so a thread costs one
+// round trip (the kernel is latency-bound at decode sizes).
 template <bool SH, bool RES>
 __global__ void __launch_bounds__(kThreads)
     combine_reduce_kernel(const float *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                           int64_t N, uint16_t *y, const uint16_t *s, const float *gate_logit, int64_t gate_ld,
                           uint32_t gate_index, uint32_t *err, const uint16_t *resid, uint16_t *out) {
-    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 8;
+    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
     if (i >= M * N) return;
     const int64_t m = i / N, n = i % N;
+    // the loads that do not depend on the sum go out with the partials' (one round trip for the thread)
+    float gl = 0.f;
+    uint2 su = make_uint2(0, 0), xu = make_uint2(0, 0);
+    if constexpr (SH) gl = gate_logit[m * gate_ld], su = *reinterpret_cast<const uint2 *>(s + i);
+    if constexpr (RES) xu = *reinterpret_cast<const uint2 *>(resid + i);
     bool ok = true;
-    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int64_t s_ = 0; s_ < A; ++s_) {
-        const int32_t id = ids[m * A + s_];
-        ok = ok && id >= 0 && id < E;
-        const float c = coef[m * A + s_];
-        const float4 p0 = *reinterpret_cast<const float4 *>(partial + (m * A + s_) * N + n);
-        const float4 p1 = *reinterpret_cast<const float4 *>(partial + (m * A + s_) * N + n + 4);
-        const float p[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    float v[4] = {0, 0, 0, 0};
+    constexpr int B = 16;  // slots whose loads are in flight together
+    for (int64_t a0 = 0; a0 < A; a0 += B) {
+        float4 p[B];
+        float c[B];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = fmaf(c, p[k], v[k]);
+        for (int b = 0; b < B; ++b) {
+            const int64_t a = a0 + b;
+            if (a < A) {
+                p[b] = *reinterpret_cast<const float4 *>(partial + (m * A + a) * N + n);
+                c[b] = coef[m * A + a];
+                const int32_t id = ids[m * A + a];
+                ok = ok && id >= 0 && id < E;
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            if (a0 + b >= A) break;
+            v[0] = fmaf(c[b], p[b].x, v[0]);
+            v[1] = fmaf(c[b], p[b].y, v[1]);
+            v[2] = fmaf(c[b], p[b].z, v[2]);
+            v[3] = fmaf(c[b], p[b].w, v[3]);
+        }
     }
     if (!ok)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = qnan();
+        for (int k = 0; k < 4; ++k) v[k] = qnan();
     if constexpr (SH) {
-        const float gl = gate_logit[m * gate_ld];
         const bool gok = isfinite(gl);
         if (!gok && n == 0 && atomicCAS(&err[0], 0u, 1u) == 0u) {
             err[1] = (uint32_t)m;
             err[2] = gate_index;
         }
         const float gv = gok ? 1.f / (1.f + expf(-gl)) : qnan();
-        const uint4 su = *reinterpret_cast<const uint4 *>(s + i);
-        const uint32_t sw[4] = {su.x, su.y, su.z, su.w};
+        const uint32_t sw[2] = {su.x, su.y};
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < 4; ++k) {
             const float sv = __uint_as_float(k % 2 ? sw[k / 2] & 0xffff0000u : sw[k / 2] << 16);
             const float tv = gv * sv;
             v[k] = bf16_round(v[k]) + tv;
         }
     }
-    uint32_t yw[4];
+    uint32_t yw[2];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) yw[k] = (uint32_t)f32_to_bf16(v[2 * k]) | ((uint32_t)f32_to_bf16(v[2 * k + 1]) << 16);
-    *reinterpret_cast<uint4 *>(y + i) = make_uint4(yw[0], yw[1], yw[2], yw[3]);
+    for (int k = 0; k < 2; ++k) yw[k] = (uint32_t)f32_to_bf16(v[2 * k]) | ((uint32_t)f32_to_bf16(v[2 * k + 1]) << 16);
+    *reinterpret_cast<uint2 *>(y + i) = make_uint2(yw[0], yw[1]);
     if constexpr (RES) {
-        const uint4 xu = *reinterpret_cast<const uint4 *>(resid + i);
-        const uint32_t xw[4] = {xu.x, xu.y, xu.z, xu.w};
-        uint32_t ow[4];
+        const uint32_t xw[2] = {xu.x, xu.y};
+        uint32_t ow[2];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < 2; ++k) {
             const float a0 = __uint_as_float(xw[k] << 16) + __uint_as_float(yw[k] << 16);
             const float a1 = __uint_as_float(xw[k] & 0xffff0000u) + __uint_as_float(yw[k] & 0xffff0000u);
             ow[k] = (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
         }
-        *reinterpret_cast<uint4 *>(out + i) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        *reinterpret_cast<uint2 *>(out + i) = make_uint2(ow[0], ow[1]);
     }
 }
 
@@ -895,7 +957,7 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
 void combine_reduce(const float *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                     int64_t N, uint16_t *y, const MoeSharedAdd *sh, const uint16_t *resid, uint16_t *out,
                     hipStream_t stream) {
-    const unsigned blocks = (unsigned)((M * N / 8 + kThreads - 1) / kThreads);
+    const unsigned blocks = (unsigned)((M * N / 4 + kThreads - 1) / kThreads);
     const uint16_t *s = sh ? static_cast<const uint16_t *>(sh->s) : nullptr;
     const float *gl = sh ? sh->gate_logit : nullptr;
     const int64_t gld = sh ? sh->gate_ld : 0;
@@ -1101,7 +1163,7 @@ namespace strix {
 
 namespace {
 struct LayerWs {
-    int64_t logits, ids, coef, route, h, partial, sh_h, sh_s, total;
+    int64_t logits, ids, coef, route, h, partial, sh_h, sh_s, sh_part, total;
     size_t route_bytes;
 };
 int64_t al(int64_t b) { return (b + 255) / 256 * 256; }
@@ -1118,6 +1180,8 @@ LayerWs layer_ws(const MoeLayerWeights &w, int64_t M) {
     L.partial = o, o += al(M * k * H * 4);
     L.sh_h = o, o += al(w.has_shared ? M * I * 2 : 0);
     L.sh_s = o, o += al(w.has_shared ? M * H * 2 : 0);
+    // the split-K parts of the shared expert's projections at M <= 16 (gate_up, then down, in the same space)
+    L.sh_part = o, o += al(w.has_shared && M <= 16 ? kernels::kSharedParts * M * std::max(2 * I, H) * 4 : 0);
     L.total = o;
     return L;
 }
@@ -1201,6 +1265,27 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         if (M >= 128 && H % gemm::BK == 0 && I % gemm::BK == 0 && gv.G % gemm::BK == 0 && dv.G % gemm::BK == 0) {
             launch_expert_gemm<8, DENSE, EPI_SWIGLU, false, false>(a, ss->s);
             launch_expert_gemm<8, DENSE, EPI_BF16, false, false>(b, ss->s);
+        } else if (M <= 16) {
+            // split over K: each projection is a few MB streamed by hundreds of waves, then an in-order sum of parts
+            float *part = reinterpret_cast<float *>(base + L.sh_part);
+            auto split = [&](const GemmArgs &g, bool swi, uint16_t *out) {
+                const int64_t spans = g.K / QFmt<8>::SPAN;
+                // parts of at least 4 steps, at most kSharedParts
+                const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(kSharedParts, spans / 4));
+                const int spp = (int)((spans + parts - 1) / parts);
+                const int64_t waves = g.N / 16 * parts;
+                dense_parts_kernel<8><<<(unsigned)((waves + kWaves - 1) / kWaves), kThreads, 0, ss->s>>>(g, spp, parts,
+                                                                                                        part);
+                const int64_t outs = M * (swi ? g.N / 2 : g.N);
+                if (swi)
+                    dense_parts_finish<true><<<(unsigned)((outs + kThreads - 1) / kThreads), kThreads, 0, ss->s>>>(
+                        part, parts, M, g.N, out);
+                else
+                    dense_parts_finish<false><<<(unsigned)((outs + kThreads - 1) / kThreads), kThreads, 0, ss->s>>>(
+                        part, parts, M, g.N, out);
+            };
+            split(a, true, sh_h);
+            split(b, false, sh_s);
         } else {
             launch_gemm<8, DENSE, EPI_SWIGLU, false, false, false>(a, (M + 15) / 16, ss->s);
             launch_gemm<8, DENSE, EPI_BF16, false, false, false>(b, (M + 15) / 16, ss->s);

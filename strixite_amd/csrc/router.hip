@@ -55,37 +55,40 @@ __global__ void __launch_bounds__(kThreads)
                                    e[6] | (uint32_t)e[7] << 16);
             }
         }
+        // every token row's chunks are loaded before any arithmetic (rows past M re-read the last row, unused), so a
+        // batch costs one memory round trip, not one per token
+        uint4 xu[MR][NB];
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
-            if (r < rows) {
-                const uint16_t *xr = x + (m0 + r) * K;
-                uint4 xu[NB];
+            const uint16_t *xr = x + (m0 + (r < rows ? r : rows - 1)) * K;
 #pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const int64_t c = cb + (int64_t)b * kWave;
-                    if constexpr (VEC) {
-                        xu[b] = c < chunks ? *reinterpret_cast<const uint4 *>(xr + c * 8) : make_uint4(0, 0, 0, 0);
-                    } else {
-                        uint16_t e[8];
+            for (int b = 0; b < NB; ++b) {
+                const int64_t c = cb + (int64_t)b * kWave;
+                if constexpr (VEC) {
+                    xu[r][b] = c < chunks ? *reinterpret_cast<const uint4 *>(xr + c * 8) : make_uint4(0, 0, 0, 0);
+                } else {
+                    uint16_t e[8];
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) e[i] = c * 8 + i < K ? xr[c * 8 + i] : 0;
-                        xu[b] = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
-                                           e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
-                    }
+                    for (int i = 0; i < 8; ++i) e[i] = c * 8 + i < K ? xr[c * 8 + i] : 0;
+                    xu[r][b] = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                                          e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
                 }
+            }
+        }
 #pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const int64_t c = cb + (int64_t)b * kWave;
-                    if (c >= chunks) break;
-                    const uint32_t wd[4] = {wu[b].x, wu[b].y, wu[b].z, wu[b].w};
-                    const uint32_t xd[4] = {xu[b].x, xu[b].y, xu[b].z, xu[b].w};
+        for (int r = 0; r < MR; ++r) {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        if (!VEC && c * 8 + i >= K) break;
-                        const float xv = __uint_as_float(i % 2 ? xd[i / 2] & 0xffff0000u : xd[i / 2] << 16);
-                        const float wv = __uint_as_float(i % 2 ? wd[i / 2] & 0xffff0000u : wd[i / 2] << 16);
-                        acc[r] = fmaf(xv, wv, acc[r]);
-                    }
+            for (int b = 0; b < NB; ++b) {
+                const int64_t c = cb + (int64_t)b * kWave;
+                if (c >= chunks) break;
+                const uint32_t wd[4] = {wu[b].x, wu[b].y, wu[b].z, wu[b].w};
+                const uint32_t xd[4] = {xu[r][b].x, xu[r][b].y, xu[r][b].z, xu[r][b].w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if (!VEC && c * 8 + i >= K) break;
+                    const float xv = __uint_as_float(i % 2 ? xd[i / 2] & 0xffff0000u : xd[i / 2] << 16);
+                    const float wv = __uint_as_float(i % 2 ? wd[i / 2] & 0xffff0000u : wd[i / 2] << 16);
+                    acc[r] = fmaf(xv, wv, acc[r]);
                 }
             }
         }
@@ -165,6 +168,76 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     }
 }
 
+// Small batches (M <= 64): a wave computes TT tokens x TE rows with all of its loads issued at once (NCH chunks a
+// lane: K = 8 * 64 * NCH), so a wave costs one memory round trip. The TT * TE lane partials meet in the reduce-scatter
+// of router_tile_kernel: bit-identical to the canonical order.
+template <typename TY, int TT, int TE, int NCH>
+__global__ void __launch_bounds__(kThreads)
+    router_small_kernel(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K) {
+    constexpr int P = TT * TE;
+    static_assert(P <= kWave && (P & (P - 1)) == 0, "pairs: a power of two, at most a wave");
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int64_t n0 = ((int64_t)blockIdx.x * (kThreads / kWave) + wave) * TE, m0 = (int64_t)blockIdx.y * TT;
+    if (n0 >= N) return;  // no barrier in this kernel
+    uint4 wu[NCH][TE], xu[NCH][TT];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const int64_t c = lane + (int64_t)i * kWave;
+#pragma unroll
+        for (int e = 0; e < TE; ++e)
+            wu[i][e] = *reinterpret_cast<const uint4 *>(w + (n0 + e < N ? n0 + e : N - 1) * K + c * 8);
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+            xu[i][t] = *reinterpret_cast<const uint4 *>(x + (m0 + t < M ? m0 + t : M - 1) * K + c * 8);
+    }
+    float v[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) v[p] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const uint32_t xd[4] = {xu[i][t].x, xu[i][t].y, xu[i][t].z, xu[i][t].w};
+#pragma unroll
+            for (int e = 0; e < TE; ++e) {
+                const uint32_t wd[4] = {wu[i][e].x, wu[i][e].y, wu[i][e].z, wu[i][e].w};
+                float a = v[t * TE + e];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float xv = __uint_as_float(k % 2 ? xd[k / 2] & 0xffff0000u : xd[k / 2] << 16);
+                    const float wv = __uint_as_float(k % 2 ? wd[k / 2] & 0xffff0000u : wd[k / 2] << 16);
+                    a = fmaf(xv, wv, a);
+                }
+                v[t * TE + e] = a;
+            }
+        }
+    // reduce-scatter along the butterfly while pairs remain, then a plain butterfly; lane l ends with pair
+    // (l / (64 / P)) (every lane of its group holds the same sum)
+#pragma unroll
+    for (int lvl = 0; lvl < 6; ++lvl) {
+        const int o = kWave / 2 >> lvl, n = P >> lvl;
+        if (n > 1) {
+            const bool up = lane & o;
+#pragma unroll
+            for (int i = 0; i < n / 2; ++i) {
+                const float send = up ? v[i] : v[n / 2 + i];
+                const float keep = up ? v[n / 2 + i] : v[i];
+                v[i] = keep + __shfl_xor(send, o, kWave);
+            }
+        } else {
+            v[0] = v[0] + __shfl_xor(v[0], o, kWave);
+        }
+    }
+    constexpr int G = kWave / P;  // lanes holding one pair
+    if (lane % G == 0) {
+        const int p = lane / G, t = p / TE, e = p % TE;
+        if (m0 + t < M && n0 + e < N) {
+            if constexpr (std::is_same_v<TY, float>) y[(m0 + t) * N + n0 + e] = v[0];
+            else y[(m0 + t) * N + n0 + e] = f32_to_bf16(v[0]);
+        }
+    }
+}
+
 template <typename TY>
 void launch_router_rows(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K,
                         hipStream_t stream) {
@@ -179,15 +252,23 @@ void launch_router_rows(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, 
         if (vec) router_rows_kernel<TY, MR, true><<<grid, block, 0, stream>>>(x, w, y, M, N, K, TG);
         else router_rows_kernel<TY, MR, false><<<grid, block, 0, stream>>>(x, w, y, M, N, K, TG);
     };
-    if (M >= 256 && vec) {
+    if (M <= 64 && vec && K % 512 == 0 && (K / 512 == 4 || K / 512 == 6 || K / 512 == 8)) {
+        // 4 tokens x 1 row a wave (one row a wave keeps enough waves in flight; measured on MI355X at M 16, N 513,
+        // K 3072: 4 x 1 5.1 us, 4 x 2 6.0, 4 x 4 8.9, the per-row form with loads in order 8.3)
+        constexpr int TT = 4, TE = 1;
+        const int64_t per_block = TE * (kThreads / kWave);
+        dim3 grid((unsigned)((N + per_block - 1) / per_block), (unsigned)((M + TT - 1) / TT)), block(kThreads);
+        if (K / 512 == 4) router_small_kernel<TY, TT, TE, 4><<<grid, block, 0, stream>>>(x, w, y, M, N, K);
+        else if (K / 512 == 6) router_small_kernel<TY, TT, TE, 6><<<grid, block, 0, stream>>>(x, w, y, M, N, K);
+        else router_small_kernel<TY, TT, TE, 8><<<grid, block, 0, stream>>>(x, w, y, M, N, K);
+    } else if (M >= 256 && vec) {
         const int64_t by = (M + kTT - 1) / kTT;
         STRIX_CHECK(by <= 65535, "linear_bf16w: M = ", M, " needs ", by, " token blocks, grid.y holds 65535");
         const int64_t per_block = kTE * (kThreads / kWave);
         dim3 grid((unsigned)((N + per_block - 1) / per_block), (unsigned)by), block(kThreads);
         router_tile_kernel<TY><<<grid, block, 0, stream>>>(x, w, y, M, N, K);
     } else if (M == 1) go(std::integral_constant<int, 1>{});
-    else if (M <= 64) go(std::integral_constant<int, 4>{});
-    else go(std::integral_constant<int, 16>{});
+    else go(std::integral_constant<int, 4>{});  // a wave holds its 4 tokens' chunks in registers
 }
 
 // ---- top-k ----------------------------------------------------------------------------------------------------

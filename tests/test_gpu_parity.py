@@ -53,7 +53,7 @@ def test_synth_matches_host_generator():
 
 # ---- router -----------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("M,N,K", [(1, 65, 2048), (16, 513, 3072), (5, 7, 1000), (37, 129, 512), (300, 513, 3072),
-                                   (257, 70, 512)])
+                                   (257, 70, 512), (7, 30, 4096), (64, 513, 2048), (3, 17, 3072)])
 def test_linear_bf16w_bit_exact(M, N, K):
     say("linear_bf16w", M, N, K)
     x = orc.gen_bf16_normal(orc.tensor_key(1, "x"), 1.0, (M, K))
