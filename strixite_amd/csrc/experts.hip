@@ -1163,7 +1163,7 @@ namespace strix {
 
 namespace {
 struct LayerWs {
-    int64_t logits, ids, coef, route, h, partial, sh_h, sh_s, sh_part, total;
+    int64_t logits, norms, ids, coef, route, h, partial, sh_h, sh_s, sh_part, total;
     size_t route_bytes;
 };
 int64_t al(int64_t b) { return (b + 255) / 256 * 256; }
@@ -1172,6 +1172,7 @@ LayerWs layer_ws(const MoeLayerWeights &w, int64_t M) {
     const int64_t E = w.E, k = w.k, H = w.H, I = w.I, ld = E + (w.has_shared ? 1 : 0);
     int64_t o = 0;
     L.logits = o, o += al(M * ld * 4);
+    L.norms = o, o += al((M + ld) * 4);  // the prefill router's row norms
     L.ids = o, o += al(M * k * 4);
     L.coef = o, o += al(M * k * 4);
     L.route_bytes = kernels::moe_route_workspace_bytes(M, k, E);
@@ -1296,16 +1297,26 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
 
     // router projection (+ harness bias) and top-k
     const float *lg = logits_in;
+    bool routed = false;  // ids and coef already written (the prefill router selects as it projects)
     if (!lg) {
-        linear_bf16w(x, w.router, logits, M, ld, H, Act::BF16, Act::F32, stream);
-        if (w.router_bias) {
-            const int64_t b = (M * E + 255) / 256;
-            add_bias_kernel<<<(unsigned)(b < 65536 ? b : 65536), 256, 0, stream>>>(logits, ld, M, E, w.router_bias);
-            STRIX_HIP_CHECK_LAUNCH(fn, " router bias");
-        }
         lg = logits;
+        // prefill sizes: bf16 MFMA projection + exact recomputation of the candidates (the same routing bits)
+        routed = M >= 256 && moe_router_prefill(x, w.router, w.router_bias, M, H, E, k, w.has_shared, logits,
+                                                reinterpret_cast<float *>(base + L.norms), ids, coef, err_router,
+                                                stream);
+        if (!routed) {
+            linear_bf16w(x, w.router, logits, M, ld, H, Act::BF16, Act::F32, stream);
+            if (w.router_bias) {
+                const int64_t b = (M * E + 255) / 256;
+                add_bias_kernel<<<(unsigned)(b < 65536 ? b : 65536), 256, 0, stream>>>(logits, ld, M, E,
+                                                                                       w.router_bias);
+                STRIX_HIP_CHECK_LAUNCH(fn, " router bias");
+            }
+        }
     }
-    if (M * k <= 1024) {  // one launch: top-k and packing with the ids kept in LDS
+    if (routed) {
+        moe_group_routes(ids, M, k, E, route, L.route_bytes, err_expert, stream);
+    } else if (M * k <= 1024) {  // one launch: top-k and packing with the ids kept in LDS
         moe_topk_group_routes_small(lg, ld, M, E, k, ids, coef, route, L.route_bytes, err_router, err_expert, stream);
     } else {
         moe_router(lg, ld, M, E, k, nullptr, 0, 0, ids, coef, Act::F32, err_router, stream);

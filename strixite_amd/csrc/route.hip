@@ -239,19 +239,33 @@ __global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, La
     int fb = INT_MAX;
     for (int64_t c = t; c < L.nch; c += blockDim.x) fb = min(fb, ws[L.bad() + c]);
     if (fb != INT_MAX) atomicMin(&bad_lds, fb);
+    // the chunk histograms are read 16 at a time (independent loads in flight together: a round trip per 16 chunks
+    // instead of one per chunk)
+    constexpr int B = 16;
     int cnt = 0;
     if (t <= E)
-        for (int64_t c = 0; c < L.nch; ++c) cnt += ws[L.hist() + c * (E + 1) + t];
+        for (int64_t c0 = 0; c0 < L.nch; c0 += B) {
+            int h[B];
+#pragma unroll
+            for (int b = 0; b < B; ++b) h[b] = c0 + b < L.nch ? ws[L.hist() + (c0 + b) * (E + 1) + t] : 0;
+#pragma unroll
+            for (int b = 0; b < B; ++b) cnt += h[b];
+        }
     int v[3] = {cnt, (cnt + kTileRows - 1) / kTileRows, (cnt + kWideRows - 1) / kWideRows}, tot[3];
     block_scan3(v, wsum, tot);
     if (t <= E) {
         write_bucket(t, cnt, v, ws, L);
         int run = v[0];
-        for (int64_t c = 0; c < L.nch; ++c) {
-            int32_t *p = ws + L.hist() + c * (E + 1) + t;
-            const int k = *p;
-            *p = run;
-            run += k;
+        for (int64_t c0 = 0; c0 < L.nch; c0 += B) {
+            int h[B];
+#pragma unroll
+            for (int b = 0; b < B; ++b) h[b] = c0 + b < L.nch ? ws[L.hist() + (c0 + b) * (E + 1) + t] : 0;
+#pragma unroll
+            for (int b = 0; b < B; ++b)
+                if (c0 + b < L.nch) {
+                    ws[L.hist() + (c0 + b) * (E + 1) + t] = run;
+                    run += h[b];
+                }
         }
     }
     if (t == 0) {

@@ -1,0 +1,342 @@
+// Prefill-size routing on gfx950's matrix cores with the routing of the canonical FP32 order, bit for bit.
+//
+// The router projection (strixite kernels/linear.hip:83-147 semantics, FP32) is the one place on the path whose result
+// decides a discrete choice (the top-k), so it must be reproduced exactly - in this library's canonical summation
+// order (lane l of a wave64 takes the 8-element chunks l, l + 64, ... with fmaf, then a butterfly over the 64 lanes;
+// oracle: orc_router_logits). That order does not map onto MFMA, and at 4096 tokens x 513 rows x 3072 the VALU form
+// costs ~0.3 ms. So the projection runs in two passes:
+//   1. approx: logits a = x . w^T with bf16 MFMA (FP32 accumulation, any internal order), and the 2-norms |x_m|,
+//      |w_e|. For ANY order of summing the K exact bf16 x bf16 products in FP32 - rounded to nearest or toward zero,
+//      FP32 denormals kept or flushed - the result differs from the exact sum by at most (2K u) S + K 2^-125 with
+//      u = 2^-24 and S = sum_k |x_k w_k| <= |x| |w| (Cauchy-Schwarz). Both the canonical and the MFMA sums obey it, so
+//      |a - c| <= delta = (4K + 64) u |x| |w| + K 2^-124 (norms rounded up).
+//   2. select (a wave per token): with the (optional FP32) bias, a value v = fl(c + b) lies within delta' = delta +
+//      2^-22 (|a| + |b|) of fl(a + b). tau = the k-th largest of (fl(a + b) - delta'); an expert with fl(a + b) +
+//      delta' < tau has at least k experts whose exact value is larger, so it is never chosen, ties included. The
+//      others (the candidates, typically k + 1 or 2) and the shared-expert gate row are recomputed in the canonical
+//      order; the top-k over the candidates' exact values (value desc, index asc) and the softmax over the picks are
+//      then exactly those of the full exact row. Any non-finite a, b, or norm sends the token to the exact path for
+//      all of its experts (the non-finite handling of strixite kernels/moe_router.hip:40-67).
+// The logits workspace row of a token ends with exact values at the candidates and the shared gate (the entries the
+// layer reads later) and approximate values elsewhere.
+#include "common.hpp"
+#include "topk.hpp"
+
+#include <climits>
+
+namespace strix::kernels {
+namespace {
+
+using namespace strix::dev;
+constexpr int kWave = 64, kThreads = 256;
+
+// ---- pass 1: approximate logits + norms -----------------------------------------------------------------------------
+// Block tile 128 tokens x 64 rows, K in steps of 64 through LDS (rows padded to 144 bytes: the 16 lanes of a
+// fragment read hit 16 distinct 16-byte bank groups). Wave w computes tokens 32 w .. 32 w + 31 of the tile x all 64
+// rows: 2 x 4 tiles of v_mfma_f32_16x16x32_bf16 whose A and B fragments are both 16-byte row segments (x rows for
+// tokens, w rows for experts). The next K step's tiles are loaded into registers while the current one is multiplied.
+constexpr int kBM = 128, kBN = 64, kBK = 64, kLd = kBK + 8;
+
+__device__ __forceinline__ float sumsq8(const uint4 &v) {
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = __uint_as_float(d[i] << 16), b = __uint_as_float(d[i] & 0xffff0000u);
+        s = fmaf(a, a, s);
+        s = fmaf(b, b, s);
+    }
+    return s;
+}
+
+__global__ void __launch_bounds__(kThreads)
+    router_approx_kernel(const uint16_t *x, const uint16_t *w, float *a_out, int64_t ld, int64_t M, int64_t N,
+                         int64_t K, float *nx, float *nw) {
+    __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLd], Bs[kBN * kLd];
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave, g = lane / 16, j = lane % 16;
+    const int64_t n0 = (int64_t)blockIdx.x * kBN, m0 = (int64_t)blockIdx.y * kBM;
+    // staging: A chunk u covers row (t >> 3) + 32 u, 16 bytes at column 8 (t & 7); B chunk u row (t >> 3) + 32 u
+    const int sr = t >> 3, sc = (t & 7) * 8;
+    uint4 ra[4], rb[2];
+    float qa[4] = {0, 0, 0, 0}, qb[2] = {0, 0};
+    auto load = [&](int64_t k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t r = m0 + sr + 32 * u;
+            ra[u] = r < M ? *reinterpret_cast<const uint4 *>(x + r * K + k0 + sc) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t r = n0 + sr + 32 * u;
+            rb[u] = r < N ? *reinterpret_cast<const uint4 *>(w + r * K + k0 + sc) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    float4v acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = float4v{0, 0, 0, 0};
+    load(0);
+    for (int64_t k0 = 0; k0 < K; k0 += kBK) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            *reinterpret_cast<uint4 *>(&As[(sr + 32 * u) * kLd + sc]) = ra[u];
+            qa[u] += sumsq8(ra[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            *reinterpret_cast<uint4 *>(&Bs[(sr + 32 * u) * kLd + sc]) = rb[u];
+            qb[u] += sumsq8(rb[u]);
+        }
+        __syncthreads();
+        if (k0 + kBK < K) load(k0 + kBK);
+#pragma unroll
+        for (int s = 0; s < kBK / 32; ++s) {
+            Frag af[2], bf[4];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(&As[(32 * wave + 16 * a + j) * kLd + 32 * s + 8 * g]);
+                af[a] = Frag{{v.x, v.y, v.z, v.w}};
+            }
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(&Bs[(16 * b + j) * kLd + 32 * s + 8 * g]);
+                bf[b] = Frag{{v.x, v.y, v.z, v.w}};
+            }
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) acc[a][b] = mfma_bf16(af[a], bf[b], acc[a][b]);
+        }
+        __syncthreads();
+    }
+    // D: lane (j, g) holds tokens 4 g + r of column j
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = m0 + 32 * wave + 16 * a + 4 * g + r, n = n0 + 16 * b + j;
+                if (m < M && n < N) a_out[m * ld + n] = acc[a][b][r];
+            }
+    // norms: the 8 threads staging a row meet; rounded up (relative error of the FP32 sums < 2^-10 for K <= 2^13)
+    constexpr float up = 1.0f + 1.0f / 256;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        float q = qa[u];
+        q += __shfl_xor(q, 1, kWave);
+        q += __shfl_xor(q, 2, kWave);
+        q += __shfl_xor(q, 4, kWave);
+        const int64_t r = m0 + sr + 32 * u;
+        if (blockIdx.x == 0 && (t & 7) == 0 && r < M) nx[r] = sqrtf(q) * up;
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        float q = qb[u];
+        q += __shfl_xor(q, 1, kWave);
+        q += __shfl_xor(q, 2, kWave);
+        q += __shfl_xor(q, 4, kWave);
+        const int64_t r = n0 + sr + 32 * u;
+        if (blockIdx.y == 0 && (t & 7) == 0 && r < N) nw[r] = sqrtf(q) * up;
+    }
+}
+
+// ---- pass 2: select -------------------------------------------------------------------------------------------------
+// The canonical dot of token row xr (this lane's NCH chunks, preloaded) with weight row wr: lane l's fmaf chain over
+// chunks l, l + 64, ... (element order), then the butterfly; every lane gets the sum.
+template <int NCH>
+__device__ __forceinline__ float canonical_dot(const uint4 (&xr)[NCH], const uint16_t *wr) {
+    const int lane = threadIdx.x % kWave;
+    uint4 wc[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) wc[i] = *reinterpret_cast<const uint4 *>(wr + (lane + i * kWave) * 8);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const uint32_t xd[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w}, wd[4] = {wc[i].x, wc[i].y, wc[i].z, wc[i].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float xv = __uint_as_float(e % 2 ? xd[e / 2] & 0xffff0000u : xd[e / 2] << 16);
+            const float wv = __uint_as_float(e % 2 ? wd[e / 2] & 0xffff0000u : wd[e / 2] << 16);
+            acc = fmaf(xv, wv, acc);
+        }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, kWave);
+    return acc;
+}
+
+// k rounds over this lane's keys (0 = not eligible): lane r < k ends with the r-th pick's id and key
+template <int NV>
+__device__ __forceinline__ void rounds(uint32_t (&key)[NV], int k, int &id, uint32_t &my_k, uint32_t &top) {
+    const int lane = threadIdx.x % kWave;
+    uint32_t lk = 0;
+    int lj = 0;
+    auto lane_best = [&]() __attribute__((always_inline)) {
+        lk = 0, lj = 0;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (key[j] > lk) lk = key[j], lj = j;
+    };
+    lane_best();
+    id = -1, my_k = 0, top = 0;
+    for (int r = 0; r < k; ++r) {
+        const uint32_t best = topk::wave_reduce_u32<false>(lk);
+        const uint64_t holders = __ballot(lk == best);
+        int win;
+        if ((holders & (holders - 1)) == 0) {
+            win = __builtin_ctzll(holders);
+        } else {
+            const uint32_t mine = lk == best ? (uint32_t)(lane + lj * kWave) : 0xffffffffu;
+            win = (int)(topk::wave_reduce_u32<true>(mine) % kWave);
+        }
+        const int wj = __builtin_amdgcn_readlane(lj, win);
+        if (r == 0) top = best;
+        if (lane == r) my_k = best, id = win + wj * kWave;
+        if (lane == win) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                if (j == wj) key[j] = 0u;
+            lane_best();
+        }
+    }
+}
+
+template <int NV, int NCH>
+__global__ void __launch_bounds__(kThreads)
+    router_select_kernel(const uint16_t *x, const uint16_t *w, const float *bias, float *logits, int64_t ld,
+                         int64_t M, int E, int k, bool shared, const float *nx, const float *nw, int32_t *ids,
+                         float *coef, uint32_t *err) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t m = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+    if (m >= M) return;  // whole wave; no barrier in this kernel
+    constexpr int64_t K = (int64_t)NCH * 512;
+    const uint16_t *xm = x + m * K;
+    float *row = logits + m * ld;
+    uint4 xr[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) xr[i] = *reinterpret_cast<const uint4 *>(xm + (lane + i * kWave) * 8);
+    const float nxm = nx[m];
+    float va[NV], dl[NV], bv[NV];
+    bool fin = isfinite(nxm);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int e = lane + j * kWave;
+        const float a = e < E ? row[e] : 0.f, b = e < E && bias ? bias[e] : 0.f, n = e < E ? nw[e] : 0.f;
+        bv[j] = b;
+        va[j] = bias ? a + b : a;
+        fin = fin && isfinite(va[j]) && isfinite(n);
+        // delta' = (4K + 64) u |x| |w| + K 2^-124 + 2^-22 (|a| + |b|), rounded up by the 1 + 2^-10 factor
+        dl[j] = ((4.0f * (float)K + 64.0f) * 0x1p-24f * nxm * n + (float)K * 0x1p-124f +
+                 0x1p-22f * (fabsf(a) + fabsf(b))) * (1.0f + 0x1p-10f);
+    }
+    const bool exact_all = __ballot(!fin) != 0;  // uniform
+    uint32_t key[NV];
+    bool cand[NV];
+    if (!exact_all) {
+        // tau: the k-th largest lower bound
+#pragma unroll
+        for (int j = 0; j < NV; ++j) key[j] = lane + j * kWave < E ? topk::order_key(va[j] - dl[j]) : 0u;
+        int id_unused;
+        uint32_t my_unused, top_unused;
+        // after k rounds the k-th pick's key is the last best; recover it: lane k - 1 holds it
+        rounds<NV>(key, k, id_unused, my_unused, top_unused);
+        const uint32_t tau = __builtin_amdgcn_readlane(my_unused, k - 1);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) cand[j] = lane + j * kWave < E && topk::order_key(va[j] + dl[j]) >= tau;
+    } else {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) cand[j] = lane + j * kWave < E;
+    }
+    // exact values of the candidates (one wave-wide canonical dot each), bias added as the unfused path does
+    float ex[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        ex[j] = 0.f;
+        uint64_t mask = __ballot(cand[j]);
+        while (mask) {
+            const int l = __builtin_ctzll(mask);
+            mask &= mask - 1;
+            const int e = l + j * kWave;
+            float v = canonical_dot<NCH>(xr, w + (int64_t)e * K);
+            if (bias) v = v + bias[e];
+            if (lane == l) ex[j] = v;
+        }
+        if (cand[j]) row[lane + j * kWave] = ex[j];
+    }
+    if (shared) {
+        const float sv = canonical_dot<NCH>(xr, w + (int64_t)E * K);
+        if (lane == 0) row[E] = sv;
+    }
+    int bad = INT_MAX;
+    if (exact_all) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (lane + j * kWave < E && !isfinite(ex[j]) && lane + j * kWave < bad) bad = lane + j * kWave;
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off, kWave));
+    }
+    int32_t *id_row = ids + m * k;
+    float *coef_row = coef + m * k;
+    if (bad != INT_MAX) {  // strixite kernels/moe_router.hip:40-67: the token's ids -1, coefficients NaN, err
+        if (lane == 0 && atomicCAS(&err[0], 0u, 1u) == 0u) {
+            err[1] = (uint32_t)m;
+            err[2] = (uint32_t)bad;
+        }
+        if (lane < k) id_row[lane] = -1, coef_row[lane] = qnan();
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) key[j] = cand[j] ? topk::order_key(ex[j]) : 0u;
+    int id;
+    uint32_t my_k, top;
+    rounds<NV>(key, k, id, my_k, top);
+    const float e0 = lane < k ? expf(topk::key_value(my_k) - topk::key_value(top)) : 0.f;
+    float sum = e0;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, kWave);
+    if (lane < k) id_row[lane] = id, coef_row[lane] = e0 / sum;
+}
+
+}  // namespace
+
+bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
+                        int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
+                        hipStream_t stream) {
+    const int64_t nch = H / 512, ld = E + (shared ? 1 : 0);
+    if (H % 512 != 0 || nch < 1 || nch > 8 || E > 1024 || k > 32 || k > E ||
+        reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
+        return false;
+    float *nx = norms, *nw = norms + M;
+    dim3 g1((unsigned)((ld + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM));
+    STRIX_CHECK(g1.y <= 65535, "moe_router_prefill: M = ", M, " too large");
+    router_approx_kernel<<<g1, kThreads, 0, stream>>>(static_cast<const uint16_t *>(x), w, logits, ld, M, ld, H, nx,
+                                                       nw);
+    const unsigned g2 = (unsigned)((M + 3) / 4);
+    const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
+    auto go = [&](auto nvc, auto nchc) {
+        router_select_kernel<decltype(nvc)::value, decltype(nchc)::value><<<g2, kThreads, 0, stream>>>(
+            static_cast<const uint16_t *>(x), w, bias, logits, ld, M, (int)E, (int)k, shared, nx, nw, ids, coef, err);
+    };
+    auto by_nch = [&](auto nvc) {
+        switch (nch) {
+            case 4: go(nvc, std::integral_constant<int, 4>{}); break;
+            case 6: go(nvc, std::integral_constant<int, 6>{}); break;
+            case 8: go(nvc, std::integral_constant<int, 8>{}); break;
+            default: go(nvc, std::integral_constant<int, 2>{}); break;
+        }
+    };
+    if (nch != 2 && nch != 4 && nch != 6 && nch != 8) return false;
+    switch (nv) {
+        case 1: by_nch(std::integral_constant<int, 1>{}); break;
+        case 2: by_nch(std::integral_constant<int, 2>{}); break;
+        case 4: by_nch(std::integral_constant<int, 4>{}); break;
+        case 8: by_nch(std::integral_constant<int, 8>{}); break;
+        default: by_nch(std::integral_constant<int, 16>{}); break;
+    }
+    STRIX_HIP_CHECK_LAUNCH("moe_router_prefill M=", M, " E=", E, " k=", k, " H=", H);
+    return true;
+}
+
+}  // namespace strix::kernels

@@ -349,6 +349,44 @@ def test_layer_fused_topk_packing_matches_router(M, E, k):
     assert np.all(np.isfinite(to_np(out["y"]).view(np.uint16)[ok] != 0x7fc0))
 
 
+@pytest.mark.parametrize("biased", [False, True])
+def test_layer_prefill_router_exact_routing(biased):
+    """Prefill-size layers route through the bf16 MFMA projection + exact recomputation of the candidates: ids and
+    coefficients equal the canonical-order router's (linear_bf16w + bias + moe_router) bit for bit, with exact ties
+    (duplicated router rows), a block of all-zero rows, near ties one bf16 ulp apart, and a non-finite token, which
+    takes the exact path for all its experts and raises the router error."""
+    say("prefill router", biased)
+    H, E, k, M = 1024, 64, 8, 512
+    rng = np.random.default_rng(17)
+    bias = torch.from_numpy((0.3 * rng.standard_normal(E)).astype(np.float32)).to(DEV) if biased else None
+    layer = moe.MoeLayer.synth(H, E, k, 128, seed=5, router_bias=bias)
+    r = layer.router
+    rn = to_np(r).copy()
+    rn[10:20] = rn[5]         # exact ties: equal logits, the lower index wins
+    rn[30:40] = 0             # ten logits exactly 0
+    rn[50] = rn[49]
+    rn[50, 3] ^= 1            # one bf16 ulp apart in one element: near ties
+    r.copy_(torch.from_numpy(rn.view(np.int16)).to(DEV).view(torch.bfloat16))
+    x = moe.synth_bf16_normal(5, "x", 0, (M, H), 1.0)
+    x[7, 100] = float("inf")  # a non-finite token
+    x[9] = x[8]               # two identical tokens
+    out = layer.forward(x)
+    torch.cuda.synchronize()
+    lg = moe.linear_bf16w(x, r)
+    if biased:
+        lg[:, :E] += bias  # one FP32 add, as the layer applies it
+    rids, rcoef, rerr = moe.moe_router(lg, E, k, ld=E + 1)
+    assert np.array_equal(to_np(out["ids"]), to_np(rids))
+    assert np.array_equal(to_np(out["coef"]).view(np.uint32), to_np(rcoef).view(np.uint32))
+    err = to_np(out["err"]).view(np.uint32)
+    assert err[0] == 1 and err[1] == 7 and to_np(rerr).view(np.uint32)[0] == 1
+    # and the canonical logits are the oracle's (the router itself is pinned there)
+    ref = orc.router_logits(to_np(x), to_np(r), bias=to_np(bias) if biased else None)
+    oids, _, _ = orc.topk(ref, E, k)
+    ok = np.all(np.isfinite(ref[:, :E]), axis=1)
+    assert np.array_equal(to_np(out["ids"])[ok], oids[ok])
+
+
 def test_layer_config1_decode_q8():
     """1 token, H 2048, 64 experts, top-8, I 512, Q8 routed experts, no shared expert."""
     say("layer cfg1")
