@@ -20,7 +20,8 @@ void moe_topk_group_routes_small(const float *logits, int64_t ld, int64_t M, int
                                  hipStream_t stream);
 // Internal entry (router_prefill.hip), used by the layer forward for prefill-size batches: router projection (+ the
 // optional FP32 bias) and top-k with the canonical order's exact routing via bf16 MFMA plus exact recomputation of the
-// candidates. norms: M + E (+1) floats of scratch. Returns false (nothing launched) for shapes it does not take.
+// candidates. logits: [4][M][E (+1)] floats (the layer's logits are part 0); norms: 4 (M + E (+1)) floats of
+// scratch. Returns false (nothing launched) for shapes it does not take.
 bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
                         int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
                         hipStream_t stream);

@@ -1171,8 +1171,10 @@ LayerWs layer_ws(const MoeLayerWeights &w, int64_t M) {
     LayerWs L{};
     const int64_t E = w.E, k = w.k, H = w.H, I = w.I, ld = E + (w.has_shared ? 1 : 0);
     int64_t o = 0;
-    L.logits = o, o += al(M * ld * 4);
-    L.norms = o, o += al((M + ld) * 4);  // the prefill router's row norms
+    // the prefill router's K parts of approximate logits (the layer's logits are part 0) and their squared norms
+    // (room for up to 4 parts)
+    L.logits = o, o += al(4 * M * ld * 4);
+    L.norms = o, o += al(4 * (M + ld) * 4);
     L.ids = o, o += al(M * k * 4);
     L.coef = o, o += al(M * k * 4);
     L.route_bytes = kernels::moe_route_workspace_bytes(M, k, E);

@@ -30,12 +30,18 @@ namespace {
 using namespace strix::dev;
 constexpr int kWave = 64, kThreads = 256;
 
+
 // ---- pass 1: approximate logits + norms -----------------------------------------------------------------------------
-// Block tile 128 tokens x 64 rows, K in steps of 64 through LDS (rows padded to 144 bytes: the 16 lanes of a
-// fragment read hit 16 distinct 16-byte bank groups). Wave w computes tokens 32 w .. 32 w + 31 of the tile x all 64
-// rows: 2 x 4 tiles of v_mfma_f32_16x16x32_bf16 whose A and B fragments are both 16-byte row segments (x rows for
-// tokens, w rows for experts). The next K step's tiles are loaded into registers while the current one is multiplied.
-constexpr int kBM = 128, kBN = 64, kBK = 64, kLd = kBK + 8;
+// Only the E routed rows (the shared gate row is computed exactly by pass 2). Block tile 128 tokens x 128 rows, K in
+// steps of 64 through LDS (rows padded to 144 bytes: the 16 lanes of a fragment read hit 16 distinct 16-byte bank
+// groups); wave w computes tokens 64 (w / 2) .. + 63 x rows 64 (w % 2) .. + 63 as 4 x 4 v_mfma_f32_16x16x32_bf16
+// tiles whose A and B fragments are both 16-byte row segments (x rows for tokens, w rows for experts). The next K
+// step's tiles are loaded into registers while the current one is multiplied. K is split into kParts parts (grid z),
+// each summed by its own blocks into its own output (the pass is bound by latency and by L2 re-reads of the tiles,
+// which the large tiles keep to 4 reads of x and 32 of w at E 512, M 4096).
+// (parts: 1, 2, 4 measured 139, 122, 124 us for both passes at 4096 x 512 x 3072 on MI355X - more parts shorten this
+// pass but their partial logits push the router rows out of L2 before pass 2 re-reads them)
+constexpr int kBM = 128, kBN = 128, kBK = 64, kLd = kBK + 8, kParts = 2;
 
 __device__ __forceinline__ float sumsq8(const uint4 &v) {
     const uint32_t d[4] = {v.x, v.y, v.z, v.w};
@@ -53,58 +59,55 @@ __global__ void __launch_bounds__(kThreads)
     router_approx_kernel(const uint16_t *x, const uint16_t *w, float *a_out, int64_t ld, int64_t M, int64_t N,
                          int64_t K, float *nx, float *nw) {
     __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLd], Bs[kBN * kLd];
+    // K part blockIdx.z of gridDim.z: its sums go to part z of the outputs ([parts][M][ld], [parts][M], [parts][N])
+    const int64_t kp = K / gridDim.z, kbeg = kp * blockIdx.z, kend = kbeg + kp;
+    a_out += (int64_t)blockIdx.z * M * ld, nx += (int64_t)blockIdx.z * M, nw += (int64_t)blockIdx.z * N;
     const int t = threadIdx.x, lane = t % kWave, wave = t / kWave, g = lane / 16, j = lane % 16;
+    const int wm = 64 * (wave / 2), wn = 64 * (wave % 2);
     const int64_t n0 = (int64_t)blockIdx.x * kBN, m0 = (int64_t)blockIdx.y * kBM;
-    // staging: A chunk u covers row (t >> 3) + 32 u, 16 bytes at column 8 (t & 7); B chunk u row (t >> 3) + 32 u
+    // staging: chunk u covers row (t >> 3) + 32 u, 16 bytes at column 8 (t & 7), of A and of B
     const int sr = t >> 3, sc = (t & 7) * 8;
-    uint4 ra[4], rb[2];
-    float qa[4] = {0, 0, 0, 0}, qb[2] = {0, 0};
+    uint4 ra[4], rb[4];
+    float qa[4] = {0, 0, 0, 0}, qb[4] = {0, 0, 0, 0};
     auto load = [&](int64_t k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int64_t r = m0 + sr + 32 * u;
+            const int64_t r = m0 + sr + 32 * u, c = n0 + sr + 32 * u;
             ra[u] = r < M ? *reinterpret_cast<const uint4 *>(x + r * K + k0 + sc) : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int64_t r = n0 + sr + 32 * u;
-            rb[u] = r < N ? *reinterpret_cast<const uint4 *>(w + r * K + k0 + sc) : make_uint4(0, 0, 0, 0);
+            rb[u] = c < N ? *reinterpret_cast<const uint4 *>(w + c * K + k0 + sc) : make_uint4(0, 0, 0, 0);
         }
     };
-    float4v acc[2][4];
+    float4v acc[4][4];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = float4v{0, 0, 0, 0};
-    load(0);
-    for (int64_t k0 = 0; k0 < K; k0 += kBK) {
+    load(kbeg);
+    for (int64_t k0 = kbeg; k0 < kend; k0 += kBK) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             *reinterpret_cast<uint4 *>(&As[(sr + 32 * u) * kLd + sc]) = ra[u];
-            qa[u] += sumsq8(ra[u]);
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
             *reinterpret_cast<uint4 *>(&Bs[(sr + 32 * u) * kLd + sc]) = rb[u];
+            qa[u] += sumsq8(ra[u]);
             qb[u] += sumsq8(rb[u]);
         }
         __syncthreads();
-        if (k0 + kBK < K) load(k0 + kBK);
+        if (k0 + kBK < kend) load(k0 + kBK);
 #pragma unroll
         for (int s = 0; s < kBK / 32; ++s) {
-            Frag af[2], bf[4];
+            Frag af[4], bf[4];
 #pragma unroll
-            for (int a = 0; a < 2; ++a) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(&As[(32 * wave + 16 * a + j) * kLd + 32 * s + 8 * g]);
+            for (int a = 0; a < 4; ++a) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(&As[(wm + 16 * a + j) * kLd + 32 * s + 8 * g]);
                 af[a] = Frag{{v.x, v.y, v.z, v.w}};
             }
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(&Bs[(16 * b + j) * kLd + 32 * s + 8 * g]);
+                const uint4 v = *reinterpret_cast<const uint4 *>(&Bs[(wn + 16 * b + j) * kLd + 32 * s + 8 * g]);
                 bf[b] = Frag{{v.x, v.y, v.z, v.w}};
             }
 #pragma unroll
-            for (int a = 0; a < 2; ++a)
+            for (int a = 0; a < 4; ++a)
 #pragma unroll
                 for (int b = 0; b < 4; ++b) acc[a][b] = mfma_bf16(af[a], bf[b], acc[a][b]);
         }
@@ -112,58 +115,46 @@ __global__ void __launch_bounds__(kThreads)
     }
     // D: lane (j, g) holds tokens 4 g + r of column j
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t m = m0 + 32 * wave + 16 * a + 4 * g + r, n = n0 + 16 * b + j;
+                const int64_t m = m0 + wm + 16 * a + 4 * g + r, n = n0 + wn + 16 * b + j;
                 if (m < M && n < N) a_out[m * ld + n] = acc[a][b][r];
             }
-    // norms: the 8 threads staging a row meet; rounded up (relative error of the FP32 sums < 2^-10 for K <= 2^13)
-    constexpr float up = 1.0f + 1.0f / 256;
+    // squared norms of this K part: the 8 threads staging a row meet
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        float q = qa[u];
+        float q = qa[u], p = qb[u];
         q += __shfl_xor(q, 1, kWave);
         q += __shfl_xor(q, 2, kWave);
         q += __shfl_xor(q, 4, kWave);
-        const int64_t r = m0 + sr + 32 * u;
-        if (blockIdx.x == 0 && (t & 7) == 0 && r < M) nx[r] = sqrtf(q) * up;
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        float q = qb[u];
-        q += __shfl_xor(q, 1, kWave);
-        q += __shfl_xor(q, 2, kWave);
-        q += __shfl_xor(q, 4, kWave);
-        const int64_t r = n0 + sr + 32 * u;
-        if (blockIdx.y == 0 && (t & 7) == 0 && r < N) nw[r] = sqrtf(q) * up;
+        p += __shfl_xor(p, 1, kWave);
+        p += __shfl_xor(p, 2, kWave);
+        p += __shfl_xor(p, 4, kWave);
+        const int64_t r = m0 + sr + 32 * u, c = n0 + sr + 32 * u;
+        if (blockIdx.x == 0 && (t & 7) == 0 && r < M) nx[r] = q;
+        if (blockIdx.y == 0 && (t & 7) == 0 && c < N) nw[c] = p;
     }
 }
 
 // ---- pass 2: select -------------------------------------------------------------------------------------------------
-// The canonical dot of token row xr (this lane's NCH chunks, preloaded) with weight row wr: lane l's fmaf chain over
-// chunks l, l + 64, ... (element order), then the butterfly; every lane gets the sum.
+// The canonical lane partial of token row xr (this lane's NCH chunks) with weight row chunks c: the fmaf chain over
+// chunks l, l + 64, ... in element order; the wave's butterfly then gives the canonical sum.
 template <int NCH>
-__device__ __forceinline__ float canonical_dot(const uint4 (&xr)[NCH], const uint16_t *wr) {
-    const int lane = threadIdx.x % kWave;
-    uint4 wc[NCH];
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) wc[i] = *reinterpret_cast<const uint4 *>(wr + (lane + i * kWave) * 8);
+__device__ __forceinline__ float lane_chain(const uint4 (&xr)[NCH], const uint4 (&c)[NCH]) {
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-        const uint32_t xd[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w}, wd[4] = {wc[i].x, wc[i].y, wc[i].z, wc[i].w};
+        const uint32_t xd[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w}, wd[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float xv = __uint_as_float(e % 2 ? xd[e / 2] & 0xffff0000u : xd[e / 2] << 16);
-            const float wv = __uint_as_float(e % 2 ? wd[e / 2] & 0xffff0000u : wd[e / 2] << 16);
+        for (int k = 0; k < 8; ++k) {
+            const float xv = __uint_as_float(k % 2 ? xd[k / 2] & 0xffff0000u : xd[k / 2] << 16);
+            const float wv = __uint_as_float(k % 2 ? wd[k / 2] & 0xffff0000u : wd[k / 2] << 16);
             acc = fmaf(xv, wv, acc);
         }
     }
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, kWave);
     return acc;
 }
 
@@ -203,28 +194,39 @@ __device__ __forceinline__ void rounds(uint32_t (&key)[NV], int k, int &id, uint
     }
 }
 
+// One wave per token. parts: the approx pass's K parts [kParts][M][ld] (part 0 is the layer's logits buffer: the
+// exact values are written there); nx2 / nw2: the parts' squared norms.
 template <int NV, int NCH>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     router_select_kernel(const uint16_t *x, const uint16_t *w, const float *bias, float *logits, int64_t ld,
-                         int64_t M, int E, int k, bool shared, const float *nx, const float *nw, int32_t *ids,
+                         int64_t M, int E, int k, bool shared, const float *nx2, const float *nw2, int32_t *ids,
                          float *coef, uint32_t *err) {
+    __shared__ int cand_lds[kThreads / kWave][1040];  // a wave's candidate list (at most E + 1 <= 1025)
     const int lane = threadIdx.x % kWave;
     const int64_t m = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
     if (m >= M) return;  // whole wave; no barrier in this kernel
     constexpr int64_t K = (int64_t)NCH * 512;
+    const int64_t N = E;  // rows of the approximate pass (the routed ones)
     const uint16_t *xm = x + m * K;
     float *row = logits + m * ld;
     uint4 xr[NCH];
 #pragma unroll
     for (int i = 0; i < NCH; ++i) xr[i] = *reinterpret_cast<const uint4 *>(xm + (lane + i * kWave) * 8);
-    const float nxm = nx[m];
-    float va[NV], dl[NV], bv[NV];
+    float q = 0.f;
+#pragma unroll
+    for (int p = 0; p < kParts; ++p) q += nx2[p * M + m];
+    constexpr float up = 1.0f + 1.0f / 256;  // the FP32 sums of squares are within 2^-10 of the exact ones
+    const float nxm = sqrtf(q) * up;
+    float va[NV], dl[NV];
     bool fin = isfinite(nxm);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int e = lane + j * kWave;
-        const float a = e < E ? row[e] : 0.f, b = e < E && bias ? bias[e] : 0.f, n = e < E ? nw[e] : 0.f;
-        bv[j] = b;
+        float a = 0.f, n2 = 0.f;
+        if (e < E)
+#pragma unroll
+            for (int p = 0; p < kParts; ++p) a += row[p * M * ld + e], n2 += nw2[p * N + e];
+        const float b = e < E && bias ? bias[e] : 0.f, n = sqrtf(n2) * up;
         va[j] = bias ? a + b : a;
         fin = fin && isfinite(va[j]) && isfinite(n);
         // delta' = (4K + 64) u |x| |w| + K 2^-124 + 2^-22 (|a| + |b|), rounded up by the 1 + 2^-10 factor
@@ -235,39 +237,65 @@ __global__ void __launch_bounds__(kThreads)
     uint32_t key[NV];
     bool cand[NV];
     if (!exact_all) {
-        // tau: the k-th largest lower bound
+        // tau: the k-th largest lower bound (the key lane k - 1 ends with after k rounds)
 #pragma unroll
         for (int j = 0; j < NV; ++j) key[j] = lane + j * kWave < E ? topk::order_key(va[j] - dl[j]) : 0u;
         int id_unused;
-        uint32_t my_unused, top_unused;
-        // after k rounds the k-th pick's key is the last best; recover it: lane k - 1 holds it
-        rounds<NV>(key, k, id_unused, my_unused, top_unused);
-        const uint32_t tau = __builtin_amdgcn_readlane(my_unused, k - 1);
+        uint32_t kth, top_unused;
+        rounds<NV>(key, k, id_unused, kth, top_unused);
+        const uint32_t tau = __builtin_amdgcn_readlane(kth, k - 1);
 #pragma unroll
         for (int j = 0; j < NV; ++j) cand[j] = lane + j * kWave < E && topk::order_key(va[j] + dl[j]) >= tau;
     } else {
 #pragma unroll
         for (int j = 0; j < NV; ++j) cand[j] = lane + j * kWave < E;
     }
-    // exact values of the candidates (one wave-wide canonical dot each), bias added as the unfused path does
-    float ex[NV];
+    // the candidates in ascending expert order (then the shared gate row E) as a list in this wave's LDS
+    int *cl = cand_lds[threadIdx.x / kWave];
+    int nc = 0;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        ex[j] = 0.f;
-        uint64_t mask = __ballot(cand[j]);
-        while (mask) {
-            const int l = __builtin_ctzll(mask);
-            mask &= mask - 1;
-            const int e = l + j * kWave;
-            float v = canonical_dot<NCH>(xr, w + (int64_t)e * K);
-            if (bias) v = v + bias[e];
-            if (lane == l) ex[j] = v;
-        }
-        if (cand[j]) row[lane + j * kWave] = ex[j];
+        const uint64_t mk = __ballot(cand[j]);
+        if (cand[j]) cl[nc + __popcll(mk & ((1ull << lane) - 1ull))] = lane + j * kWave;
+        nc += __popcll(mk);
     }
-    if (shared) {
-        const float sv = canonical_dot<NCH>(xr, w + (int64_t)E * K);
-        if (lane == 0) row[E] = sv;
+    if (shared && lane == 0) cl[nc] = E;
+    nc += shared ? 1 : 0;
+
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's list writes are done (its lanes read them next)
+    float ex[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) ex[j] = 0.f;
+    // one candidate at a time; the next one's row loads are issued before this one's chain and butterfly
+    auto load = [&](int e, uint4 (&c)[NCH]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i)
+            c[i] = *reinterpret_cast<const uint4 *>(w + (int64_t)e * K + (lane + i * kWave) * 8);
+    };
+    uint4 cur[NCH], nxt[NCH];
+    int ec = __builtin_amdgcn_readfirstlane(cl[0]);
+    load(ec, cur);
+    for (int s2 = 0; s2 < nc; ++s2) {
+        const int en = s2 + 1 < nc ? __builtin_amdgcn_readfirstlane(cl[s2 + 1]) : ec;
+        if (s2 + 1 < nc) load(en, nxt);
+        float d = lane_chain<NCH>(xr, cur);
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) d = d + __shfl_xor(d, off, kWave);
+        if (ec == E) {
+            if (lane == 0) row[E] = d;  // the shared gate logit, unbiased
+        } else {
+            const float vb = bias ? d + bias[ec] : d;  // one FP32 add, as the unfused path
+            if (lane == ec % kWave) {
+                const int js = ec / kWave;
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    if (j == js) ex[j] = vb;
+                row[ec] = vb;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) cur[i] = nxt[i];
+        ec = en;
     }
     int bad = INT_MAX;
     if (exact_all) {
@@ -305,13 +333,13 @@ bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int
                         int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
                         hipStream_t stream) {
     const int64_t nch = H / 512, ld = E + (shared ? 1 : 0);
-    if (H % 512 != 0 || nch < 1 || nch > 8 || E > 1024 || k > 32 || k > E ||
+    if (H % 512 != 0 || nch < 1 || nch > 8 || E > 1024 || k > 32 || k > E || (H / kParts) % kBK != 0 ||
         reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
         return false;
-    float *nx = norms, *nw = norms + M;
-    dim3 g1((unsigned)((ld + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM));
+    float *nx = norms, *nw = norms + (int64_t)kParts * M;
+    dim3 g1((unsigned)((E + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM), (unsigned)kParts);
     STRIX_CHECK(g1.y <= 65535, "moe_router_prefill: M = ", M, " too large");
-    router_approx_kernel<<<g1, kThreads, 0, stream>>>(static_cast<const uint16_t *>(x), w, logits, ld, M, ld, H, nx,
+    router_approx_kernel<<<g1, kThreads, 0, stream>>>(static_cast<const uint16_t *>(x), w, logits, ld, M, E, H, nx,
                                                        nw);
     const unsigned g2 = (unsigned)((M + 3) / 4);
     const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
