@@ -42,7 +42,25 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run 4 plain 256 MiB device copies (the known-size reference for FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_gate_up_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode gate_up kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarized
+    in profiles/ (a line `traffic_bytes_per_launch: N`), or None when that summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip().split()[0])
+    except OSError:
+        pass
+    return None
 
 
 def log(*a):
@@ -67,6 +85,13 @@ def main():
 
     torch.cuda.set_device(0)
     dev = "cuda"
+    if args.calibrate:
+        ca = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        cb = torch.empty_like(ca)
+        for _ in range(4):
+            cb.copy_(ca)
+        torch.cuda.synchronize()
+        del ca, cb
     nl = args.layers
     t0 = time.time()
     layers = []
@@ -237,9 +262,9 @@ def main():
                    "tokens_per_step": Md, "layers_rotated": nl, "graph": graphs is not None,
                    "unique_experts_mean": round(statistics.mean(uniq), 1),
                    "layer_algorithmic_GBps": round(dec_layer_gbs, 1)},
-        "roofline": {"bound": "hbm", "kernel": "expert_gemm_kernel<Q4, GROUPED, SWIGLU> (gate_up + SwiGLU)",
+        "roofline": {"bound": "hbm", "kernel": "expert_stream_kernel<Q4, GROUPED, SWIGLU> (decode gate_up + SwiGLU)",
                      "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes_per_launch": int(gu_bytes), "us_per_launch": round(gu_us, 3)},
         "cpu_baseline": cpu,
         "prefill": pre,
