@@ -165,6 +165,9 @@ def moe_route_workspace_bytes(M: int, A: int, E: int) -> int:
 
 def moe_group_routes(ids: torch.Tensor, E: int, ws: torch.Tensor | None = None, err: torch.Tensor | None = None):
     """strixite kernels/moe_grouped.hpp:52-53. Returns (ws int32, err)."""
+    if ids.dtype != torch.int32 or ids.dim() != 2 or not ids.is_contiguous():
+        raise TypeError(f"moe_group_routes: ids must be a contiguous [M, A] int32 tensor, got {ids.dtype} "
+                        f"{tuple(ids.shape)}")
     M, A = ids.shape
     nbytes = moe_route_workspace_bytes(M, A, E)
     if ws is None:

@@ -248,6 +248,38 @@ def test_perslot_kernels_match_grouped():
     assert to_np(err).view(np.uint32).tolist() == [1, E + 5, 6]
 
 
+@pytest.mark.parametrize("M,A,E", [(4, 6, 24), (40, 3, 6)])
+def test_decode_kernels_match_perslot(M, A, E):
+    """The decode-size grouped kernels at the served shape (H 3072, I 512, Q4 g128): h bit for bit that of the per-slot
+    kernel, h and the down partials against the oracle; (40, 3, 6) puts 20 slots
+    on each expert, so each expert has two token tiles."""
+    say("decode kernels vs per-slot", M, A, E)
+    H, I = 3072, 512
+    gu, dn = _experts(4, E, H, I, seed=13)
+    x = orc.gen_bf16_normal(orc.tensor_key(6, "x"), 1.0, (M, H))
+    ids = np.stack([np.random.default_rng(100 + m).permutation(E)[:A] for m in range(M)]).astype(np.int32)
+    tid = torch.from_numpy(ids).to(DEV)
+    err = moe.zero_err()
+    ws, _ = moe.moe_group_routes(tid, E)
+    hg = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)
+    hp = moe.experts_gather(bf16(x), gu, E, tid, err, swiglu=True)
+    assert torch.equal(hg, hp)
+    b, q, s, m, G = qspec(gu)
+    href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G), E, ids)
+    assert rel_err(to_np(hg), href) < 1e-2
+    coef = torch.from_numpy(np.random.default_rng(7).random((M, A)).astype(np.float32)).to(DEV)
+    pt = torch.empty((M * A, H), dtype=torch.float32, device=DEV)
+    yg = moe.experts_combine_grouped(hg, dn, E, tid, coef, ws, M, A, partial=pt)
+    b, q, s, m, G = qspec(dn)
+    part = orc.experts_down(to_np(hg), orc.qview(b, q, s, m, dn.N, I, G), E, ids)
+    assert rel_err(pt.cpu().numpy(), part) < 1e-4
+    # the per-slot combine sums each group's activations on the VALU, the grouped kernels on the matrix cores: the
+    # FP32 dots may differ in the last bits, so an output may round to the neighbouring bf16
+    yp = moe.experts_combine(hg, dn, E, tid, coef, err)
+    assert rel_err(to_np(yg), to_np(yp)) <= 2.0 ** -8
+    assert to_np(err)[0] == 0
+
+
 def test_linear_q8_and_swiglu():
     say("linear_q8 / swiglu")
     M, N, K = 20, 1024, 3072
