@@ -13,6 +13,7 @@
 // A span (Q4: 128 codes, Q8: 64) never crosses a group: Q4 needs G = 128, Q8 G = 64 or 128 (the reference's
 // served layout: q4g128, q8g64).
 #include "common.hpp"
+#include "route_small.hpp"
 
 #include <algorithm>
 #include <map>
@@ -27,7 +28,7 @@ namespace route {
 // 16-slot tile records
 __host__ __device__ __forceinline__ int64_t slots_at(int64_t E) { return 4 + E + 2; }
 __host__ __device__ __forceinline__ int64_t t16_rec_at(int64_t S, int64_t E) { return (4 + E + 2 + S + 3) / 4 * 4; }
-constexpr int kRec16 = 20;  // ints per tile record: {bucket, first index into slots, rows, 0, slot[16], -1 past rows}
+static_assert(kRec16 == 20, "tile record: {bucket, first index into slots, rows, 0, slot[16], -1 past rows}");
 }  // namespace route
 
 namespace {
@@ -458,11 +459,71 @@ __device__ __forceinline__ void stage_store(const Stage<RT> &sg, int tid, int nt
     }
 }
 
-template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST>
+// ---- the shared expert folded into the decode launches ------------------------------------------------------------
+// At decode sizes the shared expert (dense Q8, at most 16 tokens) is a few MB of weights next to hundreds of MB of
+// routed experts. On its own it costs four latency-bound launches, or a second stream whose joins cost as much; so its
+// pieces ride along in launches the layer makes anyway, as extra blocks at the front of their grids:
+//   top-k + packing launch (one busy block): the gate_up's split-K parts;
+//   routed gate_up launch: the gate_up's finish, h = bf16(silu(sum g) * sum u), sums over the parts in order;
+//   routed down launch: the down's split-K parts;
+//   combine launch: the down's finish, s = bf16(sum over the parts in order), read where the stored s was.
+// A unit of the split-K projection: wave w computes rows tile * 16 .. + 15 over K steps [part * spp, (part + 1) * spp)
+// for all M tokens and writes its FP32 sums to part[part][m][n].
+template <int BITS>
+__device__ __forceinline__ void dense_part_unit(const GemmArgs &a, int spp, int parts, float *part, int64_t w) {
+    const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
+    const int64_t tile = w / parts, pt = w % parts;
+    const int64_t spans = a.K / QFmt<BITS>::SPAN, s0 = pt * spp, s1 = s0 + spp < spans ? s0 + spp : spans;
+    const int64_t tile_row[1] = {tile * 16};
+    float4v acc[1];
+    wave_gemm<BITS, 1, false>(a, j < a.M ? a.x + j * a.K : nullptr, tile_row, s0, s1, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (4 * g + r < a.M) part[(pt * a.M + 4 * g + r) * a.N + tile * 16 + j] = acc[0][r];
+}
+// Output i of the in-order sum of the parts: SWI: h[m, c] = bf16(silu(g) * u), g and u the sums of rows c and N / 2 + c
+// (i = m * N / 2 + c); otherwise y[m, n] = bf16(sum) (i = m * N + n).
+template <bool SWI>
+__device__ __forceinline__ float parts_sum(const float *part, int parts, int64_t M, int64_t N, int64_t i) {
+    const int64_t no = SWI ? N / 2 : N, m = i / no, c = i % no;
+    float v0 = 0.f, v1 = 0.f;
+    for (int p = 0; p < parts; ++p) {
+        v0 += part[(p * M + m) * N + c];
+        if constexpr (SWI) v1 += part[(p * M + m) * N + no + c];
+    }
+    return SWI ? silu(v0) * v1 : v0;
+}
+
+struct SharedJob {
+    GemmArgs a;         // SH 2: the down projection (M tokens); SH 1: a.M, a.N = 2I of the gate_up
+    const float *pin;   // SH 1: the gate_up's parts [parts][M][2I]
+    float *pout;        // SH 2: the down's parts [parts][M][H]
+    uint16_t *out;      // SH 1: h [M][I]
+    int spp, parts;
+    int64_t units;      // SH 1: outputs M * I, a thread each; SH 2: waves (H / 16) * parts
+    int blocks;         // leading blocks of the grid that take the units
+};
+
+// SH: the shared expert's projection riding along (0 none, 1 the Q8 gate_up + SwiGLU, 2 the Q8 down)
+template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<EPI == EPI_SWIGLU>())))
     expert_stream_kernel(GemmArgs a, int64_t tiles_bound, int64_t col_blocks, int ks, uint32_t q_bytes,
-                         uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
+                         uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes, SharedJob sh) {
     using F = QFmt<BITS>;
+    int bid = (int)blockIdx.x, nblk = (int)gridDim.x;  // this block among the routed blocks
+    if constexpr (SH != 0) {
+        if (bid < sh.blocks) {  // a shared-expert block: its units, then done (no barrier in this branch)
+            if constexpr (SH == 1) {
+                const int64_t i = (int64_t)bid * blockDim.x + threadIdx.x;
+                if (i < sh.units) sh.out[i] = f32_to_bf16(parts_sum<true>(sh.pin, sh.parts, sh.a.M, sh.a.N, i));
+            } else {
+                const int64_t w = (int64_t)bid * (blockDim.x / kWave) + threadIdx.x / kWave;
+                if (w < sh.units) dense_part_unit<8>(sh.a, sh.spp, sh.parts, sh.pout, w);
+            }
+            return;
+        }
+        bid -= sh.blocks, nblk -= sh.blocks;
+    }
     constexpr bool SWI = EPI == EPI_SWIGLU;
     constexpr int RT = wave_tiles<SWI>();
     constexpr int KS = SWI ? kWaves : 1;  // most waves of a block sharing an item (SwiGLU: the block's ks waves)
@@ -484,8 +545,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     int64_t n_tiles = tiles_bound;
     if constexpr (MODE == GROUPED) n_tiles = a.ws[0] < tiles_bound ? a.ws[0] : tiles_bound;
     const int64_t n_items = n_tiles * col_blocks;
-    const int64_t first = SWI ? (int64_t)blockIdx.x : (int64_t)blockIdx.x * kWaves + wave;
-    const int64_t stride = SWI ? (int64_t)gridDim.x : (int64_t)gridDim.x * kWaves;
+    const int64_t first = SWI ? (int64_t)bid : (int64_t)bid * kWaves + wave;
+    const int64_t stride = SWI ? (int64_t)nblk : (int64_t)nblk * kWaves;
     if (first >= n_items) return;  // SwiGLU: uniform per block, before any barrier
     const bool report = wave == 0;
 
@@ -653,50 +714,25 @@ __global__ void __launch_bounds__(kThreads) perslot_combine_kernel(GemmArgs a, c
     }
 }
 
-constexpr int kSharedParts = 8;  // most K parts of the split-K dense projection
+constexpr int kSharedParts = 8;  // most K parts of the shared expert's split-K projections
+constexpr int kSharedUnitsPerBlock = 4;  // shared-expert units a block of the top-k launch takes
 
-// Dense projection of at most 16 tokens (the shared expert at decode sizes), split over K so that hundreds of waves
-// stream its rows at once: wave (tile, part) computes rows tile * 16 .. + 15 over K steps [part * spp, (part + 1) *
-// spp) for all tokens and writes its FP32 sums to part[part][m][n]; dense_parts_finish adds the parts in order.
-template <int BITS>
-__global__ void __launch_bounds__(kThreads) dense_parts_kernel(GemmArgs a, int spp, int parts, float *part) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const int g = lane / 16, j = lane % 16;
-    const int64_t w = (int64_t)blockIdx.x * kWaves + wave, tiles = a.N / 16;
-    if (w >= tiles * parts) return;  // no barrier in this kernel
-    const int64_t tile = w / parts, pt = w % parts;
-    const int64_t spans = a.K / QFmt<BITS>::SPAN, s0 = pt * spp, s1 = s0 + spp < spans ? s0 + spp : spans;
-    const int64_t tile_row[1] = {tile * 16};
-    float4v acc[1];
-    wave_gemm<BITS, 1, false>(a, j < a.M ? a.x + j * a.K : nullptr, tile_row, s0, s1, acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-        if (4 * g + r < a.M) part[(pt * a.M + 4 * g + r) * a.N + tile * 16 + j] = acc[0][r];
-}
-
-// SWI: h[m, c] = bf16(silu(g) * u) with g, u the in-order sums of the parts of rows c and I + c (I = N / 2); otherwise
-// y[m, n] = bf16(sum). One thread an output.
-template <bool SWI>
-__global__ void __launch_bounds__(kThreads) dense_parts_finish(const float *part, int parts, int64_t M, int64_t N,
-                                                               uint16_t *y) {
-    const int64_t no = SWI ? N / 2 : N, i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i >= M * no) return;
-    const int64_t m = i / no, c = i % no;
-    float g[kSharedParts], u[kSharedParts];
-#pragma unroll
-    for (int p = 0; p < kSharedParts; ++p)
-        if (p < parts) {
-            g[p] = part[(p * M + m) * N + c];
-            if constexpr (SWI) u[p] = part[(p * M + m) * N + no + c];
-        }
-    float v0 = 0.f, v1 = 0.f;
-#pragma unroll
-    for (int p = 0; p < kSharedParts; ++p)
-        if (p < parts) {
-            v0 += g[p];
-            if constexpr (SWI) v1 += u[p];
-        }
-    y[m * no + c] = f32_to_bf16(SWI ? silu(v0) * v1 : v0);
+// Top-k + packing of a small batch (block 0, route_small.hpp) with the shared expert's gate_up parts riding along in
+// the other blocks: the one-block launch otherwise leaves the chip idle.
+template <int NV>
+__global__ void __launch_bounds__(1024)
+    topk_route_shared_kernel(const float *logits, int64_t ld, int M, int E, int k, int32_t *ids, float *coef,
+                             route::Layout L, int nbits, int32_t *ws, uint32_t *err_router, uint32_t *err_route,
+                             GemmArgs sa, int spp, int parts, float *part, int64_t units) {
+    extern __shared__ int lds[];
+    if (blockIdx.x == 0) {
+        route::topk_route_small_body<NV>(logits, ld, M, E, k, ids, coef, L, nbits, ws, err_router, err_route, lds);
+        return;
+    }
+    // 4 units a block (its other waves exit): the units spread over many CUs
+    const int64_t w = (int64_t)(blockIdx.x - 1) * kSharedUnitsPerBlock + threadIdx.x / kWave;
+    if (threadIdx.x / kWave < kSharedUnitsPerBlock && w < units)
+        dense_part_unit<8>(sa, spp, parts, part, w);  // no barrier in this kernel
 }
 
 // y[m, n] = sum_a coef[m, a] * partial[m * A + a, n] in slot order (fmaf), rounded once; NaN for a token with an
@@ -707,14 +743,28 @@ template <bool SH, bool RES>
 __global__ void __launch_bounds__(kThreads)
     combine_reduce_kernel(const float *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                           int64_t N, uint16_t *y, const uint16_t *s, const float *gate_logit, int64_t gate_ld,
-                          uint32_t gate_index, uint32_t *err, const uint16_t *resid, uint16_t *out) {
+                          uint32_t gate_index, uint32_t *err, const uint16_t *resid, uint16_t *out,
+                          const float *s_part, int s_parts) {
     const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
     if (i >= M * N) return;
     const int64_t m = i / N, n = i % N;
     // the loads that do not depend on the sum go out with the partials' (one round trip for the thread)
     float gl = 0.f;
     uint2 su = make_uint2(0, 0), xu = make_uint2(0, 0);
-    if constexpr (SH) gl = gate_logit[m * gate_ld], su = *reinterpret_cast<const uint2 *>(s + i);
+    if constexpr (SH) {
+        gl = gate_logit[m * gate_ld];
+        if (s_part == nullptr) {
+            su = *reinterpret_cast<const uint2 *>(s + i);
+        } else {  // s = bf16 of the in-order sum of the shared down's K parts (parts_sum's arithmetic)
+            float sv[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int p = 0; p < s_parts; ++p) {
+                const float4 q = *reinterpret_cast<const float4 *>(s_part + (p * M + m) * N + n);
+                sv[0] += q.x, sv[1] += q.y, sv[2] += q.z, sv[3] += q.w;
+            }
+            su = make_uint2((uint32_t)f32_to_bf16(sv[0]) | ((uint32_t)f32_to_bf16(sv[1]) << 16),
+                            (uint32_t)f32_to_bf16(sv[2]) | ((uint32_t)f32_to_bf16(sv[3]) << 16));
+        }
+    }
     if constexpr (RES) xu = *reinterpret_cast<const uint2 *>(resid + i);
     bool ok = true;
     float v[4] = {0, 0, 0, 0};
@@ -846,8 +896,8 @@ int swiglu_ks(int64_t spans, int D) {
     return ks;
 }
 
-template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST>
-void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
+template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH>
+void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, const SharedJob &sh, hipStream_t stream) {
     constexpr bool SWI = EPI == EPI_SWIGLU;
     constexpr int RT = wave_tiles<SWI>();
     const int64_t spans = a.K / QFmt<BITS>::SPAN;
@@ -857,7 +907,7 @@ void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
     const int threads = SWI ? ks * kWave : kThreads;
     const int64_t col_blocks = SWI ? (a.N / 2 + 16 * RT / 2 - 1) / (16 * RT / 2) : (a.N + 16 * RT - 1) / (16 * RT);
     const int64_t items = tiles_bound * col_blocks, per_block = SWI ? 1 : kWaves;
-    auto kernel = expert_stream_kernel<BITS, MODE, EPI, XF16, XROW_DIV, HF16, SST>;
+    auto kernel = expert_stream_kernel<BITS, MODE, EPI, XF16, XROW_DIV, HF16, SST, SH>;
     // resident blocks a CU, cached for the last (block size, LDS) this instantiation was launched with
     static thread_local int occ_threads = -1, occ = 1;
     static thread_local size_t occ_lds = 0;
@@ -866,7 +916,8 @@ void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
         occ_threads = threads, occ_lds = lds;
     }
     const int64_t want = (items + per_block - 1) / per_block, cap = (int64_t)device_cus() * occ;
-    const int64_t blocks = std::max<int64_t>(1, std::min(want, cap));
+    // shared-expert blocks come first in the grid and finish in a few microseconds; the routed blocks fill the rest
+    const int64_t blocks = std::max<int64_t>(1, std::min(want, cap)) + sh.blocks;
     // 32-bit buffer offsets: the weight view and the activations must each stay below 2 GiB
     const int64_t q_bytes = a.N * a.E * a.K * BITS / 8, s_bytes = a.N * a.E * (a.K / a.G) * 2;
     const int64_t x_rows = MODE == GROUPED ? (XROW_DIV ? a.S / a.A : a.S) : MODE == DENSE ? a.M : (XROW_DIV ? a.M : a.M * a.A);
@@ -877,18 +928,28 @@ void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
                 "expert kernels: weight (", q_bytes, " B), activation (", x_bytes, " B) or output (", y_bytes,
                 " B) tensor at or above 2 GiB (32-bit buffer offsets)");
     kernel<<<(unsigned)blocks, threads, lds, stream>>>(a, tiles_bound, col_blocks, ks, (uint32_t)q_bytes,
-                                                      (uint32_t)s_bytes, (uint32_t)x_bytes, (uint32_t)y_bytes);
+                                                      (uint32_t)s_bytes, (uint32_t)x_bytes, (uint32_t)y_bytes, sh);
 }
 
+// sh: the shared expert's projection to run in the same launch (GROUPED bf16 activations only), or null
 template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
-void launch_gemm(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream) {
+void launch_gemm(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream, const SharedJob *sh = nullptr) {
     // scale staging when an item's scales fit kStageMax dwords a lane of the item's waves
     constexpr bool SWI = EPI == EPI_SWIGLU;
+    constexpr int SHK = SWI ? 1 : 2;
     const int lanes = (SWI ? swiglu_ks(a.K / QFmt<BITS>::SPAN, ring_depth<true>()) : 1) * kWave;
     const int64_t per_tensor = wave_tiles<SWI>() * 8 * (a.K / a.G);  // dwords
-    if ((per_tensor + lanes - 1) / lanes * 2 <= kStageMax)
-        return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, true>(a, tiles_bound, stream);
-    launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, false>(a, tiles_bound, stream);
+    const bool sst = (per_tensor + lanes - 1) / lanes * 2 <= kStageMax;
+    const SharedJob none{};
+    if constexpr (MODE == GROUPED && !XF16 && (EPI == EPI_SWIGLU || EPI == EPI_F32)) {
+        if (sh != nullptr) {
+            if (sst) return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, true, SHK>(a, tiles_bound, *sh, stream);
+            return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, false, SHK>(a, tiles_bound, *sh, stream);
+        }
+    }
+    STRIX_CHECK(sh == nullptr, "expert kernels: a shared projection rides along only with a grouped gate_up or down");
+    if (sst) return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, true, 0>(a, tiles_bound, none, stream);
+    launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, false, 0>(a, tiles_bound, none, stream);
 }
 
 template <int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
@@ -904,6 +965,37 @@ GemmArgs make_args(const QV &w, int64_t E, const void *x, void *y, int64_t ldy) 
     a.N = w.N / E, a.K = w.K, a.G = w.G, a.E = E;
     a.y = y, a.ldy = ldy;
     return a;
+}
+
+// The small-batch top-k + packing (moe_topk_group_routes_small's launch) with the shared expert's gate_up parts in
+// the grid's other blocks.
+void launch_topk_route_shared(const float *logits, int64_t ld, int64_t M, int64_t E, int64_t k, int32_t *ids,
+                              float *coef, void *ws, size_t ws_bytes, uint32_t *err_router, uint32_t *err_route,
+                              const GemmArgs &sa, int spp, int parts, float *part, hipStream_t stream) {
+    const char *fn = "moe_layer_forward (top-k + packing)";
+    STRIX_CHECK(M >= 1 && k >= 1 && k <= 64 && k <= E && E <= kMoeMaxExperts && M * k <= route::kFusedSlots, fn,
+                ": M = ", M, ", E = ", E, ", k = ", k);
+    STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, k, E) && reinterpret_cast<uintptr_t>(ws) % 16 == 0, fn,
+                ": workspace of ", ws_bytes, " bytes, needs ", moe_route_workspace_bytes(M, k, E), ", 16-byte aligned");
+    const route::Layout L = route::layout(M, k, E);
+    const int nbits = route::bucket_bits(E);
+    const size_t lds = route::topk_route_small_lds(L);
+    const int64_t units = sa.N / 16 * parts;
+    const unsigned blocks = 1 + (unsigned)((units + kSharedUnitsPerBlock - 1) / kSharedUnitsPerBlock);
+    const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
+    auto go = [&](auto nvc) {
+        topk_route_shared_kernel<decltype(nvc)::value><<<blocks, 1024, lds, stream>>>(
+            logits, ld, (int)M, (int)E, (int)k, ids, coef, L, nbits, static_cast<int32_t *>(ws), err_router, err_route,
+            sa, spp, parts, part, units);
+    };
+    switch (nv) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        case 8: go(std::integral_constant<int, 8>{}); break;
+        default: go(std::integral_constant<int, 16>{}); break;
+    }
+    STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " E=", E, " k=", k);
 }
 
 void check_grouped(const char *fn, const void *x, const QV &w, int64_t E, const void *ws, size_t ws_bytes, int64_t M,
@@ -954,9 +1046,10 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E, " N=", N, " K=", w.K, " G=", w.G, h_f16 ? " (F16 h)" : "");
 }
 
+// s_part: the shared expert's down as K parts [s_parts][M][N] instead of the stored sh->s
 void combine_reduce(const float *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                     int64_t N, uint16_t *y, const MoeSharedAdd *sh, const uint16_t *resid, uint16_t *out,
-                    hipStream_t stream) {
+                    hipStream_t stream, const float *s_part = nullptr, int s_parts = 0) {
     const unsigned blocks = (unsigned)((M * N / 4 + kThreads - 1) / kThreads);
     const uint16_t *s = sh ? static_cast<const uint16_t *>(sh->s) : nullptr;
     const float *gl = sh ? sh->gate_logit : nullptr;
@@ -965,7 +1058,7 @@ void combine_reduce(const float *partial, const int32_t *ids, const float *coef,
     uint32_t *err = sh ? sh->err : nullptr;
     auto go = [&](auto shc, auto resc) {
         combine_reduce_kernel<decltype(shc)::value, decltype(resc)::value><<<blocks, kThreads, 0, stream>>>(
-            partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, resid, out);
+            partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, resid, out, s_part, s_parts);
     };
     if (sh && out) go(std::true_type{}, std::true_type{});
     else if (sh) go(std::true_type{}, std::false_type{});
@@ -1250,10 +1343,44 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     uint16_t *sh_s = reinterpret_cast<uint16_t *>(base + L.sh_s);
     uint32_t *err_router = err, *err_expert = err + 3;
 
-    // shared expert (dense Q8) on the helper stream: gate_up + SwiGLU -> sh_h, down -> sh_s
+    // shared expert (dense Q8): at decode sizes folded into the routed gate_up and down launches (no second stream,
+    // whose join would cost more than the shared expert's few MB); otherwise on the helper stream: gate_up + SwiGLU ->
+    // sh_h, down -> sh_s
+    const bool fold = w.has_shared && M <= 16 && M * k <= 1024;
+    SharedJob sh_jobs[2]{};  // ride along in the routed gate_up and down launches
+    GemmArgs sh_gu{};        // its gate_up parts ride along in the top-k launch
+    int sh_gu_spp = 0, sh_gu_parts = 0;
+    float *sh_part = reinterpret_cast<float *>(base + L.sh_part);
+    if (fold) {
+        const QV gv = qv(w.sh_gate_up), dv = qv(w.sh_down);
+        check_view(fn, gv, 1);
+        check_view(fn, dv, 1);
+        // K parts of at least 4 steps, at most kSharedParts: hundreds of waves stream each projection's rows at once
+        auto split = [&](int64_t K, int &spp, int &parts) {
+            const int64_t spans = K / QFmt<8>::SPAN;
+            parts = (int)std::max<int64_t>(1, std::min<int64_t>(kSharedParts, spans / 4));
+            spp = (int)((spans + parts - 1) / parts);
+        };
+        sh_gu = make_args(gv, 1, x, nullptr, 0);
+        sh_gu.M = M;
+        split(gv.K, sh_gu_spp, sh_gu_parts);
+        const int ks = swiglu_ks(w.gate_up.K / (w.gate_up_bits == 4 ? QFmt<4>::SPAN : QFmt<8>::SPAN), ring_depth<true>());
+        SharedJob &j0 = sh_jobs[0];
+        j0.a.M = M, j0.a.N = gv.N;
+        j0.pin = sh_part, j0.out = sh_h, j0.parts = sh_gu_parts;
+        j0.units = M * (gv.N / 2);
+        j0.blocks = (int)((j0.units + ks * kWave - 1) / (ks * kWave));
+        SharedJob &j1 = sh_jobs[1];
+        j1.a = make_args(dv, 1, sh_h, nullptr, 0);
+        j1.a.M = M;
+        split(dv.K, j1.spp, j1.parts);
+        j1.pout = sh_part;
+        j1.units = dv.N / 16 * j1.parts;
+        j1.blocks = (int)((j1.units + kWaves - 1) / kWaves);
+    }
     std::unique_lock<std::mutex> side_lock(side_mu, std::defer_lock);
     SideStream *ss = nullptr;
-    if (w.has_shared) {
+    if (w.has_shared && !fold) {
         const QV gv = qv(w.sh_gate_up), dv = qv(w.sh_down);
         check_view(fn, gv, 1);
         check_view(fn, dv, 1);
@@ -1268,27 +1395,6 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         if (M >= 128 && H % gemm::BK == 0 && I % gemm::BK == 0 && gv.G % gemm::BK == 0 && dv.G % gemm::BK == 0) {
             launch_expert_gemm<8, DENSE, EPI_SWIGLU, false, false>(a, ss->s);
             launch_expert_gemm<8, DENSE, EPI_BF16, false, false>(b, ss->s);
-        } else if (M <= 16) {
-            // split over K: each projection is a few MB streamed by hundreds of waves, then an in-order sum of parts
-            float *part = reinterpret_cast<float *>(base + L.sh_part);
-            auto split = [&](const GemmArgs &g, bool swi, uint16_t *out) {
-                const int64_t spans = g.K / QFmt<8>::SPAN;
-                // parts of at least 4 steps, at most kSharedParts
-                const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(kSharedParts, spans / 4));
-                const int spp = (int)((spans + parts - 1) / parts);
-                const int64_t waves = g.N / 16 * parts;
-                dense_parts_kernel<8><<<(unsigned)((waves + kWaves - 1) / kWaves), kThreads, 0, ss->s>>>(g, spp, parts,
-                                                                                                        part);
-                const int64_t outs = M * (swi ? g.N / 2 : g.N);
-                if (swi)
-                    dense_parts_finish<true><<<(unsigned)((outs + kThreads - 1) / kThreads), kThreads, 0, ss->s>>>(
-                        part, parts, M, g.N, out);
-                else
-                    dense_parts_finish<false><<<(unsigned)((outs + kThreads - 1) / kThreads), kThreads, 0, ss->s>>>(
-                        part, parts, M, g.N, out);
-            };
-            split(a, true, sh_h);
-            split(b, false, sh_s);
         } else {
             launch_gemm<8, DENSE, EPI_SWIGLU, false, false, false>(a, (M + 15) / 16, ss->s);
             launch_gemm<8, DENSE, EPI_BF16, false, false, false>(b, (M + 15) / 16, ss->s);
@@ -1319,7 +1425,11 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     if (routed) {
         moe_group_routes(ids, M, k, E, route, L.route_bytes, err_expert, stream);
     } else if (M * k <= 1024) {  // one launch: top-k and packing with the ids kept in LDS
-        moe_topk_group_routes_small(lg, ld, M, E, k, ids, coef, route, L.route_bytes, err_router, err_expert, stream);
+        if (fold)
+            launch_topk_route_shared(lg, ld, M, E, k, ids, coef, route, L.route_bytes, err_router, err_expert, sh_gu,
+                                     sh_gu_spp, sh_gu_parts, sh_part, stream);
+        else
+            moe_topk_group_routes_small(lg, ld, M, E, k, ids, coef, route, L.route_bytes, err_router, err_expert, stream);
     } else {
         moe_router(lg, ld, M, E, k, nullptr, 0, 0, ids, coef, Act::F32, err_router, stream);
         moe_group_routes(ids, M, k, E, route, L.route_bytes, err_expert, stream);
@@ -1329,8 +1439,18 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     const Q8DeviceView gu8{w.gate_up.q, w.gate_up.scale, w.gate_up.minv, w.gate_up.N, w.gate_up.K, w.gate_up.G};
     const Q8DeviceView dn8{w.down.q, w.down.scale, w.down.minv, w.down.N, w.down.K, w.down.G};
     // h in bf16: the oracle's rounding of silu(g) * u, with bf16's range (the f16 form is the reference API's option)
-    if (q8) linear_q8_experts_gather_grouped_swiglu(x, gu8, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
-    else linear_q4_experts_gather_grouped_swiglu(x, w.gate_up, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
+    if (fold) {
+        const QV gv = q8 ? qv(gu8) : qv(w.gate_up);
+        check_grouped(fn, x, gv, E, route, L.route_bytes, M, k, h, Act::BF16, M * k * I * 2, M);
+        GemmArgs a = make_args(gv, E, x, h, I);
+        a.A = k, a.ws = static_cast<const int32_t *>(route), a.S = M * k;
+        if (q8) launch_gemm<8, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, k, E), stream, &sh_jobs[0]);
+        else launch_gemm<4, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, k, E), stream, &sh_jobs[0]);
+    } else if (q8) {
+        linear_q8_experts_gather_grouped_swiglu(x, gu8, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
+    } else {
+        linear_q4_experts_gather_grouped_swiglu(x, w.gate_up, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
+    }
     {
         const QV dv = q8 ? qv(dn8) : qv(w.down);
         check_view(fn, dv, E);
@@ -1339,13 +1459,17 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         if (use_expert_gemm(M * k, E, dv.K, dv.G)) {
             if (q8) launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
             else launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
-        } else if (q8) launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream);
-        else launch_gemm<4, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream);
+        } else if (q8) {
+            launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream, fold ? &sh_jobs[1] : nullptr);
+        } else {
+            launch_gemm<4, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream, fold ? &sh_jobs[1] : nullptr);
+        }
     }
     if (ss) STRIX_HIP_CHECK(hipStreamWaitEvent(stream, ss->join, 0), fn, ": join wait");
     const MoeSharedAdd sh{sh_s, lg + E, ld, (uint32_t)E, err_router};
     combine_reduce(partial, ids, coef, M, k, E, H, static_cast<uint16_t *>(y), w.has_shared ? &sh : nullptr,
-                   static_cast<const uint16_t *>(x), static_cast<uint16_t *>(x_out), stream);
+                   static_cast<const uint16_t *>(x), static_cast<uint16_t *>(x_out), stream, fold ? sh_part : nullptr,
+                   fold ? sh_jobs[1].parts : 0);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " E=", E, " k=", k);
 }
 

@@ -7,168 +7,16 @@
 // equal buckets in lane order and one leader lane updates the bucket's count - no atomics, so the placement is the
 // stable order by construction. Small S (<= 16 chunks) runs as one 1024-thread block with everything in LDS; larger S
 // as three launches (chunk histograms, scan, placement) through the workspace.
-#include "common.hpp"
-#include "topk.hpp"
+#include "route_small.hpp"
 
-#include <algorithm>
-#include <climits>
 #include <type_traits>
 
 namespace strix::kernels {
-
-namespace route {
-
-constexpr int kWave = 64;
-constexpr int kChunk = 256;          // slots per wave chunk
-constexpr int kSmallWaves = 16;      // the one-block path: 1024 threads
-constexpr int kTileRows = 16;        // slots per tile of the grouped expert kernels
-constexpr int kWideRows = 64;        // slots per wide tile (kept for the large-M kernels)
-constexpr int kRec16 = 4 + kTileRows; // ints per 16-slot tile record
-
-struct Layout {
-    int64_t S, E, T16, T64, nch;
-    __host__ __device__ int64_t offsets() const { return 4; }
-    __host__ __device__ int64_t slots() const { return offsets() + E + 2; }
-    // 16-slot tile records {bucket, first index into slots, rows, 0, slot[16] (-1 past rows)}: everything an
-    // expert kernel needs about a tile in independent loads; 64-slot tiles {bucket, first index, rows, 0}
-    __host__ __device__ int64_t t16_rec() const { return (slots() + S + 3) / 4 * 4; }
-    __host__ __device__ int64_t t64_rec() const { return t16_rec() + kRec16 * T16; }
-    __host__ __device__ int64_t hist() const { return t64_rec() + 4 * T64; }       // [nch][E + 1]
-    __host__ __device__ int64_t bad() const { return hist() + nch * (E + 1); }    // [nch]
-    __host__ __device__ int64_t ints() const { return bad() + nch; }
-};
-
-inline Layout layout(int64_t M, int64_t A, int64_t E) {
-    const int64_t S = M * A;
-    // sum over buckets of ceil(count / R) <= min(S, S / R + (E + 1)): a tile holds at least one slot
-    const int64_t t16 = std::min(S, S / kTileRows + E + 2), t64 = std::min(S, S / kWideRows + E + 2);
-    return {S, E, t16, t64, (S + kChunk - 1) / kChunk};
-}
-
-}  // namespace route
 
 namespace {
 
 using namespace route;
 
-__device__ __forceinline__ int bucket_of(int32_t id, int E) { return (id < 0 || id >= E) ? E : id; }
-
-// Lanes of the wave whose (valid) bucket equals this lane's: a ballot per bucket bit.
-__device__ __forceinline__ uint64_t match_bucket(int b, bool valid, int nbits) {
-    uint64_t m = __ballot(valid);
-    for (int bit = 0; bit < nbits; ++bit) {
-        const bool one = (b >> bit) & 1;
-        const uint64_t bb = __ballot(one);
-        m &= one ? bb : ~bb;
-    }
-    return m;
-}
-
-__device__ __forceinline__ uint64_t lanes_below() { return (1ull << (threadIdx.x % kWave)) - 1ull; }
-
-// Histogram of chunk [s0, s1) into the wave-private counters h[E + 1] (zeroed by the caller); returns the chunk's
-// smallest invalid slot (INT_MAX if none) on every lane.
-__device__ int chunk_hist(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *h) {
-    const int lane = threadIdx.x % kWave;
-    int first_bad = INT_MAX;
-    for (int64_t base = s0; base < s1; base += kWave) {
-        const int64_t s = base + lane;
-        const bool valid = s < s1;
-        const int32_t id = valid ? ids[s] : 0;
-        const int b = bucket_of(id, E);
-        const uint64_t same = match_bucket(b, valid, nbits);
-        if (valid && (same & lanes_below()) == 0) h[b] += __popcll(same);
-        if (valid && b == E && (int)s < first_bad) first_bad = (int)s;
-    }
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, off, kWave));
-    return first_bad;
-}
-
-// Stable placement of chunk [s0, s1) through the wave-private cursors c[E + 1] (each at the bucket's first free
-// position for this chunk).
-__device__ void chunk_place(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *c, int32_t *slots) {
-    const int lane = threadIdx.x % kWave;
-    for (int64_t base = s0; base < s1; base += kWave) {
-        const int64_t s = base + lane;
-        const bool valid = s < s1;
-        const int32_t id = valid ? ids[s] : 0;
-        const int b = bucket_of(id, E);
-        const uint64_t same = match_bucket(b, valid, nbits);
-        const int rank = __popcll(same & lanes_below());
-        int cur = 0;
-        if (valid) cur = c[b];
-        if (valid) slots[cur + rank] = (int32_t)s;
-        if (valid && rank == 0) c[b] = cur + __popcll(same);
-    }
-}
-
-// Exclusive scan of three ints over the 1024 threads of a block; totals returned through tot[3].
-__device__ void block_scan3(int (&v)[3], int *wsum /* [16][3] LDS */, int (&tot)[3]) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    int inc[3] = {v[0], v[1], v[2]};
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int o = __shfl_up(inc[j], off, kWave);
-            if (lane >= off) inc[j] += o;
-        }
-    if (lane == kWave - 1)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) wsum[wave * 3 + j] = inc[j];
-    __syncthreads();
-    int before[3] = {0, 0, 0};
-    for (int w = 0; w < (int)(blockDim.x / kWave); ++w)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int t = wsum[w * 3 + j];
-            if (w < wave) before[j] += t;
-            if (w == 0) tot[j] = 0;
-            tot[j] += t;
-        }
-#pragma unroll
-    for (int j = 0; j < 3; ++j) v[j] = before[j] + inc[j] - v[j];
-    __syncthreads();
-}
-
-// Bucket t's offsets and tile tables, given its exclusive prefixes (slots, 16-slot tiles, 64-slot tiles).
-__device__ void write_bucket(int t, int cnt, const int (&pre)[3], int32_t *ws, const Layout &L) {
-    int32_t *offsets = ws + L.offsets();
-    offsets[t] = pre[0];
-    const int n16 = (cnt + kTileRows - 1) / kTileRows, n64 = (cnt + kWideRows - 1) / kWideRows;
-    for (int i = 0; i < n16; ++i)
-        *reinterpret_cast<int4 *>(ws + L.t16_rec() + kRec16 * (pre[1] + i)) =
-            make_int4(t, pre[0] + i * kTileRows, min(kTileRows, cnt - i * kTileRows), 0);
-    for (int i = 0; i < n64; ++i)
-        *reinterpret_cast<int4 *>(ws + L.t64_rec() + 4 * (pre[2] + i)) =
-            make_int4(t, pre[0] + i * kWideRows, min(kWideRows, cnt - i * kWideRows), 0);
-}
-
-// After placement: each 16-slot tile record gets its slots (-1 past its rows). Threads t, t + nthreads, ... of the
-// caller copy entries [t, n_tiles * 16).
-__device__ void fill_tile_slots(int32_t *ws, const Layout &L, int64_t n_tiles, int64_t t, int64_t nthreads) {
-    for (int64_t i = t; i < n_tiles * kTileRows; i += nthreads) {
-        int32_t *rec = ws + L.t16_rec() + kRec16 * (i / kTileRows);
-        const int jj = (int)(i % kTileRows);
-        rec[4 + jj] = jj < rec[2] ? ws[L.slots() + rec[1] + jj] : -1;
-    }
-}
-
-__device__ void write_header(int32_t *ws, const Layout &L, const int (&tot)[3]) {
-    ws[0] = tot[1];
-    ws[1] = (int32_t)L.S;
-    ws[2] = (int32_t)L.E;
-    ws[3] = tot[2];
-    ws[L.offsets() + L.E + 1] = tot[0];
-}
-
-__device__ void report_bad(const int32_t *ids, int first_bad, uint32_t *err) {
-    if (first_bad != INT_MAX && atomicCAS(&err[0], 0u, 1u) == 0u) {
-        err[1] = (uint32_t)ids[first_bad];
-        err[2] = (uint32_t)first_bad;
-    }
-}
 
 // ---- S <= kSmallWaves * kChunk: one block -------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024) route_small_kernel(const int32_t *ids, Layout L, int nbits, int32_t *ws,
@@ -292,87 +140,14 @@ __global__ void __launch_bounds__(256) route_tiles_kernel(Layout L, int32_t *ws)
 }
 
 
-// ---- top-k + packing for small batches (S = M k <= 1024): one 1024-thread block, ids never leave LDS ---------------
-// Phase A: wave w takes tokens w, w + 16, ...: top-k (ids, coef out, and ids into LDS). Phase B: wave w takes slots
-// [64 w, 64 w + 64): histogram, block scan, placement into LDS, then the workspace written from LDS (slots, offsets,
-// tile records). The workspace layout and contents are those of moe_group_routes.
-constexpr int kFusedSlots = 1024;
-
 template <int NV>
 __global__ void __launch_bounds__(1024)
     topk_route_small_kernel(const float *logits, int64_t ld, int M, int E, int k, int32_t *ids_out, float *coef_out,
                             Layout L, int nbits, int32_t *ws, uint32_t *err_router, uint32_t *err_route) {
     extern __shared__ int lds[];
-    const int S = (int)L.S, nb = E + 1, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, t = threadIdx.x;
-    int *sids = lds;                          // [S] ids by slot
-    int *sl = sids + kFusedSlots;             // [S] slots by position
-    int *cnt = sl + kFusedSlots;              // [16][E + 1] wave counts, then cursors
-    int *bstart = cnt + kSmallWaves * nb;     // [E + 1] bucket start
-    int *btile = bstart + nb;                 // [E + 1] bucket's first 16-slot tile
-    int *bcount = btile + nb;                 // [E + 1]
-    int *tile_b = bcount + nb;                // [T16] bucket of a tile
-    int *wsum = tile_b + L.T16;               // [48]
-    int *bad = wsum + 48;                     // [1]
-    // A: top-k
-    for (int m = wave; m < M; m += kSmallWaves) {
-        int id;
-        float cf;
-        const int rb = topk::wave_topk<float, NV>(logits + (int64_t)m * ld, E, k, id, cf);
-        if (rb != INT_MAX) {
-            if (lane == 0 && atomicCAS(&err_router[0], 0u, 1u) == 0u) {
-                err_router[1] = (uint32_t)m;
-                err_router[2] = (uint32_t)rb;
-            }
-            id = -1, cf = dev::qnan();
-        }
-        if (lane < k) {
-            ids_out[m * k + lane] = id;
-            coef_out[m * k + lane] = cf;
-            sids[m * k + lane] = id;
-        }
-    }
-    for (int i = t; i < kSmallWaves * nb; i += blockDim.x) cnt[i] = 0;
-    if (t == 0) *bad = INT_MAX;
-    __syncthreads();
-    // B: histogram of this wave's chunk
-    const int s0 = wave * kWave, s1 = min(s0 + kWave, S);
-    if (s0 < S) {
-        const int fb = chunk_hist(sids, s0, s1, E, nbits, cnt + wave * nb);
-        if (lane == 0 && fb != INT_MAX) atomicMin(bad, fb);
-    }
-    __syncthreads();
-    int c = 0;
-    if (t <= E)
-        for (int w = 0; w < kSmallWaves; ++w) c += cnt[w * nb + t];
-    int v[3] = {c, (c + kTileRows - 1) / kTileRows, (c + kWideRows - 1) / kWideRows}, tot[3];
-    block_scan3(v, wsum, tot);
-    if (t <= E) {
-        write_bucket(t, c, v, ws, L);
-        bstart[t] = v[0], btile[t] = v[1], bcount[t] = c;
-        for (int i = 0; i < (c + kTileRows - 1) / kTileRows; ++i) tile_b[v[1] + i] = t;
-        int run = v[0];
-        for (int w = 0; w < kSmallWaves; ++w) {
-            const int x = cnt[w * nb + t];
-            cnt[w * nb + t] = run;
-            run += x;
-        }
-    }
-    if (t == 0) {
-        write_header(ws, L, tot);
-        // the ids live in LDS here: report_bad reads them through this pointer
-        report_bad(sids, *bad, err_route);
-    }
-    __syncthreads();
-    if (s0 < S) chunk_place(sids, s0, s1, E, nbits, cnt + wave * nb, sl);
-    __syncthreads();
-    for (int i = t; i < S; i += blockDim.x) ws[L.slots() + i] = sl[i];
-    // tile records' slot lists from LDS: thread per (tile, slot)
-    for (int i = t; i < tot[1] * kTileRows; i += blockDim.x) {
-        const int ti = i / kTileRows, jj = i % kTileRows, b = tile_b[ti], r = ti - btile[b];
-        const int rows = min(kTileRows, bcount[b] - r * kTileRows);
-        ws[L.t16_rec() + kRec16 * ti + 4 + jj] = jj < rows ? sl[bstart[b] + r * kTileRows + jj] : -1;
-    }
+    topk_route_small_body<NV>(logits, ld, M, E, k, ids_out, coef_out, L, nbits, ws, err_router, err_route, lds);
 }
+
 
 }  // namespace
 
@@ -425,8 +200,7 @@ void moe_topk_group_routes_small(const float *logits, int64_t ld, int64_t M, int
     const route::Layout L = route::layout(M, k, E);
     int nbits = 0;
     while ((1ll << nbits) <= E) ++nbits;
-    const size_t lds = ((size_t)2 * kFusedSlots + (size_t)route::kSmallWaves * (E + 1) + 3 * (size_t)(E + 1) +
-                        (size_t)L.T16 + 48 + 1) * 4;
+    const size_t lds = route::topk_route_small_lds(L);
     const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
     auto go = [&](auto nvc) {
         topk_route_small_kernel<decltype(nvc)::value><<<1, 1024, lds, stream>>>(
