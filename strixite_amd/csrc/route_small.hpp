@@ -196,7 +196,9 @@ __device__ inline void topk_route_small_body(const float *logits, int64_t ld, in
             sids[m * k + lane] = id;
         }
     }
-    for (int i = t; i < kSmallWaves * nb; i += blockDim.x) cnt[i] = 0;
+    // only the waves that hold slots (chunks of 64) count: their counters are the only ones cleared and summed
+    const int nw = (S + kWave - 1) / kWave;
+    for (int i = t; i < nw * nb; i += blockDim.x) cnt[i] = 0;
     if (t == 0) *bad = INT_MAX;
     __syncthreads();
     // B: histogram of this wave's chunk
@@ -208,7 +210,7 @@ __device__ inline void topk_route_small_body(const float *logits, int64_t ld, in
     __syncthreads();
     int c = 0;
     if (t <= E)
-        for (int w = 0; w < kSmallWaves; ++w) c += cnt[w * nb + t];
+        for (int w = 0; w < nw; ++w) c += cnt[w * nb + t];
     int v[3] = {c, (c + kTileRows - 1) / kTileRows, (c + kWideRows - 1) / kWideRows}, tot[3];
     block_scan3(v, wsum, tot);
     if (t <= E) {
@@ -216,7 +218,7 @@ __device__ inline void topk_route_small_body(const float *logits, int64_t ld, in
         bstart[t] = v[0], btile[t] = v[1], bcount[t] = c;
         for (int i = 0; i < (c + kTileRows - 1) / kTileRows; ++i) tile_b[v[1] + i] = t;
         int run = v[0];
-        for (int w = 0; w < kSmallWaves; ++w) {
+        for (int w = 0; w < nw; ++w) {
             const int x = cnt[w * nb + t];
             cnt[w * nb + t] = run;
             run += x;
