@@ -32,7 +32,8 @@ template <int BITS> struct Chunk {
 };
 }  // namespace gemm
 
-template <int BITS, int MODE, int EPI, bool XROW_DIV, bool HF16, bool G1>
+// CPG: K chunks a quantization group (1 or 2, known at compile time; 0: a.G / BK at run time)
+template <int BITS, int MODE, int EPI, bool XROW_DIV, bool HF16, int CPG>
 __global__ void __launch_bounds__(gemm::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     expert_gemm_kernel(GemmArgs a, int64_t tiles_bound, int64_t rec64, uint32_t q_bytes, uint32_t s_bytes,
                        uint32_t x_bytes, uint32_t y_bytes) {
@@ -70,7 +71,7 @@ __global__ void __launch_bounds__(gemm::kThreads) __attribute__((amdgpu_waves_pe
     const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, x_bytes), rq = rsrc(a.q, q_bytes), rs = rsrc(a.scale, s_bytes),
                                  rm = rsrc(a.minv, s_bytes), ry = rsrc(a.y, y_bytes);
     const uint32_t K = (uint32_t)a.K, groups = (uint32_t)(a.K / a.G);
-    const int chunks = (int)(a.K / BK), cpg = G1 ? 1 : (int)(a.G / BK);  // chunks, chunks a group
+    const int chunks = (int)(a.K / BK), cpg = CPG > 0 ? CPG : (int)(a.G / BK);  // chunks, chunks a group
     // this thread's activation rows (t / 8, t / 8 + 32)
     uint32_t xoff[2];
 #pragma unroll
@@ -171,9 +172,11 @@ __global__ void __launch_bounds__(gemm::kThreads) __attribute__((amdgpu_waves_pe
     };
 
     // one chunk: activations -> LDS, prefetch chunk c + PF into the same registers, MFMAs, rescale at a group's end
-    auto run = [&](int c, Chunk<BITS> &ch) __attribute__((always_inline)) {
+    // p: the chunk's place in the prefetch trip (c = trip start + p, trip starts a multiple of PF and of CPG)
+    auto run = [&](int c, Chunk<BITS> &ch, int p) __attribute__((always_inline)) {
         const int gi = c / cpg;
-        const bool closes = G1 || c % cpg == cpg - 1;
+        const bool first = CPG > 0 ? p % CPG == 0 : c % cpg == 0;
+        const bool closes = CPG > 0 ? p % CPG == CPG - 1 : c % cpg == cpg - 1;
         uint16_t *as = As[c & 1];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -200,8 +203,8 @@ __global__ void __launch_bounds__(gemm::kThreads) __attribute__((amdgpu_waves_pe
             }
             const uint4 vw = *reinterpret_cast<const uint4 *>(&as[(16 * wave + j) * LDA + 16 * g + 8 * ks]);
             const Frag aw{{vw.x, vw.y, vw.z, vw.w}};
-            // one chunk a group: its first K step starts the partials from zero (an inline operand, no clearing)
-            if (G1 && ks == 0) {
+            // a group's first K step starts the partials from zero (an inline operand, no clearing)
+            if (first && ks == 0) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -226,13 +229,6 @@ __global__ void __launch_bounds__(gemm::kThreads) __attribute__((amdgpu_waves_pe
             }
             // this wave's tile of the group's token sums, for the window's tail
             xsum[(gi / GW) & 1][gi % GW][16 * wave + j] = sx[0];
-            if constexpr (!G1) {
-                sx = float4v{0, 0, 0, 0};
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) d[i][u] = float4v{0, 0, 0, 0};
-            }
 
         }
     };
@@ -250,7 +246,7 @@ __global__ void __launch_bounds__(gemm::kThreads) __attribute__((amdgpu_waves_pe
     // whole trips: a chunk past K loads zeros and adds exactly 0 (its codes meet zero activations, its scales are 0)
     for (int c = 0; c < chunks; c += PF) {
 #pragma unroll
-        for (int p = 0; p < PF; ++p) run(c + p, ch[p]);
+        for (int p = 0; p < PF; ++p) run(c + p, ch[p], p);
     }
     __syncthreads();
     tail(((int)groups - 1) / GW);
@@ -310,8 +306,10 @@ void launch_expert_gemm(const GemmArgs &a, hipStream_t stream) {
     STRIX_CHECK(blocks < (1ll << 31), "expert gemm: grid of ", blocks, " blocks");
     const int64_t rec64 = MODE == GROUPED ? t64_rec_at(a.S, a.E) : 0;
     // a group of one chunk (G == 64, the formats' group size) has its own kernel: no partial clearing
-    auto kern = a.G == BK ? expert_gemm_kernel<BITS, MODE, EPI, XROW_DIV, HF16, true>
-                          : expert_gemm_kernel<BITS, MODE, EPI, XROW_DIV, HF16, false>;
+    static_assert(PF % 2 == 0, "a prefetch trip holds whole two-chunk groups");
+    auto kern = a.G == BK ? expert_gemm_kernel<BITS, MODE, EPI, XROW_DIV, HF16, 1>
+                : a.G == 2 * BK ? expert_gemm_kernel<BITS, MODE, EPI, XROW_DIV, HF16, 2>
+                                : expert_gemm_kernel<BITS, MODE, EPI, XROW_DIV, HF16, 0>;
     const size_t lds = (size_t)2 * BN * table_stride((int)(a.K / a.G)) * 2;
     kern<<<(unsigned)blocks, gemm::kThreads, lds, stream>>>(a, tiles_bound, rec64, (uint32_t)q_bytes, (uint32_t)s_bytes,
                                                           (uint32_t)x_bytes, (uint32_t)y_bytes);
