@@ -224,6 +224,68 @@ def experts_down(h, view: QView, E, ids, threads=None):
     return p
 
 
+# ---- the reference's F16 matrix-unit math (MoeMath::WmmaF16 kinds, Q4 experts) -----------------------------------
+# strixite kernels/moe_grouped.hpp:32-33 and moe_grouped.hip:348-351: x rounded to F16 toward zero, each weight one
+# F16 rounding of code * s + m with s and m rounded to F16, products summed in FP32 over all of K. numpy only: the
+# sums here run in float64 (the GPU's FP32 order differs; tests allow for that).
+def bf16_to_f16_rtz(b: np.ndarray) -> np.ndarray:
+    """BF16 bits -> F16 rounded toward zero (strixite kernels/moe_grouped.hip:30-32, v_cvt_pkrtz of the value)."""
+    v = bf16_to_f32(np.asarray(b, dtype=np.uint16))
+    with np.errstate(over="ignore"):
+        h = v.astype(np.float16)  # round to nearest even ...
+    up = np.abs(h.astype(np.float32)) > np.abs(v)  # ... stepped back one F16 ulp where it rounded away from zero
+    h[up] = np.nextafter(h[up], np.float16(0))
+    return h
+
+
+def q4_codes(q: np.ndarray, N: int, K: int) -> np.ndarray:
+    """[N, K] Q4 codes: code 2j in the low nibble of byte j of a row, 2j + 1 in the high (formats/q4.cpp)."""
+    b = np.asarray(q, dtype=np.uint8).reshape(N, K // 2)
+    c = np.empty((N, K), dtype=np.uint8)
+    c[:, 0::2], c[:, 1::2] = b & 0x0F, b >> 4
+    return c
+
+
+def q4_weights_f16(q, s, m, N: int, K: int, G: int) -> np.ndarray:
+    """[N, K] F16 weights f16(code * f16(s) + f16(m)), one rounding (strixite kernels/wmma_gemm.hpp:116-141).
+    code * s + m is exact in float64 (5 x 11 significant bits, exponents within F16's range), so numpy's correctly
+    rounded float64 -> float16 conversion is the F16 FMA's result."""
+    s16 = bf16_to_f32(np.asarray(s, dtype=np.uint16)).astype(np.float16).astype(np.float64).reshape(N, K // G, 1)
+    m16 = bf16_to_f32(np.asarray(m, dtype=np.uint16)).astype(np.float16).astype(np.float64).reshape(N, K // G, 1)
+    w = q4_codes(q, N, K).astype(np.float64).reshape(N, K // G, G) * s16 + m16
+    return w.astype(np.float16).reshape(N, K)
+
+
+def _f16_grouped(x_rows, w16, E, ids, row_of_slot):
+    """FP32 outputs [M * A, N] of slot s = x16[row_of_slot(s)] . W16[ids[s]]^T (float64 sums rounded once)."""
+    N = w16.shape[0] // E
+    x16 = bf16_to_f16_rtz(x_rows).astype(np.float64)
+    flat = np.asarray(ids).ravel()
+    out = np.full((flat.size, N), np.nan, dtype=np.float32)
+    for e in np.unique(flat):
+        sl = np.nonzero(flat == e)[0]
+        if 0 <= e < E:
+            out[sl] = (x16[row_of_slot(sl)] @ w16[e * N:(e + 1) * N].astype(np.float64).T).astype(np.float32)
+    return out
+
+
+def experts_gate_up_swiglu_f16math(x, bits, q, s, m, N_total, K, G, E, ids):
+    """h [M * A, I] (BF16 bits) = bf16(silu(g) * u) of the F16 math (strixite kernels/moe_grouped.hip:354, 348-351)."""
+    assert bits == 4, "F16 matrix-unit math: Q4 experts"
+    A = ids.shape[1]
+    gu = _f16_grouped(x, q4_weights_f16(q, s, m, N_total, K, G), E, ids, lambda sl: sl // A)
+    I = gu.shape[1] // 2
+    g, u = gu[:, :I], gu[:, I:]
+    with np.errstate(over="ignore", invalid="ignore"):
+        return f32_to_bf16((g / (np.float32(1) + np.exp(-g))) * u)
+
+
+def experts_down_f16math(h, bits, q, s, m, N_total, K, G, E, ids):
+    """FP32 per-slot down outputs [M * A, N] of the F16 math (h BF16 bits, slot rows)."""
+    assert bits == 4, "F16 matrix-unit math: Q4 experts"
+    return _f16_grouped(h, q4_weights_f16(q, s, m, N_total, K, G), E, ids, lambda sl: sl)
+
+
 def dense(x, view: QView, threads=None):
     M = x.shape[0]
     y = np.empty((M, view.N), dtype=np.float32)

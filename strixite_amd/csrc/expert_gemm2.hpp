@@ -1,0 +1,349 @@
+// Prefill-size grouped projections of the Q4 (g128) experts in the reference's F16 matrix-unit math: included by
+// experts.hip after expert_gemm.hpp (it uses GemmArgs, the epilogues, the buffer-load helpers and the 64-slot tile
+// records).
+//
+// The math is MoeMath::WmmaF16's for Q4 experts (strixite kernels/moe_grouped.hpp:32-33, moe_grouped.hip:348-351): x
+// rounded to F16 toward zero (exact for BF16 values in F16's normal range; strixite kernels/moe_grouped.hip:30-32),
+// each weight dequantized to F16 in registers as one F16 FMA code * s + m of the group's scale and min rounded to F16
+// (strixite kernels/wmma_gemm.hpp:116-141), FP32 accumulation over all of K. There are no per-group partials
+// (expert_gemm_kernel keeps the weights exact and rescales every group on the FP32 accumulators), so a wave holds
+// 128 tokens x 64 weight rows in 8 v_mfma_f32_32x32x16_f16 tiles and each decoded fragment feeds up to 4 MFMAs.
+//
+// Block: 4 waves, BM = 128 token slots (two consecutive 64-slot tile records of one expert's bucket) x BN = 256 weight
+// rows (SwiGLU: 128 gate rows and the matching 128 up rows, a wave 32 + 32; otherwise a wave 64 consecutive rows).
+// K runs in chunks of 64, two per quantization group. The block's activations (gathered by slot) reach LDS two
+// chunks ahead: X16 (x already F16 in the paired order below) straight from memory into one of three LDS buffers;
+// otherwise (BF16 x) through registers, converted there, into one of two. The 16-byte columns of an LDS row are
+// XOR-swizzled by the row, so the MFMA reads are conflict-free. Each lane loads its weight row's 32 codes of a chunk
+// (16 bytes) two chunks ahead. A block whose slots fill fewer than 4 of its 32-token sub-tiles runs a K loop for just
+// the live ones.
+//
+// The k order of an MFMA operand: lane half h takes k 32 h .. 32 h + 31 of a chunk and K step ks the 8 at
+// 32 h + 8 ks, whose 8 halves hold k = 0, 4, 1, 5, 2, 6, 3, 7 of that block (the paired order), for the activations
+// and the weights alike (an MFMA sums over k in any order both operands share). In that order a dword of 8 Q4 codes
+// (code i at bits 4 i) gives each F16 pair in one and-or: pair j = bits 4 j and 16 + 4 j.
+#pragma once
+
+namespace g2 {
+constexpr int BM = 128, BN = 256, BK = 64, kThreads = 256;
+// h forms of the SwiGLU epilogue: BF16, F16 (natural order), F16 in the paired order (an X16 input)
+enum HForm { H_BF16 = 0, H_F16 = 1, H_F16P = 2 };
+}  // namespace g2
+
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float16v mfma32_f16(const Frag &a, const Frag &b, float16v c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c, 0,
+                                                  0, 0);
+}
+
+// a BF16 scale or min as an F16 pair (round to nearest even)
+__device__ __forceinline__ f16x2v bf16_to_f16x2(uint16_t b) {
+    const _Float16 h = (_Float16)bf16_to_f32(b);
+    return f16x2v{h, h};
+}
+
+__device__ __forceinline__ uint32_t pk_f16_rtz(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
+// position of k (0..7) of an 8-element block in the paired order
+__host__ __device__ constexpr int paired_pos(int k) { return (k % 4) * 2 + k / 4; }
+
+// 8 Q4 codes -> F16 code * s + m (one F16 FMA each) in the paired order. A code n under the F16 exponent of 1024
+// (bias = 0x64006400: 0x6400 | n = 1024 + n exactly) loses 1024 exactly, then the FMA rounds once.
+__device__ __forceinline__ Frag q4_dequant_f16(uint32_t w, f16x2v s, f16x2v m, uint32_t bias) {
+    const f16x2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t c = ((w >> (4 * j)) & 0x000F000Fu) | bias;
+        f.d[j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2v, c) - k1024, s, m));
+    }
+    return f;
+}
+
+// 8 BF16 activations in natural k order -> F16 toward zero in the paired order
+__device__ __forceinline__ uint4 bf16x8_to_f16_paired(const uint4 &v) {
+    auto lo = [](uint32_t d) { return __uint_as_float(d << 16); };
+    auto hi = [](uint32_t d) { return __uint_as_float(d & 0xFFFF0000u); };
+    return make_uint4(pk_f16_rtz(lo(v.x), lo(v.z)), pk_f16_rtz(hi(v.x), hi(v.z)), pk_f16_rtz(lo(v.y), lo(v.w)),
+                      pk_f16_rtz(hi(v.y), hi(v.w)));
+}
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// [rows, K] BF16 -> F16 toward zero in the paired order (the X16 input of the gate_up projection); n8 = rows * K / 8
+__global__ void __launch_bounds__(256) bf16_to_f16_paired_kernel(const uint4 *x, uint4 *y, int64_t n8) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = bf16x8_to_f16_paired(x[i]);
+}
+
+template <int EPI, bool XROW_DIV, int HF, bool X16>
+__global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+    expert_gemm2_kernel(GemmArgs a, int64_t tiles_bound, int64_t col_blocks, int64_t rec64, uint32_t q_bytes,
+                        uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
+    using namespace g2;
+    constexpr bool SWI = EPI == EPI_SWIGLU;
+    constexpr int NB = X16 ? 3 : 2;  // LDS activation buffers
+    // the activation buffers [row * 8 + (col ^ (row & 7))], separate arrays picked at compile time: the compiler
+    // then tells a read of one from the loads still landing in another and waits for those loads no longer than it
+    // must
+    __shared__ __attribute__((aligned(16))) uint4 As0[BM * BK / 8], As1[BM * BK / 8], As2[X16 ? BM * BK / 8 : 1];
+    auto abuf = [&](int i) __attribute__((always_inline)) -> uint4 * { return i == 0 ? As0 : i == 1 ? As1 : As2; };
+    __shared__ int32_t orow[BM];
+    const int tid = threadIdx.x, lane = tid % kWave, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int h = lane / 32, l32 = lane % 32;
+
+    // the item: blocks are dealt to the 8 XCDs round-robin (block b to XCD b % 8). XCD x takes records x, x + 8, ..
+    // in turn and the column blocks of each consecutively, so the column blocks of one token tile run together on
+    // one XCD and read its activations through the same L2, while consecutive records (one expert's tiles) spread
+    // over the XCDs. A block takes two 64-slot records of one bucket (the even-indexed one).
+    const int64_t j = blockIdx.x / 8, rec = 8 * (j / col_blocks) + blockIdx.x % 8, cb = j % col_blocks;
+    if (rec >= tiles_bound) return;
+    const int64_t n64 = a.ws[3] < tiles_bound ? a.ws[3] : tiles_bound;
+    if (rec >= n64) return;  // uniform per block, before any barrier
+    const int4 r0 = *reinterpret_cast<const int4 *>(a.ws + rec64 + 4 * rec);
+    const int32_t bucket = __builtin_amdgcn_readfirstlane(r0.x), start = __builtin_amdgcn_readfirstlane(r0.y);
+    const bool nan = bucket < 0 || bucket >= a.E;
+    const int32_t first = a.ws[4 + (bucket < 0 ? 0 : bucket > a.E ? a.E : bucket)];  // offsets[bucket] (header: 4)
+    if (((start - first) / 64) % 2 != 0) return;  // the previous record's block covers this one
+    int32_t rows = r0.z;
+    if (rec + 1 < n64) {
+        const int4 r1 = *reinterpret_cast<const int4 *>(a.ws + rec64 + 4 * (rec + 1));
+        if (r1.x == bucket) rows += r1.z;
+    }
+    rows = __builtin_amdgcn_readfirstlane(rows);
+    const uint32_t expert = nan ? 0u : (uint32_t)bucket;
+    const int32_t *slots = a.ws + route::slots_at(a.E) + start;
+    if (tid < BM) orow[tid] = tid < rows ? slots[tid] : -1;
+
+    const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, x_bytes), rq = rsrc(a.q, q_bytes), rs = rsrc(a.scale, s_bytes),
+                                 rm = rsrc(a.minv, s_bytes), ry = rsrc(a.y, y_bytes);
+    const uint32_t K = (uint32_t)a.K, groups = (uint32_t)(a.K / a.G);
+    const int chunks = (int)(a.K / BK);  // even: two a group
+    // this thread's activation pieces: LDS slots tid + 256 v (v = 0..3) = row / 8, column ^ (row & 7)
+    uint32_t xoff[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int slot = tid + 256 * v, row = slot / 8, col = (slot % 8) ^ (row & 7);
+        const int32_t s = row < rows ? slots[row] : -1;
+        xoff[v] = s >= 0 ? ((XROW_DIV ? (uint32_t)s / (uint32_t)a.A : (uint32_t)s) * K + col * 8) * 2 : x_bytes;
+    }
+    // this wave's two weight-row tiles (32 rows each): SwiGLU gate rows c0 + 32 w .. and the matching up rows;
+    // otherwise rows 256 cb + 64 w + 32 t ..; a row past the projection's rows reads the last one (not stored)
+    const int64_t nrows = SWI ? a.N / 2 : a.N;
+    int64_t col0[2];
+    uint32_t wrow[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        col0[t] = SWI ? cb * (BN / 2) + 32 * wave : cb * BN + 64 * wave + 32 * t;
+        const int64_t c = col0[t] + l32, cl = c < nrows ? c : nrows - 1;
+        wrow[t] = expert * (uint32_t)a.N + (uint32_t)(SWI && t == 1 ? a.N / 2 + cl : cl);
+    }
+    const uint32_t qoff[2] = {wrow[0] * (K / 2) + 16 * h, wrow[1] * (K / 2) + 16 * h};
+    const uint32_t soff[2] = {wrow[0] * groups * 2, wrow[1] * groups * 2};
+    // this lane's LDS fragment of K step ks in a buffer: row 32 i + l32 (row & 7 = l32 & 7), 16-byte column 4 h + ks
+    int aofs[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) aofs[ks] = l32 * 8 + ((4 * h + ks) ^ (l32 & 7));
+    uint32_t bias;  // in a VGPR, so the and-or takes the mask as its one scalar operand
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(bias));
+
+    // Loads past the last chunk read in-bounds or zero data that is never used. X16: every chunk issues the same
+    // loads in the same order (scales at a group's first chunk, then codes and activations two chunks ahead), so the
+    // activations of chunk c are in LDS once at most 6 (c even) or 10 (c odd) later loads are outstanding.
+    uint4 ar[2][4];  // !X16: activations in flight
+    constexpr int QPF = 2;  // chunks of codes in flight
+    uint4 qr[QPF][2];
+    auto load_a = [&](int c, uint4 (&dst)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dst[v] = bld16(rx, xoff[v], (uint32_t)c * BK * 2);
+    };
+    auto dma_a = [&](int c, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) lds_load16(rx, abuf(buf) + 256 * v + 64 * wave, xoff[v], (uint32_t)c * BK * 2);
+    };
+    auto load_q = [&](int c, uint4 (&dst)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) dst[t] = bld16(rq, qoff[t], (uint32_t)c * (BK / 2));
+    };
+    auto store_a = [&](const uint4 (&src)[4], int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) abuf(buf)[tid + 256 * v] = bf16x8_to_f16_paired(src[v]);
+    };
+    // scale and min of the current group for the two tiles (F16 pairs); the next group's raw bf16 loaded a group ahead
+    f16x2v sc[2], mn[2];
+    uint16_t sraw[2], mraw[2];
+    auto load_sm = [&](int gi) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t o = gi < (int)groups ? soff[t] + 2 * (uint32_t)gi : s_bytes;
+            sraw[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0);
+            mraw[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rm, o, 0, 0);
+        }
+    };
+    load_sm(0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (X16) {
+        load_q(0, qr[0]);
+        dma_a(0, 0);
+        load_q(1, qr[1]);
+        dma_a(1, 1);
+    } else {
+        load_a(0, ar[0]);
+        load_a(1, ar[1]);
+        load_q(0, qr[0]);
+        load_q(1, qr[1]);
+        store_a(ar[0], 0);
+        load_a(2, ar[0]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // the K loop and the epilogue for NT live 32-token sub-tiles (the block's slots, rounded up); K in trips of the
+    // two chunks of a group
+    auto run = [&](auto nt_c) __attribute__((always_inline)) {
+        constexpr int NT = decltype(nt_c)::value;
+        float16v acc[NT][2];
+#pragma unroll
+        for (int i = 0; i < NT; ++i)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) acc[i][t] = float16v{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        // trips of TRIP chunks (X16: 6, so the three buffers' turns are known at compile time)
+        constexpr int TRIP = X16 ? 6 : 2;
+        for (int c0 = 0; c0 < chunks; c0 += TRIP) {
+#pragma unroll
+            for (int pt = 0; pt < TRIP; ++pt) {
+                const int c = c0 + pt, p = pt % 2;
+                if (c >= chunks) break;
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (X16) {
+                    if (p == 0) wait_vmcnt<6>();
+                    else wait_vmcnt<10>();
+                }
+                if (p == 0) {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) sc[t] = bf16_to_f16x2(sraw[t]), mn[t] = bf16_to_f16x2(mraw[t]);
+                    load_sm(c / 2 + 1);
+                }
+                // chunk c's activations are visible; every wave is done with chunk c - 1's buffer. X16: each wave has
+                // waited for its own loads into LDS above; a plain barrier (no fence) keeps the later loads in flight.
+                if constexpr (X16) __builtin_amdgcn_s_barrier();
+                else __syncthreads();
+                __builtin_amdgcn_sched_barrier(0);
+                const uint4 *as = abuf(X16 ? pt % 3 : p);
+                const uint4(&q)[2] = qr[pt % QPF];
+                Frag af[2][NT];
+                auto read_a = [&](int ks, Frag (&dst)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int i = 0; i < NT; ++i) {
+                        const uint4 v = as[aofs[ks] + 256 * i];
+                        dst[i] = Frag{{v.x, v.y, v.z, v.w}};
+                    }
+                };
+                read_a(0, af[0]);
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    if (ks + 1 < 4) read_a(ks + 1, af[(ks + 1) & 1]);
+                    const uint32_t cw0 = ks == 0 ? q[0].x : ks == 1 ? q[0].y : ks == 2 ? q[0].z : q[0].w;
+                    const uint32_t cw1 = ks == 0 ? q[1].x : ks == 1 ? q[1].y : ks == 2 ? q[1].z : q[1].w;
+                    const Frag b0 = q4_dequant_f16(cw0, sc[0], mn[0], bias), b1 = q4_dequant_f16(cw1, sc[1], mn[1], bias);
+#pragma unroll
+                    for (int i = 0; i < NT; ++i) {
+                        acc[i][0] = mfma32_f16(af[ks & 1][i], b0, acc[i][0]);
+                        acc[i][1] = mfma32_f16(af[ks & 1][i], b1, acc[i][1]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                load_q(c + QPF, qr[pt % QPF]);
+                if constexpr (X16) {
+                    dma_a(c + 2, (pt + 2) % 3);  // buffer (c + 2) % 3, last read at chunk c - 1
+                } else {
+                    // the next chunk's activations to the other buffer, then the load of the one after next
+                    store_a(ar[p ^ 1], p ^ 1);
+                    load_a(c + 3, ar[p ^ 1]);
+                }
+            }
+        }
+        wait_vmcnt<0>();  // no load still writing LDS or registers when the wave ends
+
+        // epilogue: lane (h, l32) holds column l32 of each 32 x 32 tile, token rows 8 b + 4 h + i of register 4 b + i
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tok = 32 * i + 8 * (r / 4) + 4 * h + r % 4;
+                const int32_t orw = orow[tok];
+                if constexpr (SWI) {
+                    const int64_t col = col0[0] + l32;
+                    const bool live = orw >= 0 && col < nrows;
+                    // silu with the hardware exp and reciprocal (a few FP32 ulps; h is rounded to 16 bits)
+                    const float g = acc[i][0][r];
+                    const float v = nan ? qnan() : g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * acc[i][1][r];
+                    // F16 forms: the BF16-rounded h toward zero (what a BF16 h converts to on the way into the down)
+                    const uint16_t bits = HF == H_BF16 ? f32_to_bf16(v) : (uint16_t)pk_f16_rtz(bf16_round(v), 0.0f);
+                    const uint32_t cs =
+                        HF == H_F16P ? (uint32_t)((col & ~7) + paired_pos((int)(col & 7))) : (uint32_t)col;
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        bits, ry, live ? ((uint32_t)orw * (uint32_t)a.ldy + cs) * 2 : y_bytes, 0, 0);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const int64_t col = col0[t] + l32;
+                        const bool live = orw >= 0 && col < nrows;
+                        const float v = nan ? qnan() : acc[i][t][r];
+                        const uint32_t e = (uint32_t)orw * (uint32_t)a.ldy + (uint32_t)col;
+                        if constexpr (EPI == EPI_F32)
+                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, live ? e * 4 : y_bytes, 0, 0);
+                        else
+                            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), ry, live ? e * 2 : y_bytes, 0, 0);
+                    }
+                }
+            }
+        }
+    };
+    const int live_tiles = (rows + 31) / 32;
+    if (live_tiles >= 4) run(std::integral_constant<int, 4>{});
+    else if (live_tiles == 3) run(std::integral_constant<int, 3>{});
+    else if (live_tiles == 2) run(std::integral_constant<int, 2>{});
+    else run(std::integral_constant<int, 1>{});
+}
+
+// Launch for Q4 g128 grouped projections (activations BF16, or F16 in the paired order when X16; SwiGLU h in the
+// form HF, or FP32 partials); false when the shape is outside what the kernel takes.
+template <int EPI> bool expert_gemm2_fits(const GemmArgs &a) {
+    return a.G == 2 * g2::BK && a.K % a.G == 0 && (EPI == EPI_SWIGLU ? (a.N / 2) % 32 : a.N % 32) == 0;
+}
+
+template <int EPI, bool XROW_DIV, int HF, bool X16>
+bool launch_expert_gemm2(const GemmArgs &a, hipStream_t stream) {
+    using namespace g2;
+    if (!expert_gemm2_fits<EPI>(a)) return false;
+    const int64_t tiles_bound = std::min(a.S, a.S / 64 + a.E + 2);
+    const int64_t col_blocks = EPI == EPI_SWIGLU ? (a.N / 2 + BN / 2 - 1) / (BN / 2) : (a.N + BN - 1) / BN;
+    const int64_t q_bytes = a.N * a.E * a.K / 2, s_bytes = a.N * a.E * (a.K / a.G) * 2;
+    const int64_t x_bytes = (XROW_DIV ? a.S / a.A : a.S) * a.K * 2;
+    const int64_t y_bytes = a.S * a.ldy * (EPI == EPI_F32 ? 4 : 2);
+    if (q_bytes >= (1ll << 31) || s_bytes >= (1ll << 31) || x_bytes >= (1ll << 31) || y_bytes >= (1ll << 31)) return false;
+    const int64_t blocks = (tiles_bound + 7) / 8 * 8 * col_blocks;  // whole rounds of the 8 XCDs
+    if (blocks >= (1ll << 31)) return false;
+    expert_gemm2_kernel<EPI, XROW_DIV, HF, X16><<<(unsigned)blocks, g2::kThreads, 0, stream>>>(
+        a, tiles_bound, col_blocks, t64_rec_at(a.S, a.E), (uint32_t)q_bytes, (uint32_t)s_bytes, (uint32_t)x_bytes,
+        (uint32_t)y_bytes);
+    return true;
+}
+
+// x [rows, K] BF16 -> F16 paired (the X16 input); K a multiple of 8
+void bf16_to_f16_paired(const void *x, void *y, int64_t rows, int64_t K, hipStream_t stream) {
+    const int64_t n8 = rows * K / 8;
+    const int64_t blocks = std::min<int64_t>((n8 + 255) / 256, 4096);
+    if (blocks > 0)
+        bf16_to_f16_paired_kernel<<<(unsigned)blocks, 256, 0, stream>>>(static_cast<const uint4 *>(x),
+                                                                        static_cast<uint4 *>(y), n8);
+}

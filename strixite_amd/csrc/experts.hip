@@ -669,6 +669,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
 }
 
 #include "expert_gemm.hpp"
+#include "expert_gemm2.hpp"
 
 // Per-slot combine (strixite kernels/linear_q4.hip:283-322): y[m, n] = sum_a coef[m, a] * (h[m, a, :] . Wd[id] row n),
 // the slot dots in FP32 from the MFMA (token row 0 of the tile), summed over a in order with fmaf, rounded once.
@@ -1018,13 +1019,16 @@ int64_t grouped_tiles(int64_t M, int64_t A, int64_t E) { return std::min(M * A, 
 
 // Prefill-size batches (at least 1024 slots and 8 a bucket on average) take the LDS-tiled GEMM: its 64-slot tiles
 // read an expert's weights a quarter as often as the 16-slot stream tiles and keep the matrix cores busy.
+// the reference's F16 matrix-unit kinds (x and the dequantized Q4 weights in F16) against the exact-weight ones
+bool f16_math(MoeMath m) { return m >= MoeMath::WmmaF16; }
+
 bool use_expert_gemm(int64_t S, int64_t E, int64_t K, int64_t G) {
     return S >= 1024 && S >= 8 * E && K % gemm::BK == 0 && G % gemm::BK == 0 && K / G <= gemm::kMaxGroups;
 }
 
 template <typename V>
 void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E, const void *ws, size_t ws_bytes,
-                           int64_t M, int64_t A, void *h, Act act, bool h_f16, hipStream_t stream) {
+                           int64_t M, int64_t A, void *h, Act act, bool h_f16, bool f16, hipStream_t stream) {
     const QV w = qv(wv);
     const int64_t N = w.N / E, I = N / 2;
     check_grouped(fn, x, w, E, ws, ws_bytes, M, A, h, act, M * A * I * 2, M);
@@ -1035,7 +1039,9 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
     const int64_t tiles = grouped_tiles(M, A, E);
     if (use_expert_gemm(M * A, E, w.K, w.G)) {
         if (w.bits == 4) {
-            if (h_f16) launch_expert_gemm<4, GROUPED, EPI_SWIGLU, true, true>(a, stream);
+            if (f16 && (h_f16 ? launch_expert_gemm2<EPI_SWIGLU, true, g2::H_F16, false>(a, stream)
+                              : launch_expert_gemm2<EPI_SWIGLU, true, g2::H_BF16, false>(a, stream))) {
+            } else if (h_f16) launch_expert_gemm<4, GROUPED, EPI_SWIGLU, true, true>(a, stream);
             else launch_expert_gemm<4, GROUPED, EPI_SWIGLU, true, false>(a, stream);
         } else {
             if (h_f16) launch_expert_gemm<8, GROUPED, EPI_SWIGLU, true, true>(a, stream);
@@ -1069,7 +1075,7 @@ void combine_reduce(const float *partial, const int32_t *ids, const float *coef,
 template <typename V>
 void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, const int32_t *ids, const float *coef,
                      const void *ws, size_t ws_bytes, float *partial, int64_t M, int64_t A, void *y, Act act,
-                     const MoeSharedAdd *shared, bool h_f16, hipStream_t stream) {
+                     const MoeSharedAdd *shared, bool h_f16, bool f16, hipStream_t stream) {
     const QV w = qv(wv);
     const int64_t N = w.N / E;
     check_grouped(fn, h, w, E, ws, ws_bytes, M, A, y, act, M * N * 2, M * A);
@@ -1090,8 +1096,10 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
     a.A = A, a.ws = static_cast<const int32_t *>(ws), a.S = M * A;
     const int64_t tiles = grouped_tiles(M, A, E);
     if (!h_f16 && use_expert_gemm(M * A, E, w.K, w.G)) {  // (the GEMM reads bf16 activations only)
-        if (w.bits == 4) launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
-        else launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
+        if (w.bits == 4) {
+            if (!(f16 && launch_expert_gemm2<EPI_F32, false, g2::H_BF16, false>(a, stream)))
+                launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
+        } else launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
     } else if (h_f16) launch_bits<GROUPED, EPI_F32, true, false, false>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_F32, false, false, false>(w.bits, a, tiles, stream);
     combine_reduce(partial, ids, coef, M, A, E, N, static_cast<uint16_t *>(y), shared, nullptr, nullptr, stream);
@@ -1125,31 +1133,33 @@ void linear_q4_experts_gather_grouped(const void *x, const Q4DeviceView &w, int6
 }
 
 void linear_q4_experts_gather_grouped_swiglu(const void *x, const Q4DeviceView &w, int64_t E, const void *ws,
-                                             size_t ws_bytes, int64_t M, int64_t A, void *h, Act act, MoeMath,
+                                             size_t ws_bytes, int64_t M, int64_t A, void *h, Act act, MoeMath math,
                                              hipStream_t stream, bool h_f16) {
-    gather_grouped_swiglu("linear_q4_experts_gather_grouped_swiglu", x, w, E, ws, ws_bytes, M, A, h, act, h_f16, stream);
+    gather_grouped_swiglu("linear_q4_experts_gather_grouped_swiglu", x, w, E, ws, ws_bytes, M, A, h, act, h_f16,
+                          f16_math(math), stream);
 }
 
 void linear_q8_experts_gather_grouped_swiglu(const void *x, const Q8DeviceView &w, int64_t E, const void *ws,
-                                             size_t ws_bytes, int64_t M, int64_t A, void *h, Act act, MoeMath,
+                                             size_t ws_bytes, int64_t M, int64_t A, void *h, Act act, MoeMath math,
                                              hipStream_t stream, bool h_f16) {
-    gather_grouped_swiglu("linear_q8_experts_gather_grouped_swiglu", x, w, E, ws, ws_bytes, M, A, h, act, h_f16, stream);
+    gather_grouped_swiglu("linear_q8_experts_gather_grouped_swiglu", x, w, E, ws, ws_bytes, M, A, h, act, h_f16,
+                          f16_math(math), stream);
 }
 
 void linear_q4_experts_combine_grouped(const void *h, const Q4DeviceView &w, int64_t E, const int32_t *ids,
                                        const float *coef, const void *ws, size_t ws_bytes, float *partial, int64_t M,
-                                       int64_t A, void *y, Act act, MoeMath, hipStream_t stream,
+                                       int64_t A, void *y, Act act, MoeMath math, hipStream_t stream,
                                        const MoeSharedAdd *shared, bool h_f16) {
     combine_grouped("linear_q4_experts_combine_grouped", h, w, E, ids, coef, ws, ws_bytes, partial, M, A, y, act,
-                    shared, h_f16, stream);
+                    shared, h_f16, f16_math(math), stream);
 }
 
 void linear_q8_experts_combine_grouped(const void *h, const Q8DeviceView &w, int64_t E, const int32_t *ids,
                                        const float *coef, const void *ws, size_t ws_bytes, float *partial, int64_t M,
-                                       int64_t A, void *y, Act act, MoeMath, hipStream_t stream,
+                                       int64_t A, void *y, Act act, MoeMath math, hipStream_t stream,
                                        const MoeSharedAdd *shared, bool h_f16) {
     combine_grouped("linear_q8_experts_combine_grouped", h, w, E, ids, coef, ws, ws_bytes, partial, M, A, y, act,
-                    shared, h_f16, stream);
+                    shared, h_f16, f16_math(math), stream);
 }
 
 // ---- per-slot (strixite kernels/linear_q4.hpp:42-61) ----------------------------------------------------------------
@@ -1256,7 +1266,7 @@ namespace strix {
 
 namespace {
 struct LayerWs {
-    int64_t logits, norms, ids, coef, route, h, partial, sh_h, sh_s, sh_part, total;
+    int64_t logits, norms, ids, coef, route, x16, h, partial, sh_h, sh_s, sh_part, total;
     size_t route_bytes;
 };
 int64_t al(int64_t b) { return (b + 255) / 256 * 256; }
@@ -1272,6 +1282,7 @@ LayerWs layer_ws(const MoeLayerWeights &w, int64_t M) {
     L.coef = o, o += al(M * k * 4);
     L.route_bytes = kernels::moe_route_workspace_bytes(M, k, E);
     L.route = o, o += al((int64_t)L.route_bytes);
+    L.x16 = o, o += al(M * k >= 1024 ? M * H * 2 : 0);  // prefill sizes: x as F16 for the Q4 experts' F16 math
     L.h = o, o += al(M * k * I * 2);
     L.partial = o, o += al(M * k * H * 4);
     L.sh_h = o, o += al(w.has_shared ? M * I * 2 : 0);
@@ -1438,8 +1449,21 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     const bool q8 = w.gate_up_bits == 8;
     const Q8DeviceView gu8{w.gate_up.q, w.gate_up.scale, w.gate_up.minv, w.gate_up.N, w.gate_up.K, w.gate_up.G};
     const Q8DeviceView dn8{w.down.q, w.down.scale, w.down.minv, w.down.N, w.down.K, w.down.G};
-    // h in bf16: the oracle's rounding of silu(g) * u, with bf16's range (the f16 form is the reference API's option)
-    if (fold) {
+    // Q4 experts at prefill sizes run the reference's F16 math (MoeMath::WmmaF16): x converted to F16 once, h kept
+    // in F16 (the F16 form of its BF16 rounding), both in the GEMM's paired k order (the down's partials stay FP32)
+    GemmArgs gu2 = make_args(qv(w.gate_up), E, base + L.x16, h, I);
+    gu2.A = k, gu2.ws = static_cast<const int32_t *>(route), gu2.S = M * k;
+    GemmArgs dn2 = make_args(qv(w.down), E, h, partial, H);
+    dn2.A = k, dn2.ws = static_cast<const int32_t *>(route), dn2.S = M * k;
+    const bool f16p = !q8 && !fold && use_expert_gemm(M * k, E, H, w.gate_up.G) &&
+                      use_expert_gemm(M * k, E, I, w.down.G) && expert_gemm2_fits<EPI_SWIGLU>(gu2) &&
+                      expert_gemm2_fits<EPI_F32>(dn2) && H % 8 == 0 && I % 8 == 0;
+    // otherwise h in bf16: the oracle's rounding of silu(g) * u, with bf16's range
+    if (f16p) {
+        check_grouped(fn, x, qv(w.gate_up), E, route, L.route_bytes, M, k, h, Act::BF16, M * k * I * 2, M);
+        bf16_to_f16_paired(x, base + L.x16, M, H, stream);
+        STRIX_CHECK((launch_expert_gemm2<EPI_SWIGLU, true, g2::H_F16P, true>(gu2, stream)), fn, ": F16 gate_up");
+    } else if (fold) {
         const QV gv = q8 ? qv(gu8) : qv(w.gate_up);
         check_grouped(fn, x, gv, E, route, L.route_bytes, M, k, h, Act::BF16, M * k * I * 2, M);
         GemmArgs a = make_args(gv, E, x, h, I);
@@ -1456,7 +1480,9 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         check_view(fn, dv, E);
         GemmArgs a = make_args(dv, E, h, partial, H);
         a.A = k, a.ws = static_cast<const int32_t *>(route), a.S = M * k;
-        if (use_expert_gemm(M * k, E, dv.K, dv.G)) {
+        if (f16p) {
+            STRIX_CHECK((launch_expert_gemm2<EPI_F32, false, g2::H_BF16, true>(dn2, stream)), fn, ": F16 down");
+        } else if (use_expert_gemm(M * k, E, dv.K, dv.G)) {
             if (q8) launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
             else launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
         } else if (q8) {

@@ -18,7 +18,9 @@ from . import _lib as L
 from ._lib import GpuError, StrixError  # noqa: F401  (re-exported)
 
 F32, BF16 = 0, 1
-MOE_MATH_WMMA_F16 = 2  # strixite MoeMath::WmmaF16 (accepted; one gfx950 path)
+# strixite MoeMath (kernels/moe_grouped.hpp:39): the F16 kinds (2..5) run Q4 experts' prefill-size grouped GEMMs in
+# the reference's F16 math (x and the dequantized weights in F16); F32 and WmmaBf16 keep the weights exact
+MOE_MATH_F32, MOE_MATH_WMMA_BF16, MOE_MATH_WMMA_F16 = 0, 1, 2
 
 TENSOR = {  # tensor ids of the seeded generator (oracle/moe_oracle.c uses the same ids)
     "x": 1, "router": 2, "gu_q": 3, "gu_s": 4, "dn_q": 5, "dn_s": 6,
@@ -194,14 +196,14 @@ def _combine_fn(bits):
             else L.lib().strix_linear_q8_experts_combine_grouped)
 
 
-def experts_gather_grouped_swiglu(x, w: QWeight, E, ws, M, A, h_f16=False, h=None):
+def experts_gather_grouped_swiglu(x, w: QWeight, E, ws, M, A, h_f16=False, h=None, math=MOE_MATH_WMMA_F16):
     """strixite kernels/moe_grouped.hpp:66-69 (Q4; Q8 through the same signature family)."""
     I = w.N // E // 2
     if h is None:
         h = torch.empty((M * A, I), dtype=torch.float16 if h_f16 else torch.bfloat16, device=x.device)
     v = w.view()
-    L.check(_swiglu_fn(w.bits)(_p(x), C.byref(v), E, _p(ws), ws.numel() * 4, M, A, _p(h), BF16, MOE_MATH_WMMA_F16,
-                               _stream(), 1 if h_f16 else 0))
+    L.check(_swiglu_fn(w.bits)(_p(x), C.byref(v), E, _p(ws), ws.numel() * 4, M, A, _p(h), BF16, math, _stream(),
+                               1 if h_f16 else 0))
     return h
 
 
@@ -217,7 +219,7 @@ def experts_gather_grouped(x, w: QWeight, E, ws, M, A, y=None):
 
 
 def experts_combine_grouped(h, w: QWeight, E, ids, coef, ws, M, A, partial=None, y=None, shared: dict | None = None,
-                            h_f16=False):
+                            h_f16=False, math=MOE_MATH_WMMA_F16):
     """strixite kernels/moe_grouped.hpp:88-91 (+ MoeSharedAdd). Returns y [M, N]."""
     N = w.N // E
     if partial is None:
@@ -230,7 +232,7 @@ def experts_combine_grouped(h, w: QWeight, E, ids, coef, ws, M, A, partial=None,
                          _p(shared["err"]))
     v = w.view()
     L.check(_combine_fn(w.bits)(_p(h), C.byref(v), E, _p(ids), _p(coef), _p(ws), ws.numel() * 4, _p(partial), M, A,
-                                _p(y), BF16, MOE_MATH_WMMA_F16, _stream(), C.byref(sh) if sh is not None else None,
+                                _p(y), BF16, math, _stream(), C.byref(sh) if sh is not None else None,
                                 1 if h_f16 else 0))
     return y
 

@@ -153,6 +153,11 @@ def _experts(bits, E, H, I, seed=11):
     return gu, dn
 
 
+def _expert_gemm_size(S, E):
+    """The grouped projections' GEMM kernels take over at S >= 1024 slots and >= 8 slots an expert."""
+    return S >= 1024 and S >= 8 * E
+
+
 @pytest.mark.parametrize("bits,M,A,E,H,I", [(4, 16, 10, 64, 512, 256), (8, 1, 8, 64, 512, 128),
                                             (4, 300, 8, 16, 256, 128), (8, 40, 4, 8, 256, 64)])
 def test_grouped_gate_up_swiglu_and_down(bits, M, A, E, H, I):
@@ -166,6 +171,15 @@ def test_grouped_gate_up_swiglu_and_down(bits, M, A, E, H, I):
     b, q, s, m, G = qspec(gu)
     href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G), E, ids)
     assert rel_err(to_np(h), href) < 1e-2
+    # Q4 at prefill sizes runs the reference's F16 math (x and the weights rounded to F16): equal to its model up to
+    # FP32 summation order and the bf16 rounding of h
+    f16 = bits == 4 and _expert_gemm_size(M * A, E)
+    if f16:
+        h16 = orc.experts_gate_up_swiglu_f16math(x, b, q, s, m, gu.N, H, G, E, ids)
+        assert rel_err(to_np(h), h16) < 2.0 ** -8
+        # the exact-weight kinds (F32, WmmaBf16) keep their own kernel
+        hx = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A, math=moe.MOE_MATH_WMMA_BF16)
+        assert rel_err(to_np(hx), href) < 2.0 ** -7
     # the f16-bits form holds the same values wherever they lie in f16's normal range (|v| >= 2^-14)
     hf = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A, h_f16=True)
     normal = h.float().abs() >= 2.0 ** -14
@@ -176,8 +190,16 @@ def test_grouped_gate_up_swiglu_and_down(bits, M, A, E, H, I):
     y = moe.experts_combine_grouped(h, dn, E, tid, torch.from_numpy(coef).to(DEV), ws, M, A, partial=pt)
     b, q, s, m, G = qspec(dn)
     part = orc.experts_down(to_np(h), orc.qview(b, q, s, m, dn.N, I, G), E, ids)
-    # the per-slot down outputs before any bf16 rounding: fp32 accuracy (Q4's 128 + n codes cancel against m - 128 s)
-    assert rel_err(pt.cpu().numpy(), part) < 1e-4
+    if f16:  # the F16 math's per-slot outputs: its model up to FP32 summation order
+        assert rel_err(pt.cpu().numpy(), orc.experts_down_f16math(to_np(h), b, q, s, m, dn.N, I, G, E, ids)) < 1e-5
+        assert rel_err(pt.cpu().numpy(), part) < 2.0 ** -8
+        px = torch.empty_like(pt)
+        moe.experts_combine_grouped(h, dn, E, tid, torch.from_numpy(coef).to(DEV), ws, M, A, partial=px,
+                                    math=moe.MOE_MATH_WMMA_BF16)
+        assert rel_err(px.cpu().numpy(), part) < 1e-4
+    else:
+        # the per-slot down outputs before any bf16 rounding: fp32 accuracy (Q4's 128 + n codes cancel against m - 128 s)
+        assert rel_err(pt.cpu().numpy(), part) < 1e-4
     yref, _ = orc.combine(part, ids, coef, E, H)
     assert rel_err(to_np(y), yref) < 1e-2
     # the f16-h form sums in another order: an output may round to the neighbouring bf16 (2^-8 of its magnitude)
@@ -216,6 +238,39 @@ def test_invalid_ids_make_nan_rows():
     y = orc.bf16_to_f32(to_np(moe.experts_combine_grouped(torch.from_numpy(h.view(np.int16)).to(DEV).view(torch.bfloat16),
                                                           dn, E, tid, coef, ws, M, A)))
     assert np.all(np.isnan(y[1])) and np.all(np.isnan(y[3])) and not np.isnan(y[[0, 2]]).any()
+
+
+def test_prefill_gemm_ragged_buckets_and_invalid_ids():
+    """Prefill-size grouped GEMMs on skewed routing (buckets of 1 .. ~1000 slots, 128-slot pairs and lone 64-slot
+    tiles) with invalid ids: valid rows match the F16-math model, invalid slots' rows are NaN."""
+    say("prefill gemm ragged")
+    M, A, E, H, I = 512, 4, 32, 256, 128
+    gu, dn = _experts(4, E, H, I)
+    x = orc.gen_bf16_normal(orc.tensor_key(6, "x"), 1.0, (M, H))
+    rng = np.random.default_rng(11)
+    p = 1.0 / np.arange(1, E + 1) ** 1.3
+    ids = rng.choice(E, size=(M, A), p=p / p.sum()).astype(np.int32)
+    ids[7, 1], ids[300, 3], ids[511, 0] = -1, E, E + 9
+    tid = torch.from_numpy(ids).to(DEV)
+    ws, err = moe.moe_group_routes(tid, E)
+    h = to_np(moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A))
+    b, q, s, m, G = qspec(gu)
+    h16 = orc.experts_gate_up_swiglu_f16math(x, b, q, s, m, gu.N, H, G, E, ids)
+    bad = np.array([7 * A + 1, 300 * A + 3, 511 * A + 0])
+    good = np.setdiff1d(np.arange(M * A), bad)
+    assert np.all(np.isnan(orc.bf16_to_f32(h[bad])))
+    assert rel_err(h[good], h16[good]) < 2.0 ** -8
+    hz = h.copy()
+    hz[bad] = 0
+    pt = torch.empty((M * A, H), dtype=torch.float32, device=DEV)
+    coef = torch.full((M, A), 0.25, device=DEV)
+    moe.experts_combine_grouped(torch.from_numpy(hz.view(np.int16)).to(DEV).view(torch.bfloat16), dn, E, tid, coef,
+                                ws, M, A, partial=pt)
+    b, q, s, m, G = qspec(dn)
+    p16 = orc.experts_down_f16math(hz, b, q, s, m, dn.N, I, G, E, ids)
+    ptn = pt.cpu().numpy()
+    assert np.all(np.isnan(ptn[bad]))
+    assert rel_err(ptn[good], p16[good]) < 1e-5
 
 
 def test_perslot_kernels_match_grouped():

@@ -291,3 +291,53 @@ def test_swiglu_bf16_form(orc):
     s = orc.bf16_to_f32(orc.f32_to_bf16((g / (1 + np.exp(-g))).astype(np.float32)))
     ref = orc.f32_to_bf16((s * u).astype(np.float32))
     assert np.max(np.abs(h.astype(np.int32) - ref.astype(np.int32))) <= 1  # expf ulps
+
+
+# ---- the reference's F16 matrix-unit math (Q4 experts) -----------------------------------------------------------
+def test_bf16_to_f16_rtz_known_answers(orc):
+    b = np.array([0x3F80, 0x3EAB, 0x4789, 0xC789, 0x3580, 0x33C0, 0x33E0, 0x7F80, 0x3300, 0x0000], np.uint16)
+    h = orc.bf16_to_f16_rtz(b).astype(np.float64)
+    ulp = 2.0 ** -24  # F16's smallest subnormal
+    want = [1.0, 0.333984375, 65504.0, -65504.0, 2.0 ** -20, ulp, ulp, np.inf, 0.0, 0.0]
+    # 70144 -> 65504 (toward zero, not inf); 1.5 and 1.75 units of 2^-24 -> 1 unit (nearest-even would give 2);
+    # 2^-25 -> 0
+    assert list(h) == want
+    assert np.isnan(orc.bf16_to_f16_rtz(np.array([0x7FC0], np.uint16))[0])
+    # every BF16 in F16's normal range converts exactly
+    v = orc.bf16_to_f32(np.arange(0x3880, 0x4780, dtype=np.uint16))
+    assert np.array_equal(orc.bf16_to_f16_rtz(np.arange(0x3880, 0x4780, dtype=np.uint16)).astype(np.float32), v)
+
+
+def test_q4_weights_f16_one_rounding(orc):
+    N, K, G = 64, 256, 128
+    q, s, m = orc.gen_q(4, 91, 92, N, K, G)
+    w16 = orc.q4_weights_f16(q, s, m, N, K, G).astype(np.float64)
+    exact = orc.dequantize(4, q, s, m, N, K, G).astype(np.float64)  # the C oracle's code * s + m (nibble order)
+    # the generated scales and mins are exact in F16, so the F16 weight is the exact one rounded once to nearest
+    assert np.array_equal(orc.bf16_to_f32(s).astype(np.float16).astype(np.float32), orc.bf16_to_f32(s))
+    half_ulp = np.spacing(np.abs(exact).astype(np.float16)).astype(np.float64) / 2
+    assert np.all(np.abs(w16 - exact) <= half_ulp)
+    assert np.array_equal(w16, exact.astype(np.float16).astype(np.float64))
+
+
+def test_experts_f16math_against_exact_weights(orc):
+    """The F16-math gate_up / down against the exact-weight C oracle: equal to F16 rounding (2^-9 relative on these
+    sizes), and a wrong expert, slot row or operand order would be off by O(1)."""
+    w, x = _tiny_layer(orc, M=6, shared=False)
+    E, I = w["E"], w["I"]
+    H = x.shape[1]
+    ids = np.array([[0, 3], [2, 2], [1, 0], [3, 1], [0, 2], [1, 1]], np.int32)
+    bits, q, s, m, G = w["gu"]
+    h16 = orc.experts_gate_up_swiglu_f16math(x, bits, q, s, m, E * 2 * I, H, G, E, ids)
+    h = orc.experts_gate_up_swiglu(x, orc.qview(bits, q, s, m, E * 2 * I, H, G), E, ids)
+    hf, h16f = orc.bf16_to_f32(h), orc.bf16_to_f32(h16)
+    assert np.abs(h16f - hf).max() <= np.abs(hf).max() * 2 ** -9
+    bits, q, s, m, G = w["dn"]
+    p16 = orc.experts_down_f16math(h, bits, q, s, m, E * H, I, G, E, ids)
+    p = orc.experts_down(h, orc.qview(bits, q, s, m, E * H, I, G), E, ids)
+    assert np.abs(p16 - p).max() <= np.abs(p).max() * 2 ** -9
+    # brute force for one slot: F16 products summed in float64
+    sl, e = 7, ids.ravel()[7]
+    xs = orc.bf16_to_f16_rtz(h[sl]).astype(np.float64)
+    w16 = orc.q4_weights_f16(q, s, m, E * H, I, G)[e * H:(e + 1) * H].astype(np.float64)
+    assert np.allclose(p16[sl], [sum(xs[kk] * w16[n, kk] for kk in range(I)) for n in range(H)], rtol=1e-6, atol=1e-6)
