@@ -47,8 +47,10 @@ namespace kernels {
 enum class Act { F32, BF16 };
 const char *act_name(Act a);
 
-// strixite kernels/moe_grouped.hpp:38. Accepted at the boundary for source compatibility; every kind runs the one
-// gfx950 path (f16 MFMA, FP32 accumulation), which picks its tiles by shape.
+// strixite kernels/moe_grouped.hpp:38. The F16 kinds (WmmaF16, Narrow, Wide, Wide256: one math, tiles picked by
+// shape) run Q4 experts' prefill-size grouped GEMMs in the reference's F16 math (x rounded to F16 toward zero, each
+// weight one F16 rounding of code * s + m, FP32 accumulation); F32 and WmmaBf16 keep the weights exact (scaled
+// codes, FP32 accumulation). Q8 experts and decode-size calls use the exact weights under every kind.
 enum class MoeMath { F32, WmmaBf16, WmmaF16, WmmaF16Narrow, WmmaF16Wide, WmmaF16Wide256 };
 
 constexpr int64_t kMoeMaxExperts = 1023;  // strixite kernels/moe_grouped.hpp:43: E + 1 buckets
