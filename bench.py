@@ -257,8 +257,9 @@ def main():
         "metric": METRIC, "value": round(dec_tps, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps_run,
         "warmup": args.warmup, "ms_per_step": round(dec_ms, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
-        "math": "bf16 activations; Q4/Q8 codes as exact bf16 integers; bf16 MFMA, per-group scale/min on the FP32 accumulator; "
-                "router logits FP32",
+        "math": "decode: bf16 activations, Q4/Q8 codes as exact bf16 integers, bf16 MFMA, per-group scale/min on the FP32 "
+                "accumulator; prefill Q4 experts: the reference's F16 math (x and dequantized weights in f16, f16 MFMA, "
+                "FP32 accumulation); router logits FP32",
         "data": "synthetic (seeded on the device; independent weights per layer)",
         "config": {"workload": "cfg2: decode 16 tokens (2 slots x (1 + 7 MTP)), H3072 E512 top-10 + shared Q8 g64, "
                                "I512, Q4 g128 routed; 8-layer stack rotated (HBM-cold)",
