@@ -33,6 +33,7 @@ enum HForm { H_BF16 = 0, H_F16 = 1, H_F16P = 2 };
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+typedef uint32_t v4u32_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float16v mfma32_f16(const Frag &a, const Frag &b, float16v c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8v, a), __builtin_bit_cast(f16x8v, b), c, 0,
@@ -274,6 +275,37 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
         wait_vmcnt<0>();  // no load still writing LDS or registers when the wave ends
 
         // epilogue: lane (h, l32) holds column l32 of each 32 x 32 tile, token rows 8 b + 4 h + i of register 4 b + i
+        if constexpr (EPI == EPI_BF16) {
+            // BF16 rows go out through LDS as whole 128-byte lines: per 32-token sub-tile the wave writes its 32 x 64
+            // values into its own part of a free activation buffer (the part only its own loads fill: 16-byte slots
+            // 256 v + 64 w, v = 0..3, one a group of 8 rows), then stores 16 bytes a lane, 8 lanes a row
+            uint16_t *st = reinterpret_cast<uint16_t *>(abuf(X16 ? chunks % 3 : chunks & 1));
+            auto sidx = [&](int r, int c) { return ((r >> 3) * 256 + 64 * wave) * 8 + (r & 7) * 64 + c; };
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+                        st[sidx(8 * (r / 4) + 4 * h + r % 4, 32 * t + l32)] = f32_to_bf16(nan ? qnan() : acc[i][t][r]);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int row = 8 * q + lane / 8, seg = lane % 8;
+                    const uint4 v = *reinterpret_cast<const uint4 *>(st + sidx(row, 8 * seg));
+                    const int32_t orw = orow[32 * i + row];
+                    const int64_t col = col0[0] + 8 * seg;  // the wave's 64 columns from col0[0]
+                    const bool live = orw >= 0 && col < nrows;
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(v4u32_t, v), ry,
+                        live ? ((uint32_t)orw * (uint32_t)a.ldy + (uint32_t)col) * 2 : y_bytes, 0, 0);
+                }
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // the reads are done before the next sub-tile's writes
+                __builtin_amdgcn_wave_barrier();
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < NT; ++i) {
 #pragma unroll

@@ -740,9 +740,10 @@ __global__ void __launch_bounds__(1024)
 // invalid id. SH: y = stored(sum) + sigmoid(gl) * s (strixite kernels/moe_grouped.hip:948-985). RES: x_out = stored(x + y).
 // 4 columns a thread (N % 4 == 0); every slot's partials are loaded before the ordered sum, so a thread costs one
 // round trip (the kernel is latency-bound at decode sizes).
-template <bool SH, bool RES>
+// PB: the partials are BF16 (the F16 math's down stores them so, as the reference's does), else FP32
+template <bool SH, bool RES, bool PB>
 __global__ void __launch_bounds__(kThreads)
-    combine_reduce_kernel(const float *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
+    combine_reduce_kernel(const void *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                           int64_t N, uint16_t *y, const uint16_t *s, const float *gate_logit, int64_t gate_ld,
                           uint32_t gate_index, uint32_t *err, const uint16_t *resid, uint16_t *out,
                           const float *s_part, int s_parts) {
@@ -777,7 +778,14 @@ __global__ void __launch_bounds__(kThreads)
         for (int b = 0; b < B; ++b) {
             const int64_t a = a0 + b;
             if (a < A) {
-                p[b] = *reinterpret_cast<const float4 *>(partial + (m * A + a) * N + n);
+                const int64_t e = (m * A + a) * N + n;
+                if constexpr (PB) {
+                    const uint2 w = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(partial) + e);
+                    p[b] = make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xFFFF0000u),
+                                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xFFFF0000u));
+                } else {
+                    p[b] = *reinterpret_cast<const float4 *>(static_cast<const float *>(partial) + e);
+                }
                 c[b] = coef[m * A + a];
                 const int32_t id = ids[m * A + a];
                 ok = ok && id >= 0 && id < E;
@@ -1053,9 +1061,9 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
 }
 
 // s_part: the shared expert's down as K parts [s_parts][M][N] instead of the stored sh->s
-void combine_reduce(const float *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
+void combine_reduce(const void *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                     int64_t N, uint16_t *y, const MoeSharedAdd *sh, const uint16_t *resid, uint16_t *out,
-                    hipStream_t stream, const float *s_part = nullptr, int s_parts = 0) {
+                    hipStream_t stream, const float *s_part = nullptr, int s_parts = 0, bool partial_bf16 = false) {
     const unsigned blocks = (unsigned)((M * N / 4 + kThreads - 1) / kThreads);
     const uint16_t *s = sh ? static_cast<const uint16_t *>(sh->s) : nullptr;
     const float *gl = sh ? sh->gate_logit : nullptr;
@@ -1063,8 +1071,12 @@ void combine_reduce(const float *partial, const int32_t *ids, const float *coef,
     const uint32_t gi = sh ? sh->gate_index : 0;
     uint32_t *err = sh ? sh->err : nullptr;
     auto go = [&](auto shc, auto resc) {
-        combine_reduce_kernel<decltype(shc)::value, decltype(resc)::value><<<blocks, kThreads, 0, stream>>>(
-            partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, resid, out, s_part, s_parts);
+        if (partial_bf16)
+            combine_reduce_kernel<decltype(shc)::value, decltype(resc)::value, true><<<blocks, kThreads, 0, stream>>>(
+                partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, resid, out, s_part, s_parts);
+        else
+            combine_reduce_kernel<decltype(shc)::value, decltype(resc)::value, false><<<blocks, kThreads, 0, stream>>>(
+                partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, resid, out, s_part, s_parts);
     };
     if (sh && out) go(std::true_type{}, std::true_type{});
     else if (sh) go(std::true_type{}, std::false_type{});
@@ -1450,14 +1462,15 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     const Q8DeviceView gu8{w.gate_up.q, w.gate_up.scale, w.gate_up.minv, w.gate_up.N, w.gate_up.K, w.gate_up.G};
     const Q8DeviceView dn8{w.down.q, w.down.scale, w.down.minv, w.down.N, w.down.K, w.down.G};
     // Q4 experts at prefill sizes run the reference's F16 math (MoeMath::WmmaF16): x converted to F16 once, h kept
-    // in F16 (the F16 form of its BF16 rounding), both in the GEMM's paired k order (the down's partials stay FP32)
+    // in F16 (the F16 form of its BF16 rounding), both in the GEMM's paired k order, and the down's partials stored in
+    // BF16 (strixite kernels/moe_grouped.hpp:84)
     GemmArgs gu2 = make_args(qv(w.gate_up), E, base + L.x16, h, I);
     gu2.A = k, gu2.ws = static_cast<const int32_t *>(route), gu2.S = M * k;
     GemmArgs dn2 = make_args(qv(w.down), E, h, partial, H);
     dn2.A = k, dn2.ws = static_cast<const int32_t *>(route), dn2.S = M * k;
     const bool f16p = !q8 && !fold && use_expert_gemm(M * k, E, H, w.gate_up.G) &&
                       use_expert_gemm(M * k, E, I, w.down.G) && expert_gemm2_fits<EPI_SWIGLU>(gu2) &&
-                      expert_gemm2_fits<EPI_F32>(dn2) && H % 8 == 0 && I % 8 == 0;
+                      expert_gemm2_fits<EPI_BF16>(dn2) && H % 8 == 0 && I % 8 == 0;
     // otherwise h in bf16: the oracle's rounding of silu(g) * u, with bf16's range
     if (f16p) {
         check_grouped(fn, x, qv(w.gate_up), E, route, L.route_bytes, M, k, h, Act::BF16, M * k * I * 2, M);
@@ -1481,7 +1494,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         GemmArgs a = make_args(dv, E, h, partial, H);
         a.A = k, a.ws = static_cast<const int32_t *>(route), a.S = M * k;
         if (f16p) {
-            STRIX_CHECK((launch_expert_gemm2<EPI_F32, false, g2::H_BF16, true>(dn2, stream)), fn, ": F16 down");
+            STRIX_CHECK((launch_expert_gemm2<EPI_BF16, false, g2::H_BF16, true>(dn2, stream)), fn, ": F16 down");
         } else if (use_expert_gemm(M * k, E, dv.K, dv.G)) {
             if (q8) launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
             else launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
@@ -1495,7 +1508,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     const MoeSharedAdd sh{sh_s, lg + E, ld, (uint32_t)E, err_router};
     combine_reduce(partial, ids, coef, M, k, E, H, static_cast<uint16_t *>(y), w.has_shared ? &sh : nullptr,
                    static_cast<const uint16_t *>(x), static_cast<uint16_t *>(x_out), stream, fold ? sh_part : nullptr,
-                   fold ? sh_jobs[1].parts : 0);
+                   fold ? sh_jobs[1].parts : 0, f16p);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " E=", E, " k=", k);
 }
 
