@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define STRIX_MOE_ABI_VERSION 1
+#define STRIX_MOE_ABI_VERSION 2
 #define STRIX_E_PRECONDITION 1
 #define STRIX_E_GPU 2
 #define STRIX_E_OTHER 3
@@ -105,6 +105,9 @@ int strix_report_expert_error(const uint32_t *err_host, const char *what);
 /* strixite kernels/swiglu.hpp:21 swiglu */
 int strix_swiglu(const void *gu, void *h, int64_t rows, int64_t I, int act, void *stream);
 
+/* strixite kernels/linear_q4.hpp:23-31 linear_q4 (a dense Q4 projection) */
+int strix_linear_q4(const void *x, const strix_qview *w, void *y, int64_t M, int act, int out_act, void *stream);
+
 /* strixite kernels/linear_q8.hpp:13-14 linear_q8 (the shared expert's projections) */
 int strix_linear_q8(const void *x, const strix_qview *w, void *y, int64_t M, int act, int out_act, void *stream);
 
@@ -124,9 +127,13 @@ typedef struct {
 } strix_moe_layer_weights;
 
 int64_t strix_moe_layer_workspace_bytes(const strix_moe_layer_weights *w, int64_t M);
+/* ctx (optional, from strix_moe_layer_context_create): the helper stream for the shared expert at M > 16 tokens;
+ * created before any graph capture, used by one host thread at a time; null: the shared expert runs on stream. */
+int strix_moe_layer_context_create(void **ctx);
+int strix_moe_layer_context_destroy(void *ctx);
 int strix_moe_layer_forward(const strix_moe_layer_weights *w, const void *x, int64_t M, const float *logits_in,
                             void *y, void *x_out, int32_t *ids, float *coef, void *ws, size_t ws_bytes, uint32_t *err,
-                            void *stream);
+                            void *stream, void *ctx);
 
 /* Seeded synthetic tensors on the device (no reference counterpart: the bench's input generator). Element i of a
  * tensor is a function of (key, i) only; key = strix_synth_tensor_key(seed, tensor id, layer). */

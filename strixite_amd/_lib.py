@@ -61,9 +61,12 @@ _SIGS = {
     "strix_check_expert_error": (_int, [_p, C.c_char_p]),
     "strix_report_expert_error": (_int, [_p, C.c_char_p]),
     "strix_swiglu": (_int, [_p, _p, _i64, _i64, _int, _p]),
+    "strix_linear_q4": (_int, [_p, C.POINTER(QView), _p, _i64, _int, _int, _p]),
     "strix_linear_q8": (_int, [_p, C.POINTER(QView), _p, _i64, _int, _int, _p]),
     "strix_moe_layer_workspace_bytes": (_i64, [C.POINTER(LayerWeights), _i64]),
-    "strix_moe_layer_forward": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _sz, _p, _p]),
+    "strix_moe_layer_context_create": (_int, [C.POINTER(_p)]),
+    "strix_moe_layer_context_destroy": (_int, [_p]),
+    "strix_moe_layer_forward": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _sz, _p, _p, _p]),
     "strix_synth_tensor_key": (_u64, [_u64, _u32, _u32]),
     "strix_synth_bf16_normal": (_int, [_u64, _f32, _p, _i64, _p]),
     "strix_synth_q_weight": (_int, [_int, _u64, _u64, _i64, _i64, _i64, _p, _p, _p, _p]),

@@ -22,7 +22,7 @@ template <typename F> int guard(F &&f) {
         f();
         g_last_error.clear();
         return 0;
-    } catch (const strix::GpuError &e) {
+    } catch (const strix::GpuFatalError &e) {
         g_last_error = e.what();
         return STRIX_E_GPU;
     } catch (const strix::Error &e) {
@@ -217,6 +217,9 @@ int strix_swiglu(const void *gu, void *h, int64_t rows, int64_t I, int act, void
     return guard([&] { strix::kernels::swiglu(gu, h, rows, I, act_of(act), st(stream)); });
 }
 
+int strix_linear_q4(const void *x, const strix_qview *w, void *y, int64_t M, int act, int out_act, void *stream) {
+    return guard([&] { strix::kernels::linear_q4(x, q4(w), y, M, act_of(act), act_of(out_act), st(stream)); });
+}
 int strix_linear_q8(const void *x, const strix_qview *w, void *y, int64_t M, int act, int out_act, void *stream) {
     return guard([&] { strix::kernels::linear_q8(x, q8(w), y, M, act_of(act), act_of(out_act), st(stream)); });
 }
@@ -228,11 +231,22 @@ int64_t strix_moe_layer_workspace_bytes(const strix_moe_layer_weights *w, int64_
     return r;
 }
 
+int strix_moe_layer_context_create(void **ctx) {
+    return guard([&] {
+        STRIX_CHECK(ctx != nullptr, "strix_moe_layer_context_create: null ctx");
+        *ctx = strix::moe_layer_context_create();
+    });
+}
+int strix_moe_layer_context_destroy(void *ctx) {
+    return guard([&] { strix::moe_layer_context_destroy(static_cast<strix::MoeLayerContext *>(ctx)); });
+}
+
 int strix_moe_layer_forward(const strix_moe_layer_weights *w, const void *x, int64_t M, const float *logits_in,
                             void *y, void *x_out, int32_t *ids, float *coef, void *ws, size_t ws_bytes, uint32_t *err,
-                            void *stream) {
+                            void *stream, void *ctx) {
     return guard([&] {
-        strix::moe_layer_forward(layer_of(w), x, M, logits_in, y, x_out, ids, coef, ws, ws_bytes, err, st(stream));
+        strix::moe_layer_forward(layer_of(w), x, M, logits_in, y, x_out, ids, coef, ws, ws_bytes, err, st(stream),
+                                 static_cast<strix::MoeLayerContext *>(ctx));
     });
 }
 

@@ -15,6 +15,8 @@ namespace strix {
 // Internal entry (route.hip), used by the layer forward for small batches: top-k of FP32 logits (no shared-expert
 // slot) and the packing of moe_group_routes in one launch, M k <= 1024.
 namespace kernels {
+// "F32" / "BF16" for messages (strixite's act_name lives in its kernels/norm.hip; this library does not export one)
+const char *act_str(Act a);
 void moe_topk_group_routes_small(const float *logits, int64_t ld, int64_t M, int64_t E, int64_t k, int32_t *ids,
                                  float *coef, void *ws, size_t ws_bytes, uint32_t *err_router, uint32_t *err_route,
                                  hipStream_t stream);
@@ -49,7 +51,7 @@ template <typename... Ts> std::string cat(const Ts &...xs) {
     do {                                                                                                             \
         const hipError_t e_ = (expr);                                                                                \
         if (e_ != hipSuccess)                                                                                        \
-            throw ::strix::GpuError(::strix::detail::cat(__func__, ": ", #expr, " -> ", hipGetErrorString(e_), " ", \
+            throw ::strix::GpuFatalError(::strix::detail::cat(__func__, ": ", #expr, " -> ", hipGetErrorString(e_), " ", \
                                                          __VA_ARGS__));                                             \
     } while (0)
 

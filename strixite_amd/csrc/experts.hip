@@ -16,7 +16,8 @@
 #include "route_small.hpp"
 
 #include <algorithm>
-#include <map>
+#include <array>
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 #include <utility>
@@ -741,15 +742,17 @@ __global__ void __launch_bounds__(1024)
 // 4 columns a thread (N % 4 == 0); every slot's partials are loaded before the ordered sum, so a thread costs one
 // round trip (the kernel is latency-bound at decode sizes).
 // PB: the partials are BF16 (the F16 math's down stores them so, as the reference's does), else FP32
+// VEC consecutive outputs a thread (8 with BF16 partials measured 1.7x slower: the loads in flight cost registers);
+// the FP32 partials and the shared expert's parts are read as float4
+constexpr int kCombineVec = 4;
+static_assert(kCombineVec % 4 == 0, "float4 loads of FP32 partials");
 template <bool SH, bool RES, bool PB>
 __global__ void __launch_bounds__(kThreads)
     combine_reduce_kernel(const void *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                           int64_t N, uint16_t *y, const uint16_t *s, const float *gate_logit, int64_t gate_ld,
                           uint32_t gate_index, uint32_t *err, const uint16_t *resid, uint16_t *out,
                           const float *s_part, int s_parts) {
-    // VEC consecutive outputs a thread (8 with BF16 partials measured 1.7x slower: the loads in flight cost
-    // registers)
-    constexpr int VEC = 4, W = VEC / 2;  // W: dwords of VEC bf16
+    constexpr int VEC = kCombineVec, W = VEC / 2;  // W: dwords of VEC bf16
     const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * VEC;
     if (i >= M * N) return;
     const int64_t m = i / N, n = i % N;
@@ -1025,7 +1028,7 @@ void launch_topk_route_shared(const float *logits, int64_t ld, int64_t M, int64_
 void check_grouped(const char *fn, const void *x, const QV &w, int64_t E, const void *ws, size_t ws_bytes, int64_t M,
                    int64_t A, const void *y, Act act, int64_t y_bytes, int64_t x_rows) {
     STRIX_CHECK(x != nullptr && y != nullptr && ws != nullptr, fn, ": null pointer (x=", x, ", y=", y, ", ws=", ws, ")");
-    STRIX_CHECK(act == Act::BF16, fn, ": activations must be BF16 on this path, got ", act_name(act));
+    STRIX_CHECK(act == Act::BF16, fn, ": activations must be BF16 on this path, got ", act_str(act));
     check_view(fn, w, E);
     STRIX_CHECK(E <= kMoeMaxExperts, fn, ": E = ", E, " > ", kMoeMaxExperts);
     STRIX_CHECK(M >= 1 && A >= 1 && A <= 64 && A <= E && M * A <= kMoeMaxSlots, fn, ": M = ", M, " tokens x A = ", A,
@@ -1079,7 +1082,7 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
 void combine_reduce(const void *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                     int64_t N, uint16_t *y, const MoeSharedAdd *sh, const uint16_t *resid, uint16_t *out,
                     hipStream_t stream, const float *s_part = nullptr, int s_parts = 0, bool partial_bf16 = false) {
-    const unsigned blocks = (unsigned)((M * N / 4 + kThreads - 1) / kThreads);
+    const unsigned blocks = (unsigned)((M * N / kCombineVec + kThreads - 1) / kThreads);
     const uint16_t *s = sh ? static_cast<const uint16_t *>(sh->s) : nullptr;
     const float *gl = sh ? sh->gate_logit : nullptr;
     const int64_t gld = sh ? sh->gate_ld : 0;
@@ -1122,14 +1125,18 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
     GemmArgs a = make_args(w, E, h, partial, N);
     a.A = A, a.ws = static_cast<const int32_t *>(ws), a.S = M * A;
     const int64_t tiles = grouped_tiles(M, A, E);
+    // the F16 math keeps its per-slot partials in BF16 in the first half of partial, as the reference's F16 kinds do
+    // (strixite kernels/moe_grouped.hpp:84); every other form keeps them FP32
+    bool pb = false;
     if (!h_f16 && use_expert_gemm(M * A, E, w.K, w.G)) {  // (the GEMM reads bf16 activations only)
         if (w.bits == 4) {
-            if (!(f16 && launch_expert_gemm2<EPI_F32, false, g2::H_BF16, false>(a, stream)))
-                launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
+            pb = f16 && launch_expert_gemm2<EPI_BF16, false, g2::H_BF16, false>(a, stream);
+            if (!pb) launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
         } else launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
     } else if (h_f16) launch_bits<GROUPED, EPI_F32, true, false, false>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_F32, false, false, false>(w.bits, a, tiles, stream);
-    combine_reduce(partial, ids, coef, M, A, E, N, static_cast<uint16_t *>(y), shared, nullptr, nullptr, stream);
+    combine_reduce(partial, ids, coef, M, A, E, N, static_cast<uint16_t *>(y), shared, nullptr, nullptr, stream,
+                   nullptr, 0, pb);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E, " N=", N, " K=", w.K, " G=", w.G,
                            shared ? " +shared" : "");
 }
@@ -1137,7 +1144,7 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
 void check_perslot(const char *fn, const void *x, const QV &w, int64_t E, const int32_t *ids, int64_t M, int64_t A,
                    const void *y, Act act, uint32_t *err) {
     STRIX_CHECK(x != nullptr && y != nullptr && ids != nullptr && err != nullptr, fn, ": null pointer");
-    STRIX_CHECK(act == Act::BF16, fn, ": activations must be BF16 on this path, got ", act_name(act));
+    STRIX_CHECK(act == Act::BF16, fn, ": activations must be BF16 on this path, got ", act_str(act));
     check_view(fn, w, E);
     STRIX_CHECK(M >= 1 && A >= 1 && M * A <= 65535ll * 64, fn, ": M = ", M, ", A = ", A, " out of range");
     STRIX_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0, fn, ": input must be 16-byte aligned");
@@ -1260,18 +1267,16 @@ void swiglu(const void *gu, void *h, int64_t rows, int64_t I, Act act, hipStream
     else
         swiglu_kernel<uint16_t><<<blocks, kThreads, 0, stream>>>(static_cast<const uint16_t *>(gu),
                                                                  static_cast<uint16_t *>(h), n, I);
-    STRIX_HIP_CHECK_LAUNCH("swiglu ", act_name(act), " rows=", rows, " I=", I);
+    STRIX_HIP_CHECK_LAUNCH("swiglu ", act_str(act), " rows=", rows, " I=", I);
 }
 
-void linear_q8(const void *x, const Q8DeviceView &w, void *y, int64_t M, Act act, hipStream_t stream) {
-    linear_q8(x, w, y, M, act, act, stream);
-}
-
-void linear_q8(const void *x, const Q8DeviceView &w, void *y, int64_t M, Act act, Act out_act, hipStream_t stream) {
-    const char *fn = "linear_q8";
-    const QV v = qv(w);
+namespace {
+// y [M, N] = x [M, K] . dequant(W)^T for one Q4 or Q8 weight: 16-token tiles, each wave streaming 32 weight rows
+// over all of K (the DENSE mode of the stream kernel); FP32 accumulation, y stored in out_act
+void dense_projection(const char *fn, const QV &v, const void *x, void *y, int64_t M, Act act, Act out_act,
+                      hipStream_t stream) {
     STRIX_CHECK(x != nullptr && y != nullptr, fn, ": null pointer (x=", x, ", y=", y, ")");
-    STRIX_CHECK(act == Act::BF16, fn, ": activations must be BF16 on this path, got ", act_name(act));
+    STRIX_CHECK(act == Act::BF16, fn, ": activations must be BF16 on this path, got ", act_str(act));
     STRIX_CHECK(out_act == Act::BF16 || out_act == Act::F32, fn, ": output dtype ", (int)out_act);
     check_view(fn, v, 1);
     STRIX_CHECK(M >= 1 && (M + 15) / 16 <= 65535ll * 64, fn, ": M = ", M);
@@ -1281,9 +1286,26 @@ void linear_q8(const void *x, const Q8DeviceView &w, void *y, int64_t M, Act act
     STRIX_CHECK(disjoint(y, M * v.N * oes, x, M * v.K * 2), fn, ": y overlaps x");
     GemmArgs a = make_args(v, 1, x, y, v.N);
     a.M = M;
-    if (out_act == Act::F32) launch_gemm<8, DENSE, EPI_F32, false, false, false>(a, (M + 15) / 16, stream);
-    else launch_gemm<8, DENSE, EPI_BF16, false, false, false>(a, (M + 15) / 16, stream);
+    if (out_act == Act::F32) launch_bits<DENSE, EPI_F32, false, false, false>(v.bits, a, (M + 15) / 16, stream);
+    else launch_bits<DENSE, EPI_BF16, false, false, false>(v.bits, a, (M + 15) / 16, stream);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " N=", v.N, " K=", v.K, " G=", v.G);
+}
+}  // namespace
+
+// strixite kernels/linear_q4.hpp:23-31
+void linear_q4(const void *x, const Q4DeviceView &w, void *y, int64_t M, Act act, hipStream_t stream) {
+    dense_projection("linear_q4", qv(w), x, y, M, act, act, stream);
+}
+void linear_q4(const void *x, const Q4DeviceView &w, void *y, int64_t M, Act act, Act out_act, hipStream_t stream) {
+    dense_projection("linear_q4", qv(w), x, y, M, act, out_act, stream);
+}
+
+// strixite kernels/linear_q8.hpp:13-14
+void linear_q8(const void *x, const Q8DeviceView &w, void *y, int64_t M, Act act, hipStream_t stream) {
+    dense_projection("linear_q8", qv(w), x, y, M, act, act, stream);
+}
+void linear_q8(const void *x, const Q8DeviceView &w, void *y, int64_t M, Act act, Act out_act, hipStream_t stream) {
+    dense_projection("linear_q8", qv(w), x, y, M, act, out_act, stream);
 }
 
 }  // namespace strix::kernels
@@ -1327,33 +1349,42 @@ size_t moe_layer_workspace_bytes(const MoeLayerWeights &w, int64_t M) {
     return (size_t)layer_ws(w, M).total;
 }
 
-namespace {
-// The shared expert runs on a helper stream beside the routing kernels (router, top-k, packing), which leave most of
-// the chip idle: forked from the caller's stream with an event and joined back before the combine. One helper
-// stream and event pair per device, created on the first layer call (before any graph capture); a mutex serialises
-// layer calls so that each join waits on its own fork.
-struct SideStream {
+// The shared expert runs on the context's helper stream beside the routing kernels (router, top-k, packing), which
+// leave most of the chip idle at prefill sizes: forked from the caller's stream with an event and joined back before
+// the combine. The context is created explicitly (before any graph capture: a stream created during capture would
+// break it) and used by one host thread at a time, like a stream.
+struct MoeLayerContext {
+    int device = 0;
     hipStream_t s = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
 };
-std::mutex side_mu;
-SideStream &side_stream(const char *fn) {
-    static std::map<int, SideStream> per_device;
-    int dev = 0;
-    STRIX_HIP_CHECK(hipGetDevice(&dev), fn, ": hipGetDevice");
-    SideStream &ss = per_device[dev];
-    if (!ss.s) {
-        STRIX_HIP_CHECK(hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking), fn, ": helper stream");
-        STRIX_HIP_CHECK(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming), fn, ": fork event");
-        STRIX_HIP_CHECK(hipEventCreateWithFlags(&ss.join, hipEventDisableTiming), fn, ": join event");
+
+MoeLayerContext *moe_layer_context_create() {
+    const char *fn = "moe_layer_context_create";
+    auto *c = new MoeLayerContext;
+    try {
+        STRIX_HIP_CHECK(hipGetDevice(&c->device), fn, ": hipGetDevice");
+        STRIX_HIP_CHECK(hipStreamCreateWithFlags(&c->s, hipStreamNonBlocking), fn, ": helper stream");
+        STRIX_HIP_CHECK(hipEventCreateWithFlags(&c->fork, hipEventDisableTiming), fn, ": fork event");
+        STRIX_HIP_CHECK(hipEventCreateWithFlags(&c->join, hipEventDisableTiming), fn, ": join event");
+    } catch (...) {
+        moe_layer_context_destroy(c);
+        throw;
     }
-    return ss;
+    return c;
 }
-}  // namespace
+
+void moe_layer_context_destroy(MoeLayerContext *c) {
+    if (c == nullptr) return;
+    if (c->join) (void)hipEventDestroy(c->join);
+    if (c->fork) (void)hipEventDestroy(c->fork);
+    if (c->s) (void)hipStreamDestroy(c->s);
+    delete c;
+}
 
 void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const float *logits_in, void *y,
                        void *x_out, int32_t *ids_out, float *coef_out, void *ws, size_t ws_bytes, uint32_t *err,
-                       hipStream_t stream) {
+                       hipStream_t stream, MoeLayerContext *ctx) {
     using namespace kernels;
     const char *fn = "moe_layer_forward";
     STRIX_CHECK(x != nullptr && y != nullptr && ws != nullptr && err != nullptr, fn, ": null pointer");
@@ -1369,6 +1400,17 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     const LayerWs L = layer_ws(w, M);
     STRIX_CHECK(ws_bytes >= (size_t)L.total, fn, ": workspace of ", ws_bytes, " bytes, needs ", L.total);
     STRIX_CHECK(reinterpret_cast<uintptr_t>(ws) % 256 == 0, fn, ": workspace must be 256-byte aligned");
+    // the combine reads x and writes y / x_out kCombineVec bf16 at a time
+    const int64_t act_bytes = M * w.H * 2;
+    STRIX_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(x_out) % 16 == 0 && w.H % 8 == 0,
+                fn, ": x, y and x_out must be 16-byte aligned and H = ", w.H, " a multiple of 8");
+    STRIX_CHECK(disjoint(y, act_bytes, ws, (int64_t)ws_bytes) && disjoint(y, act_bytes, x, act_bytes), fn,
+                ": y overlaps the workspace or x");
+    if (x_out != nullptr)
+        STRIX_CHECK(disjoint(x_out, act_bytes, ws, (int64_t)ws_bytes) && disjoint(x_out, act_bytes, y, act_bytes) &&
+                        (x_out == x || disjoint(x_out, act_bytes, x, act_bytes)),
+                    fn, ": x_out overlaps the workspace or y, or partly overlaps x");
     char *base = static_cast<char *>(ws);
     const int64_t E = w.E, k = w.k, H = w.H, I = w.I, ld = E + (w.has_shared ? 1 : 0);
     float *logits = reinterpret_cast<float *>(base + L.logits);
@@ -1416,29 +1458,34 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         j1.units = dv.N / 16 * j1.parts;
         j1.blocks = (int)((j1.units + kWaves - 1) / kWaves);
     }
-    std::unique_lock<std::mutex> side_lock(side_mu, std::defer_lock);
-    SideStream *ss = nullptr;
+    // with a context the shared expert runs on its helper stream; without one, on the caller's stream first
+    hipStream_t sh_stream = stream;
     if (w.has_shared && !fold) {
         const QV gv = qv(w.sh_gate_up), dv = qv(w.sh_down);
         check_view(fn, gv, 1);
         check_view(fn, dv, 1);
-        side_lock.lock();
-        ss = &side_stream(fn);
-        STRIX_HIP_CHECK(hipEventRecord(ss->fork, stream), fn, ": fork");
-        STRIX_HIP_CHECK(hipStreamWaitEvent(ss->s, ss->fork, 0), fn, ": fork wait");
+        if (ctx != nullptr) {
+            int dev = 0;
+            STRIX_HIP_CHECK(hipGetDevice(&dev), fn, ": hipGetDevice");
+            STRIX_CHECK(dev == ctx->device, fn, ": the layer context belongs to device ", ctx->device,
+                        ", the current device is ", dev);
+            STRIX_HIP_CHECK(hipEventRecord(ctx->fork, stream), fn, ": fork");
+            STRIX_HIP_CHECK(hipStreamWaitEvent(ctx->s, ctx->fork, 0), fn, ": fork wait");
+            sh_stream = ctx->s;
+        }
         GemmArgs a = make_args(gv, 1, x, sh_h, I);
         a.M = M;
         GemmArgs b = make_args(dv, 1, sh_h, sh_s, H);
         b.M = M;
         if (M >= 128 && H % gemm::BK == 0 && I % gemm::BK == 0 && gv.G % gemm::BK == 0 && dv.G % gemm::BK == 0) {
-            launch_expert_gemm<8, DENSE, EPI_SWIGLU, false, false>(a, ss->s);
-            launch_expert_gemm<8, DENSE, EPI_BF16, false, false>(b, ss->s);
+            launch_expert_gemm<8, DENSE, EPI_SWIGLU, false, false>(a, sh_stream);
+            launch_expert_gemm<8, DENSE, EPI_BF16, false, false>(b, sh_stream);
         } else {
-            launch_gemm<8, DENSE, EPI_SWIGLU, false, false, false>(a, (M + 15) / 16, ss->s);
-            launch_gemm<8, DENSE, EPI_BF16, false, false, false>(b, (M + 15) / 16, ss->s);
+            launch_gemm<8, DENSE, EPI_SWIGLU, false, false, false>(a, (M + 15) / 16, sh_stream);
+            launch_gemm<8, DENSE, EPI_BF16, false, false, false>(b, (M + 15) / 16, sh_stream);
         }
         STRIX_HIP_CHECK_LAUNCH(fn, " shared expert M=", M);
-        STRIX_HIP_CHECK(hipEventRecord(ss->join, ss->s), fn, ": join");
+        if (ctx != nullptr) STRIX_HIP_CHECK(hipEventRecord(ctx->join, ctx->s), fn, ": join");
     }
 
     // router projection (+ harness bias) and top-k
@@ -1519,7 +1566,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
             launch_gemm<4, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream, fold ? &sh_jobs[1] : nullptr);
         }
     }
-    if (ss) STRIX_HIP_CHECK(hipStreamWaitEvent(stream, ss->join, 0), fn, ": join wait");
+    if (ctx != nullptr && w.has_shared && !fold) STRIX_HIP_CHECK(hipStreamWaitEvent(stream, ctx->join, 0), fn, ": join wait");
     const MoeSharedAdd sh{sh_s, lg + E, ld, (uint32_t)E, err_router};
     combine_reduce(partial, ids, coef, M, k, E, H, static_cast<uint16_t *>(y), w.has_shared ? &sh : nullptr,
                    static_cast<const uint16_t *>(x), static_cast<uint16_t *>(x_out), stream, fold ? sh_part : nullptr,

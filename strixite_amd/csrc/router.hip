@@ -9,7 +9,7 @@
 
 namespace strix::kernels {
 
-const char *act_name(Act a) { return a == Act::F32 ? "F32" : a == Act::BF16 ? "BF16" : "?"; }
+const char *act_str(Act a) { return a == Act::F32 ? "F32" : a == Act::BF16 ? "BF16" : "?"; }
 
 namespace {
 
@@ -369,7 +369,7 @@ void linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t 
                 (const void *)w, ", y=", y, ")");
     STRIX_CHECK(M >= 1 && N >= 1 && K >= 1 && K <= (1 << 24) && N <= 0x7fffffff, "linear_bf16w: M = ", M, ", N = ",
                 N, ", K = ", K, " out of range");
-    STRIX_CHECK(act == Act::BF16, "linear_bf16w: activations must be BF16 on this path, got ", act_name(act));
+    STRIX_CHECK(act == Act::BF16, "linear_bf16w: activations must be BF16 on this path, got ", act_str(act));
     STRIX_CHECK(out_act == Act::F32 || out_act == Act::BF16, "linear_bf16w: output dtype ", (int)out_act);
     const int64_t oes = out_act == Act::F32 ? 4 : 2;
     STRIX_CHECK(disjoint(y, M * N * oes, x, M * K * 2), "linear_bf16w: output y overlaps input x");
@@ -417,7 +417,7 @@ void moe_router(const void *logits, int64_t ld, int64_t M, int64_t E, int64_t k,
     };
     if (act == Act::F32) by_nv(float{});
     else by_nv(uint16_t{});
-    STRIX_HIP_CHECK_LAUNCH("moe_router ", act_name(act), " M=", M, " E=", E, " k=", k, shared_logit ? " +shared" : "");
+    STRIX_HIP_CHECK_LAUNCH("moe_router ", act_str(act), " M=", M, " E=", E, " k=", k, shared_logit ? " +shared" : "");
 }
 
 void check_router_error(const uint32_t *err, const char *what) {
@@ -457,7 +457,7 @@ void shared_add_common(const char *fn, void *y, const void *s, const float *gate
         shared_add_kernel<uint16_t, INJECT><<<blocks, kThreads, 0, stream>>>(
             static_cast<uint16_t *>(y), static_cast<const uint16_t *>(s), gate_logit, gate_ld, M, N, gate_index,
             static_cast<uint16_t *>(x), w_in, H, err);
-    STRIX_HIP_CHECK_LAUNCH(fn, " ", act_name(act), " M=", M, " N=", N);
+    STRIX_HIP_CHECK_LAUNCH(fn, " ", act_str(act), " M=", M, " N=", N);
 }
 }  // namespace
 

@@ -276,7 +276,36 @@ def linear_q8(x: torch.Tensor, w: QWeight, out_dtype=torch.bfloat16) -> torch.Te
     return y
 
 
+def linear_q4(x: torch.Tensor, w: QWeight, out_dtype=torch.bfloat16) -> torch.Tensor:
+    """strixite kernels/linear_q4.hpp:23-31."""
+    M = x.shape[0]
+    y = torch.empty((M, w.N), dtype=out_dtype, device=x.device)
+    v = w.view()
+    L.check(L.lib().strix_linear_q4(_p(x), C.byref(v), _p(y), M, _act(x), _act(y), _stream()))
+    return y
+
+
 # ---- the sublayer ----------------------------------------------------------------------------------------------
+class LayerContext:
+    """The helper stream (and its fork / join events) on which the sublayer runs the shared expert beside the routing
+    kernels at prefill sizes (strix_moe_layer_context_create). Create it before any graph capture, on the device it
+    serves; use it from one thread at a time."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        L.check(L.lib().strix_moe_layer_context_create(C.byref(h)))
+        self._h = h
+
+    @property
+    def handle(self):
+        return self._h
+
+    def __del__(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            L.lib().strix_moe_layer_context_destroy(self._h)
+            self._h = None
+
+
 class MoeLayer:
     """One MoE FFN sublayer's weights on the device and its forward (strixite runtime/qwen4exp.cpp:3143-3217)."""
 
@@ -332,8 +361,9 @@ class MoeLayer:
         return torch.empty(self.workspace_bytes(M), dtype=torch.uint8, device=device)
 
     def forward(self, x: torch.Tensor, logits_in: torch.Tensor | None = None, ws: torch.Tensor | None = None,
-                out: dict | None = None) -> dict:
-        """Returns {y, x_out, ids, coef, err[6]} (asynchronous; the tensors are filled on the current stream)."""
+                out: dict | None = None, ctx: LayerContext | None = None) -> dict:
+        """Returns {y, x_out, ids, coef, err[6]} (asynchronous; the tensors are filled on the current stream). ctx: a
+        LayerContext for the shared expert's helper stream at prefill sizes (None: it runs on the current stream)."""
         M = x.shape[0]
         if ws is None:
             ws = self.workspace(M, x.device)
@@ -347,5 +377,5 @@ class MoeLayer:
             }
         L.check(L.lib().strix_moe_layer_forward(C.byref(self._w), _p(x), M, _p(logits_in), _p(out["y"]),
                                                 _p(out["x_out"]), _p(out["ids"]), _p(out["coef"]), _p(ws), ws.numel(),
-                                                _p(out["err"]), _stream()))
+                                                _p(out["err"]), _stream(), ctx.handle if ctx is not None else None))
         return out

@@ -153,6 +153,13 @@ def _experts(bits, E, H, I, seed=11):
     return gu, dn
 
 
+def _bf16_partials(pt: torch.Tensor) -> np.ndarray:
+    """The F16 math's per-slot partials: BF16 [S, N] in the first half of the FP32 [S, N] partial buffer (the
+    reference's layout for its F16 kinds, strixite kernels/moe_grouped.hpp:84)."""
+    S, N = pt.shape
+    return to_np(pt.view(-1).view(torch.bfloat16)[: S * N].reshape(S, N))
+
+
 def _expert_gemm_size(S, E):
     """The grouped projections' GEMM kernels take over at S >= 1024 slots and >= 8 slots an expert."""
     return S >= 1024 and S >= 8 * E
@@ -190,21 +197,27 @@ def test_grouped_gate_up_swiglu_and_down(bits, M, A, E, H, I):
     y = moe.experts_combine_grouped(h, dn, E, tid, torch.from_numpy(coef).to(DEV), ws, M, A, partial=pt)
     b, q, s, m, G = qspec(dn)
     part = orc.experts_down(to_np(h), orc.qview(b, q, s, m, dn.N, I, G), E, ids)
-    if f16:  # the F16 math's per-slot outputs: its model up to FP32 summation order
-        assert rel_err(pt.cpu().numpy(), orc.experts_down_f16math(to_np(h), b, q, s, m, dn.N, I, G, E, ids)) < 1e-5
-        assert rel_err(pt.cpu().numpy(), part) < 2.0 ** -8
+    if f16:  # the F16 math's per-slot outputs, stored BF16: its model rounded to BF16, up to FP32 summation order
+        pb = _bf16_partials(pt)
+        p16 = orc.experts_down_f16math(to_np(h), b, q, s, m, dn.N, I, G, E, ids)
+        assert rel_err(pb, orc.f32_to_bf16(p16)) <= 2.0 ** -8
+        assert np.mean(pb == orc.f32_to_bf16(p16)) > 0.99
+        assert rel_err(pb, part) < 2.0 ** -7
         px = torch.empty_like(pt)
         moe.experts_combine_grouped(h, dn, E, tid, torch.from_numpy(coef).to(DEV), ws, M, A, partial=px,
                                     math=moe.MOE_MATH_WMMA_BF16)
         assert rel_err(px.cpu().numpy(), part) < 1e-4
+        part = orc.bf16_to_f32(pb)  # what the F16 combine sums
     else:
         # the per-slot down outputs before any bf16 rounding: fp32 accuracy (Q4's 128 + n codes cancel against m - 128 s)
         assert rel_err(pt.cpu().numpy(), part) < 1e-4
     yref, _ = orc.combine(part, ids, coef, E, H)
     assert rel_err(to_np(y), yref) < 1e-2
-    # the f16-h form sums in another order: an output may round to the neighbouring bf16 (2^-8 of its magnitude)
+    # the f16-h form sums in another order: an output may round to the neighbouring bf16 (2^-8 of its magnitude); at
+    # prefill sizes it takes the exact weights with FP32 partials, y the F16 math with BF16 partials (one more rounding
+    # and the F16 weights' own)
     y2 = moe.experts_combine_grouped(hf, dn, E, tid, torch.from_numpy(coef).to(DEV), ws, M, A, h_f16=True)
-    assert rel_err(to_np(y2), to_np(y)) < 2.0 ** -8
+    assert rel_err(to_np(y2), to_np(y)) < (2.0 ** -6 if f16 else 2.0 ** -8)
 
 
 def test_grouped_gather_plain_q4():
@@ -268,9 +281,20 @@ def test_prefill_gemm_ragged_buckets_and_invalid_ids():
                                 ws, M, A, partial=pt)
     b, q, s, m, G = qspec(dn)
     p16 = orc.experts_down_f16math(hz, b, q, s, m, dn.N, I, G, E, ids)
-    ptn = pt.cpu().numpy()
-    assert np.all(np.isnan(ptn[bad]))
-    assert rel_err(ptn[good], p16[good]) < 1e-5
+    # BF16 partials (ragged buckets, NT < 4 sub-tiles, invalid ids): the model rounded to BF16, NaN for invalid slots
+    pb = _bf16_partials(pt)
+    assert np.all(np.isnan(orc.bf16_to_f32(pb[bad])))
+    assert rel_err(pb[good], orc.f32_to_bf16(p16[good])) <= 2.0 ** -8
+    assert np.mean(pb[good] == orc.f32_to_bf16(p16[good])) > 0.99
+    # the combine over BF16 partials: the ordered sum of the stored partials, NaN rows for the invalid ids' tokens
+    y = moe.experts_combine_grouped(torch.from_numpy(hz.view(np.int16)).to(DEV).view(torch.bfloat16), dn, E, tid,
+                                    coef, ws, M, A)
+    yref, _ = orc.combine(orc.bf16_to_f32(pb), ids, np.full((M, A), 0.25, np.float32), E, H)
+    yn = orc.bf16_to_f32(to_np(y))
+    badtok = np.unique(bad // A)
+    oktok = np.setdiff1d(np.arange(M), badtok)
+    assert np.all(np.isnan(yn[badtok]))
+    assert rel_err(to_np(y)[oktok], yref[oktok]) <= 2.0 ** -8
 
 
 def test_perslot_kernels_match_grouped():
@@ -349,6 +373,21 @@ def test_linear_q8_and_swiglu():
     h = moe.swiglu(y, N // 2)
     href = orc.swiglu_bf16(to_np(y), N // 2)
     assert np.abs(to_np(h).astype(np.int32) - href.astype(np.int32)).max() <= 1  # expf ulps
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 3072), (16, 3072, 512), (37, 160, 1024)])
+def test_linear_q4_dense(M, N, K):
+    """The dense Q4 projection (strixite kernels/linear_q4.hpp:23-31) against the oracle's dequantize-then-dot, FP32
+    and BF16 outputs."""
+    say("linear_q4", M, N, K)
+    w = moe.QWeight.synth(4, 12, "gu_q", "gu_s", 3, N, K, 128)
+    x = orc.gen_bf16_normal(orc.tensor_key(12, "x"), 1.0, (M, K))
+    spec = qspec(w)
+    ref = orc.dense(x, orc.qview(*spec[:4], N, K, 128))
+    yf = moe.linear_q4(bf16(x), w, out_dtype=torch.float32)
+    assert rel_err(yf.cpu().numpy(), ref) < 1e-5
+    y = moe.linear_q4(bf16(x), w)
+    assert torch.equal(yf.to(torch.bfloat16), y)
 
 
 def test_shared_add_and_inject():
@@ -499,7 +538,11 @@ def test_layer_config3_uniform_logits():
     say("layer cfg3")
     layer = moe.MoeLayer.synth(3072, 512, 10, 512, seed=0)
     lg = moe.synth_uniform_pm1(0, "logits", 0, (512, 513))
-    _layer_parity(layer, 512, 1, logits_in=lg, sample=48)
+    out, _, _ = _layer_parity(layer, 512, 1, logits_in=lg, sample=48)
+    # routing on all 512 tokens: the top-k of the given logits
+    rids, rcoef, _ = orc.topk(np.ascontiguousarray(to_np(lg)[:, :512]), 512, 10)
+    assert np.array_equal(to_np(out["ids"]), rids)
+    assert np.allclose(to_np(out["coef"]), rcoef, rtol=2e-6, atol=1e-7)
 
 
 def test_layer_config4_zipf_prefill():
@@ -516,3 +559,41 @@ def test_layer_config4_zipf_prefill():
     assert np.array_equal(to_np(out["ids"]), rids)
     cnt = np.bincount(rids.ravel(), minlength=512)
     assert cnt.min() == 0 and cnt.max() > 400  # the load imbalance the config asks for
+
+
+def test_layer_config5_stack_decode_then_prefill():
+    """a stack of consecutive layers with independent per-layer weights and Zipf router biases
+    drawn from the seed, run as a 16-token decode step and then a 4096-token prefill step back to back (both steps'
+    buffers and one shared workspace a step live). Each layer takes its own seeded input, as the bench does (the
+    sublayer has no normalization, so feeding x_out on unnormalized synthetic weights would grow without bound).
+    Every layer: ids bit-exact on every token, and the output on seeded tokens against the oracle."""
+    say("layer cfg5")
+    NL, H, E, k, I = 4, 3072, 512, 10, 512
+    layers = []
+    for l in range(NL):
+        bias = torch.from_numpy(zipf_bias(l, E, 1.0)).to(DEV)
+        layers.append(moe.MoeLayer.synth(H, E, k, I, seed=0, layer=l, router_bias=bias))
+    ctx = moe.LayerContext()
+    steps = {}
+    for M in (16, 4096):
+        ws = layers[0].workspace(M)
+        ins, outs = [], []
+        for l in range(NL):
+            ins.append(moe.synth_bf16_normal(5, "x", 100 * M + l, (M, H), 1.0))
+            outs.append(layers[l].forward(ins[-1], ws=ws, ctx=ctx))
+        steps[M] = (ins, outs)
+    torch.cuda.synchronize()
+    for M, (ins, outs) in steps.items():
+        for l in range(NL):
+            say("cfg5 check", M, l)
+            w = oracle_weights(layers[l])
+            xn = to_np(ins[l])
+            lg = orc.router_logits(xn, w["router"], bias=w["router_bias"])
+            rids, _, _ = orc.topk(lg, E, k)
+            assert np.array_equal(to_np(outs[l]["ids"]), rids), (M, l)
+            rows = np.arange(M) if M <= 16 else np.sort(np.random.default_rng(l).choice(M, 32, replace=False))
+            o = orc.moe_layer(w, np.ascontiguousarray(xn[rows]))
+            assert np.array_equal(to_np(outs[l]["ids"])[rows], o["ids"])
+            assert rel_err(to_np(outs[l]["y"])[rows], o["y"]) < 1e-2, (M, l)
+            assert rel_err(to_np(outs[l]["x_out"])[rows], o["out"]) < 1e-2, (M, l)
+            assert to_np(outs[l]["err"])[0] == 0 and to_np(outs[l]["err"])[3] == 0
