@@ -135,6 +135,15 @@ int strix_moe_layer_forward(const strix_moe_layer_weights *w, const void *x, int
                             void *y, void *x_out, int32_t *ids, float *coef, void *ws, size_t ws_bytes, uint32_t *err,
                             void *stream, void *ctx);
 
+/* No counterpart in the reference: strix_moe_layer_forward for callers that cannot allocate (graph capture, serving
+ * loops, harnesses that forbid hipMalloc). Its scratch is a fixed 16 MiB device array per device, held until the
+ * process ends (strix_moe_layer_noalloc_max_bytes); a call needing more is refused with STRIX_E_PRECONDITION. Calls
+ * that overlap on one device share the array and race. */
+int64_t strix_moe_layer_noalloc_max_bytes(void);
+int strix_moe_layer_forward_noalloc(const strix_moe_layer_weights *w, const void *x, int64_t M,
+                                    const float *logits_in, void *y, void *x_out, int32_t *ids, float *coef,
+                                    uint32_t *err, void *stream);
+
 /* Seeded synthetic tensors on the device (no reference counterpart: the bench's input generator). Element i of a
  * tensor is a function of (key, i) only; key = strix_synth_tensor_key(seed, tensor id, layer). */
 uint64_t strix_synth_tensor_key(uint64_t seed, uint32_t tensor, uint32_t layer);

@@ -62,4 +62,14 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
                        void *x_out, int32_t *ids, float *coef, void *ws, size_t ws_bytes, uint32_t *err,
                        hipStream_t stream, MoeLayerContext *ctx = nullptr);
 
+// No counterpart in the reference: moe_layer_forward for callers that cannot allocate (code under HIP graph capture,
+// serving loops, harnesses that forbid hipMalloc). The scratch is a fixed device array of moe_layer_noalloc_max_bytes()
+// (16 MiB) that the library holds on every device it runs on until the process ends; a call whose
+// moe_layer_workspace_bytes(w, M) exceeds it is refused (strix::Error). Every call on one device shares that array:
+// calls that overlap on a device (other streams, other threads) race. Nothing is allocated; the shared expert runs on
+// the caller's stream.
+size_t moe_layer_noalloc_max_bytes();
+void moe_layer_forward_noalloc(const MoeLayerWeights &w, const void *x, int64_t M, const float *logits_in, void *y,
+                               void *x_out, int32_t *ids, float *coef, uint32_t *err, hipStream_t stream);
+
 }  // namespace strix

@@ -250,6 +250,15 @@ int strix_moe_layer_forward(const strix_moe_layer_weights *w, const void *x, int
     });
 }
 
+int64_t strix_moe_layer_noalloc_max_bytes(void) { return (int64_t)strix::moe_layer_noalloc_max_bytes(); }
+int strix_moe_layer_forward_noalloc(const strix_moe_layer_weights *w, const void *x, int64_t M,
+                                    const float *logits_in, void *y, void *x_out, int32_t *ids, float *coef,
+                                    uint32_t *err, void *stream) {
+    return guard([&] {
+        strix::moe_layer_forward_noalloc(layer_of(w), x, M, logits_in, y, x_out, ids, coef, err, st(stream));
+    });
+}
+
 uint64_t strix_synth_tensor_key(uint64_t seed, uint32_t tensor, uint32_t layer) {
     return strix::synth::tensor_key(seed, tensor, layer);
 }

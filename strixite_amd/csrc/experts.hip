@@ -1575,3 +1575,49 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
 }
 
 }  // namespace strix
+
+// ---- the sublayer on a fixed device scratch array (no workspace argument, no allocation) --------------------------
+namespace strix {
+
+namespace {
+// The layer's scratch (logits, routing tables, h, partials, the shared expert's parts) for callers that cannot
+// allocate: one array per device, held until the process ends. Every call on a device uses the same array.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::array<std::atomic<void *>, kMaxDevices> g_scratch_ptr{};
+std::mutex g_scratch_mu;  // taken only on a device's first call, to look the array's address up once
+
+// The device address of this device's copy of scratch (the array's name in host code is only a stand-in).
+void *scratch_on_current_device(const char *fn) {
+    int dev = 0;
+    STRIX_HIP_CHECK(hipGetDevice(&dev), fn, ": hipGetDevice");
+    STRIX_CHECK(dev >= 0 && dev < kMaxDevices, fn, ": device ", dev, " beyond the ", kMaxDevices, " supported");
+    void *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p != nullptr) return p;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+        STRIX_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), fn, ": address of the scratch array");
+        STRIX_CHECK(p != nullptr && reinterpret_cast<uintptr_t>(p) % 256 == 0, fn, ": scratch array address ", p);
+        g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+}  // namespace
+
+size_t moe_layer_noalloc_max_bytes() { return kNoAllocScratchBytes; }
+
+void moe_layer_forward_noalloc(const MoeLayerWeights &w, const void *x, int64_t M, const float *logits_in, void *y,
+                               void *x_out, int32_t *ids, float *coef, uint32_t *err, hipStream_t stream) {
+    const char *fn = "moe_layer_forward_noalloc";
+    const size_t need = moe_layer_workspace_bytes(w, M);
+    STRIX_CHECK(need <= kNoAllocScratchBytes, fn, ": M = ", M, " tokens need ", need,
+                " bytes of scratch, more than the fixed ", kNoAllocScratchBytes,
+                " of this entry point; call moe_layer_forward with a caller-owned workspace");
+    void *ws = scratch_on_current_device(fn);
+    moe_layer_forward(w, x, M, logits_in, y, x_out, ids, coef, ws, kNoAllocScratchBytes, err, stream, nullptr);
+}
+
+}  // namespace strix
