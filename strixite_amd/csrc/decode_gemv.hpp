@@ -1,0 +1,524 @@
+// Decode-size grouped projections of Q4 (g128) experts, for at most 16 tokens: the gate_up + SwiGLU and the down of
+// the layer's routed experts. Included by experts.hip after the stream kernel (it uses GemmArgs' helpers, the buffer
+// loads, the Q4 decoder and the shared-expert ride-along units).
+//
+// At decode sizes each active expert serves one or two tokens, so the weights are the whole cost: every byte of the
+// active experts' rows is read once and the kernels are judged by how close the stream comes to HBM bandwidth. Two
+// things decide that: enough bytes in flight on every CU, and every wave finishing at the same time.
+//
+// Work units have one size. gate_up: a unit is 16 gate rows and the matching 16 up rows of one expert over all of K
+// (16 h columns); down: 16 rows of one expert over all of K. The units of the layer (active experts x units an expert)
+// are dealt to the waves in contiguous ranges, and only as many waves run as the busiest one's share needs:
+// with N units and W waves, q = ceil(N / W) units for the busiest wave and ceil(N / q) waves active, so no wave does
+// more than q units and hardly any does fewer. The active waves are spread over all blocks (wave-major numbering).
+// A wave streams its units' K steps back to back with the code and scale loads D steps ahead, across unit boundaries.
+//
+// gate_up: all M <= 16 tokens of the batch are the MFMA's A operand for every unit (a token the expert does not
+// serve computes a row nobody stores), so the activations are loaded once per CU into LDS, in MFMA operand order,
+// with their per-group sums; a K step reads them from LDS. One block a CU.
+// down: the A operand is the unit's expert's h rows (its slots), held in registers while consecutive units stay on
+// one expert.
+//
+// Arithmetic as the stream kernel's: weights as exact integer codes in bf16 (common.hpp), v_mfma_f32_16x16x32_bf16
+// over one quantization group, acc += s * D + (m - 128 s) * sum(x over the group) on the FP32 accumulator.
+#pragma once
+
+namespace dec {
+constexpr int kSpan = 128;         // Q4 codes of a row per K step: 4 lane groups x 32 (one quantization group)
+constexpr int kMaxTokens = 16;     // the MFMA's A rows
+constexpr int kMaxSteps = 32;      // K <= 4096 (the activations' LDS image: 4 KB a step)
+}  // namespace dec
+
+struct DecodeArgs {
+    const uint16_t *x;       // gate_up: activations [M, K] BF16; down: h [S, K] BF16
+    const uint8_t *q;        // stacked expert codes [E * N, K / 2]
+    const uint16_t *scale, *minv;
+    int64_t N, K, E, A, M, S;
+    const int32_t *ws;       // the grouping workspace
+    int64_t tiles_bound;
+    void *y;                 // gate_up: h [S, N / 2] BF16; down: partial [S, N] FP32
+    uint32_t q_bytes, s_bytes, x_bytes, y_bytes;
+};
+
+// A unit's per-lane load offsets and its output rows.
+struct DecUnit {
+    uint32_t qoff;           // code bytes of this lane's row (first tile) + its 16-byte lane group
+    uint32_t soff;           // scale bytes of the dword holding this lane's row's group 0 (element e rounded down)
+    uint32_t par;            // e & 1: the row's groups start in the dword's high half
+    int32_t tile, col0;      // tile index; first output column
+    bool nan;                // the tile's bucket is not an expert (invalid ids): NaN outputs
+};
+
+// RPU: weight rows a unit starts apart (its first row is RPU c + lane's row)
+template <int RPU>
+__device__ __forceinline__ DecUnit dec_unit(const DecodeArgs &a, int64_t u, int64_t units_per_tile, int64_t rec0,
+                                            bool valid) {
+    const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
+    DecUnit d;
+    const int32_t t = valid ? (int32_t)(u / units_per_tile) : 0, c = valid ? (int32_t)(u % units_per_tile) : 0;
+    const int32_t bucket = __builtin_amdgcn_readfirstlane(a.ws[rec0 + route::kRec16 * t]);
+    d.nan = bucket < 0 || bucket >= a.E;
+    const uint32_t expert = d.nan ? 0u : (uint32_t)bucket;
+    d.tile = t;
+    d.col0 = RPU * c;
+    const uint32_t row = expert * (uint32_t)a.N + (uint32_t)(RPU * c) + (uint32_t)j;
+    const uint32_t e = row * (uint32_t)(a.K / 128);
+    d.par = e & 1u;
+    d.qoff = valid ? row * (uint32_t)(a.K / 2) + 16u * g : a.q_bytes;
+    d.soff = valid ? (e - d.par) * 2 : a.s_bytes;
+    return d;
+}
+
+// step s reads element e + s: dword (e + s) >> 1 = (e - par) / 2 + (s >> 1) + (par & s), the high half when e + s
+// is odd; the perm selector moves the wanted bf16 to the high half
+__device__ __forceinline__ uint32_t dec_sel(const DecUnit &d, int s) {
+    return (d.par ^ (uint32_t)(s & 1)) ? 0x03020C0Cu : 0x01000C0Cu;
+}
+
+template <int NT> struct DecRing {
+    uint4 q[NT];
+    uint32_t s[NT], m[NT];
+};
+
+// Loads of K step s of unit d (NT tiles: the second tile_q / tile_s bytes on); an invalid unit loads past the end.
+template <int NT>
+__device__ __forceinline__ void dec_fetch(const __amdgpu_buffer_rsrc_t &rq, const __amdgpu_buffer_rsrc_t &rs,
+                                          const __amdgpu_buffer_rsrc_t &rm, const DecUnit &d, int s,
+                                          uint32_t tile_q, uint32_t tile_s, DecRing<NT> &r) {
+    const uint32_t so = d.soff + 4 * (d.par & (uint32_t)s), sd = (uint32_t)(s >> 1) * 4;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        r.q[t] = bld16(rq, d.qoff, (uint32_t)s * 64 + t * tile_q);
+        r.s[t] = bld4(rs, so, sd + t * tile_s);
+        r.m[t] = bld4(rm, so, sd + t * tile_s);
+    }
+}
+
+// Code loads only (the scales come from elsewhere): K step s of the row at qoff (NT tiles, tile_q bytes apart)
+template <int NT>
+__device__ __forceinline__ void dec_fetch(const __amdgpu_buffer_rsrc_t &rq, const __amdgpu_buffer_rsrc_t &,
+                                          const __amdgpu_buffer_rsrc_t &, uint32_t qoff, int s, uint32_t tile_q,
+                                          DecRing<NT> &r) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) r.q[t] = bld16(rq, qoff, (uint32_t)s * 64 + t * tile_q);
+}
+
+// One K step with the scale and min given: acc[t] += s * D + (m - 128 s) * xs
+template <int NT>
+__device__ __forceinline__ void dec_step_f(const DecRing<NT> &r, const Frag (&af)[4], const float (&xs)[4],
+                                           const float (&sc)[NT], const float (&mn)[NT], float4v (&acc)[NT]) {
+    float4v dd[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dd[t] = float4v{0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) dd[t] = mfma_bf16(af[u], b_frag<4>(r.q[t], u), dd[t]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float m = fmaf(-128.0f, sc[t], mn[t]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(sc[t], dd[t][i], fmaf(m, xs[i], acc[t][i]));
+    }
+}
+
+// One K step: acc[t] += s * D + (m - 128 s) * xs, D = the step's four MFMAs over the fragments af
+template <int NT>
+__device__ __forceinline__ void dec_step(const DecRing<NT> &r, const Frag (&af)[4], const float (&xs)[4],
+                                         uint32_t sel, float4v (&acc)[NT]) {
+    float4v dd[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dd[t] = float4v{0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) dd[t] = mfma_bf16(af[u], b_frag<4>(r.q[t], u), dd[t]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float sc = __uint_as_float(__builtin_amdgcn_perm(0u, r.s[t], sel));
+        const float mn = fmaf(-128.0f, sc, __uint_as_float(__builtin_amdgcn_perm(0u, r.m[t], sel)));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(sc, dd[t][i], fmaf(mn, xs[i], acc[t][i]));
+    }
+}
+
+// The wave's unit range [u0, u1) of nu units over nw waves dealt as the header describes; false: this wave is idle.
+__device__ __forceinline__ bool dec_range(int64_t nu, int64_t gw, int64_t nw, int64_t &u0, int64_t &u1) {
+    if (nu <= 0) return false;
+    const int64_t q = (nu + nw - 1) / nw, active = (nu + q - 1) / q;
+    if (gw >= active) return false;
+    u0 = gw * nu / active, u1 = (gw + 1) * nu / active;
+    return u1 > u0;
+}
+
+// ---- gate_up + SwiGLU -------------------------------------------------------------------------------------------------
+// One block a CU, WAVES waves. A unit: 16 gate rows and the matching 16 up rows of one expert (16 h columns); the
+// block takes a contiguous range of units and its waves split K (wave w: steps SPW w .. SPW w + SPW - 1, the same for
+// every unit), so at any moment the block reads whole row spans (DRAM pages) of 32 rows. A wave's code loads run R
+// units ahead.
+// Activations: a wave only ever needs its own SPW groups of K, for all M <= 16 tokens, so it holds them in registers
+// as MFMA A fragments from the start, with their per-group sums.
+// Arithmetic per unit and tile: acc = sum over the wave's groups of s * D_group (D from the bf16 MFMA over the exact
+// codes), plus the min term sum over groups of (m - 128 s) * sum(x over the group) as one FP32 MFMA (16 x 16 x 4:
+// tokens x groups times groups x rows) - the per-step work is the decode, the MFMAs and one FMA per output.
+// The Q4 decode works in the paired k order (k0 k2 k4 k6 k1 k3 k5 k7 of every 8), the activations' fragments are
+// permuted to match once.
+// Scales and mins: a unit's are four contiguous blocks (gate / up x scale / min, 16 rows x groups bf16); each wave
+// loads its share of them with one 16-byte load R units ahead, into registers, and writes it to the unit's LDS buffer
+// at the end of the previous unit, before that unit's barrier (two buffers by unit parity).
+// At a unit's end the waves' partial sums meet in LDS (double-buffered, one barrier a unit) and wave w finishes the
+// tile rows w, w + WAVES, ..., summing the parts in K order: h[slot] = bf16(silu(g) * u).
+// LDS: the partials [2][WAVES][2 tiles][lane] float4, the scale buffers [2][4 blocks][16 rows][groups] bf16, and the
+// tiles' buckets.
+template <int WAVES, int SPW>
+constexpr size_t dec_gu_lds(int max_tiles) {
+    return (size_t)2 * WAVES * 2 * kWave * 16 + (size_t)2 * 4 * 16 * WAVES * SPW * 2 + (size_t)max_tiles * 4;
+}
+
+struct DecUnitG {
+    uint32_t qoff;   // code bytes of this lane's gate row + its 16-byte lane group
+    uint32_t soff;   // bytes of this wave's share of the unit's scale / min blocks (lanes past the share: past the end)
+    int32_t slot;    // lane j < 16: the unit's tile's slot j (-1 past its rows)
+    int32_t col0;    // first h column
+    bool nan;        // the tile's bucket is not an expert (invalid ids): NaN outputs
+};
+
+// 8 Q4 codes (a dword, code i at bits 4 i) -> bf16 128 + code in the paired order k0 k2 k4 k6 k1 k3 k5 k7
+__device__ __forceinline__ Frag q4_paired_to_bf16(uint32_t w) {
+    const uint32_t t = w & 0x0F0F0F0Fu, u = (w >> 4) & 0x0F0F0F0Fu, c = 0x43434343u;
+    // perm(c, v, sel): selector bytes 0..3 pick v's bytes, 4..7 c's: {v.b0, 0x43, v.b1, 0x43}, {v.b2, 0x43, v.b3, 0x43}
+    return Frag{{__builtin_amdgcn_perm(c, t, 0x04010400u), __builtin_amdgcn_perm(c, t, 0x04030402u),
+                 __builtin_amdgcn_perm(c, u, 0x04010400u), __builtin_amdgcn_perm(c, u, 0x04030402u)}};
+}
+// 8 bf16 in natural k order (4 dwords of pairs) -> the paired order
+__device__ __forceinline__ Frag bf16_natural_to_paired(const uint4 &v) {
+    return Frag{{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
+                 __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)}};
+}
+
+template <int WAVES, int SPW, int R, int SH>
+__global__ void __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(WAVES / 4)))
+    decode_gate_up_kernel(DecodeArgs a, SharedJob sh) {
+    constexpr int NT = 2, D = R * SPW, G = WAVES * SPW;  // tiles; ring depth; groups a row
+    static_assert(SPW <= 4, "the min term's MFMA takes 4 groups");
+    // the unit's scale blocks are 8 G pieces of 16 bytes (4 blocks of 2 G); wave w loads pieces P w .. P w + P - 1,
+    // all in one block (WPB waves a block)
+    constexpr int P = 8 * G / WAVES, WPB = 2 * G / P;
+    static_assert(8 * G % WAVES == 0 && 2 * G % P == 0 && P <= kWave, "scale pieces: whole, one block a wave");
+    extern __shared__ uint4 dec_lds[];
+    int bid = (int)blockIdx.x, nblk = (int)gridDim.x;
+    if constexpr (SH == 1) {
+        if (bid < sh.blocks) {  // the shared expert's gate_up finish: h = bf16(silu(sum g) * sum u), a thread each
+            const int64_t i = (int64_t)bid * blockDim.x + threadIdx.x;
+            if (i < sh.units) sh.out[i] = f32_to_bf16(parts_sum<true>(sh.pin, sh.parts, sh.a.M, sh.a.N, i));
+            return;
+        }
+        bid -= sh.blocks, nblk -= sh.blocks;
+    }
+    const int tid = threadIdx.x, lane = tid % kWave, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int g = lane / 16, j = lane % 16;
+    const int sblk = wave / WPB, spart = wave % WPB;  // this wave's scale block (gate s, up s, gate m, up m) and part
+    float4v *red = reinterpret_cast<float4v *>(dec_lds);                         // [2][WAVES][NT][kWave]
+    uint16_t *scl = reinterpret_cast<uint16_t *>(red + 2 * WAVES * NT * kWave);  // [2][4][16][G]
+    int32_t *tb = reinterpret_cast<int32_t *>(scl + 2 * 4 * 16 * G);
+    const int64_t n_tiles = a.ws[0] < a.tiles_bound ? a.ws[0] : a.tiles_bound;
+    const int64_t rec0 = route::t16_rec_at(a.S, a.E);
+    const int64_t upt = a.N / 32;
+    int64_t u0, u1;
+    if (!dec_range(n_tiles * upt, bid, nblk, u0, u1)) return;  // uniform per block, before any barrier
+    const __amdgpu_buffer_rsrc_t rq = rsrc(a.q, a.q_bytes), rs = rsrc(a.scale, a.s_bytes),
+                                 rm = rsrc(a.minv, a.s_bytes), rx = rsrc(a.x, a.x_bytes), ry = rsrc(a.y, a.y_bytes);
+    const uint32_t tile_q = (uint32_t)(a.N / 2) * (uint32_t)(a.K / 2);  // up rows: N / 2 rows on
+    const uint32_t half_s = (uint32_t)(a.N / 2) * G * 2;                // the up rows' scale block
+    const int ldh = (int)(a.N / 2);
+    const int sb = wave * SPW;  // this wave's first step of every unit
+    // Unit (t, c) = tile t, column block c; the prefetch position walks the block's units in order. A position past
+    // the block's last unit describes nothing: its loads read past the buffers' ends and its stores are dropped, so
+    // every unit runs the same instruction stream (no branch changes the compiler's load-wait counts).
+    // (the first units, before the buckets reach LDS: the bucket read from the workspace)
+    const int32_t U1 = (int32_t)u1;
+    auto unit = [&](int32_t u, int32_t t, int32_t c, bool from_ws) __attribute__((always_inline)) {
+        DecUnitG d;
+        const bool valid = u < U1;
+        const int32_t tt = valid ? t : 0;
+        const int32_t bucket = from_ws ? __builtin_amdgcn_readfirstlane(a.ws[rec0 + route::kRec16 * tt]) : tb[tt];
+        d.nan = bucket < 0 || bucket >= a.E;
+        const uint32_t expert = d.nan ? 0u : (uint32_t)bucket;
+        d.col0 = 16 * c;
+        const uint32_t row0 = expert * (uint32_t)a.N + (uint32_t)(16 * c);
+        d.qoff = valid ? (row0 + (uint32_t)j) * (uint32_t)(a.K / 2) + 16u * g : a.q_bytes;
+        // this wave's share of the unit's scale blocks (the up blocks N / 2 rows on)
+        d.soff = valid && lane < P ? row0 * G * 2 + (sblk & 1 ? half_s : 0u) + (uint32_t)(spart * P + lane) * 16
+                                   : a.s_bytes;
+        d.slot = valid ? a.ws[rec0 + route::kRec16 * tt + 4 + j] : -1;
+        return d;
+    };
+    auto scale_load = [&](const DecUnitG &d) __attribute__((always_inline)) {
+        return sblk < 2 ? bld16(rs, d.soff, 0) : bld16(rm, d.soff, 0);
+    };
+    auto scale_store = [&](const uint4 &v, int parity) __attribute__((always_inline)) {
+        if (lane < P) *reinterpret_cast<uint4 *>(scl + parity * 4 * 16 * G + (wave * P + lane) * 8) = v;
+    };
+    const int32_t UPT = (int32_t)upt;
+    int32_t pu = (int32_t)u0, pt = (int32_t)(u0 / upt), pc = (int32_t)(u0 % upt);  // the prefetch position
+    auto advance = [&]() __attribute__((always_inline)) {
+        ++pu;
+        const bool wrap = pc + 1 == UPT;
+        pt += wrap ? 1 : 0;
+        pc = wrap ? 0 : pc + 1;
+    };
+    // this wave's activations (token j, rows past M read zeros), in flight with the first units' loads
+    uint4 xr[SPW][4];
+    {
+        const uint32_t xo = j < a.M ? ((uint32_t)j * (uint32_t)a.K + 32u * g) * 2 : a.x_bytes;
+#pragma unroll
+        for (int t = 0; t < SPW; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) xr[t][v] = bld16(rx, xo, (uint32_t)((sb + t) * dec::kSpan + 8 * v) * 2);
+    }
+    DecUnitG ud[R];
+    uint4 sreg[R];
+    DecRing<NT> ring[D];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        ud[r] = unit(pu, pt, pc, true);
+        advance();
+        sreg[r] = scale_load(ud[r]);
+#pragma unroll
+        for (int t = 0; t < SPW; ++t) dec_fetch<NT>(rq, rs, rm, ud[r].qoff, sb + t, tile_q, ring[r * SPW + t]);
+    }
+    for (int64_t t = tid; t < n_tiles; t += WAVES * kWave) tb[t] = a.ws[rec0 + route::kRec16 * t];
+    scale_store(sreg[0], 0);
+    // the fragments in the paired order, and per group the token sums: lane (g, i) gets sum(x[i] over group sb + g)
+    Frag xf[SPW][4];
+    float xsv = 0.f;
+#pragma unroll
+    for (int t = 0; t < SPW; ++t) {
+        float p = 0.f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            xf[t][v] = bf16_natural_to_paired(xr[t][v]);
+            p = frag_sum(xr[t][v], p);
+        }
+        p += __shfl_xor(p, 16, kWave);
+        p += __shfl_xor(p, 32, kWave);
+        xsv = g == t ? p : xsv;
+    }
+    __syncthreads();  // the buckets and the first unit's scales
+
+    const uint32_t A32 = (uint32_t)a.A;
+    for (int32_t u = (int32_t)u0; u < U1; u += R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {  // unit u + r (past u1: a unit that stores nothing)
+            const DecUnitG nu = unit(pu, pt, pc, false);  // the unit whose loads go into this one's ring slots
+            advance();
+            sreg[r] = scale_load(nu);
+            const int par = (u - (int32_t)u0 + r) & 1;  // the unit's parity: its scale and partial buffers
+            const uint16_t *sc = scl + par * 4 * 16 * G + j * G + sb;  // this lane's row, the wave's first group
+            // the min term: lane (g, j) supplies m' = m - 128 s of row j, group sb + g (zero past the wave's groups)
+            float4v acc[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float sv = bf16_to_f32(sc[t * 16 * G + (g < SPW ? g : 0)]);
+                const float mv = bf16_to_f32(sc[(2 + t) * 16 * G + (g < SPW ? g : 0)]);
+                const float mp = g < SPW ? fmaf(-128.0f, sv, mv) : 0.f;
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xsv, mp, float4v{0, 0, 0, 0}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < SPW; ++t) {
+                float4v dd[NT] = {float4v{0, 0, 0, 0}, float4v{0, 0, 0, 0}};
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int tt = 0; tt < NT; ++tt) {
+                        const uint4 &q = ring[r * SPW + t].q[tt];
+                        dd[tt] = mfma_bf16(xf[t][v], q4_paired_to_bf16(v == 0 ? q.x : v == 1 ? q.y : v == 2 ? q.z : q.w),
+                                           dd[tt]);
+                    }
+#pragma unroll
+                for (int tt = 0; tt < NT; ++tt) {
+                    const float sv = bf16_to_f32(sc[tt * 16 * G + t]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[tt][i] = fmaf(sv, dd[tt][i], acc[tt][i]);
+                }
+                dec_fetch<NT>(rq, rs, rm, nu.qoff, sb + t, tile_q, ring[r * SPW + t]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // the K parts meet: wave w's partials to red[par][w]; the next unit's scales to its buffer; then wave w
+            // finishes tile rows w, w + WAVES (a row past the tile's: slot -1, its store dropped)
+            float4v *rb = red + par * WAVES * NT * kWave;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) rb[(wave * NT + t) * kWave + lane] = acc[t];
+            scale_store(sreg[(r + 1) % R], par ^ 1);
+            lds_barrier();
+#pragma unroll
+            for (int k = 0; k < 16 / WAVES; ++k) {
+                const int32_t sl = __builtin_amdgcn_readlane(ud[r].slot, wave + k * WAVES);
+                const uint32_t tok = sl >= 0 ? (uint32_t)sl / A32 : 0u, i = tok % 4;
+                const int src = (int)(tok / 4) * 16 + j;
+                float gv = 0.f, uv = 0.f;
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) {
+                    gv += reinterpret_cast<const float *>(rb + (w * NT + 0) * kWave + src)[i];
+                    uv += reinterpret_cast<const float *>(rb + (w * NT + 1) * kWave + src)[i];
+                }
+                const float v = ud[r].nan ? qnan() : silu(gv) * uv;
+                const bool live = sl >= 0 && lane < 16;
+                __builtin_amdgcn_raw_buffer_store_b16(
+                    f32_to_bf16(v), ry, live ? ((uint32_t)sl * (uint32_t)ldh + ud[r].col0 + j) * 2 : a.y_bytes, 0, 0);
+            }
+            ud[r] = nu;
+        }
+    }
+    wait_vmcnt<0>();  // no load still landing when the wave ends
+}
+
+// ---- down -------------------------------------------------------------------------------------------------------------
+// A unit: 32 rows (two 16-row tiles) of one expert over K = 512 (four steps). A operand: the tile's h rows (lane (g, i):
+// slot i's 8 values at k = 128 step + 32 g + 8 u), reloaded when the unit's tile changes; their per-group sums come from
+// one more MFMA against an all-ones B. Output: FP32 partials by slot.
+constexpr int kDecDownSteps = 4;
+template <int SH>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+    decode_down_kernel(DecodeArgs a, SharedJob sh) {
+    constexpr int NT = 2, KS = kDecDownSteps, D = KS;  // the ring: one unit ahead
+    int bid = (int)blockIdx.x, nblk = (int)gridDim.x;
+    if constexpr (SH == 2) {
+        if (bid < sh.blocks) {  // the shared expert's down, split-K parts
+            const int64_t w = (int64_t)bid * (blockDim.x / kWave) + threadIdx.x / kWave;
+            if (w < sh.units) dense_part_unit<8>(sh.a, sh.spp, sh.parts, sh.pout, w);
+            return;
+        }
+        bid -= sh.blocks, nblk -= sh.blocks;
+    }
+    const int lane = threadIdx.x % kWave, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int g = lane / 16, j = lane % 16;
+    const int64_t n_tiles = a.ws[0] < a.tiles_bound ? a.ws[0] : a.tiles_bound;
+    const int64_t upt = a.N / 32;
+    int64_t u0, u1;
+    if (!dec_range(n_tiles * upt, (int64_t)wave * nblk + bid, (int64_t)nblk * kWaves, u0, u1)) return;
+    const __amdgpu_buffer_rsrc_t rq = rsrc(a.q, a.q_bytes), rs = rsrc(a.scale, a.s_bytes),
+                                 rm = rsrc(a.minv, a.s_bytes), rx = rsrc(a.x, a.x_bytes), ry = rsrc(a.y, a.y_bytes);
+    const uint32_t tile_q = 16u * (uint32_t)(a.K / 2), tile_s = 16u * (uint32_t)(a.K / 128) * 2;  // +16 rows
+    const int64_t rec0 = route::t16_rec_at(a.S, a.E);
+    const Frag ones{{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}};
+
+    DecUnit cur = dec_unit<32>(a, u0, upt, rec0, true);
+    DecUnit nxt = dec_unit<32>(a, u0 + 1, upt, rec0, u0 + 1 < u1);
+    DecRing<NT> ring[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) dec_fetch<NT>(rq, rs, rm, cur, k, tile_q, tile_s, ring[k]);
+    // segments of units on one tile: the tile's h rows (and their per-group sums) are loaded at a segment's start
+    for (int64_t u = u0; u < u1;) {
+        const int32_t slot_l = a.ws[rec0 + route::kRec16 * cur.tile + 4 + j];  // a slot past the tile's rows: -1
+        const uint32_t xo = slot_l >= 0 ? ((uint32_t)slot_l * (uint32_t)a.K + 32u * g) * 2 : a.x_bytes;
+        Frag hf[KS][4];
+        float hs[KS][4];  // per-group sums of the tile rows this lane's outputs belong to
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint4 t = bld16(rx, xo, (uint32_t)(s * dec::kSpan + 8 * v) * 2);
+                hf[s][v] = Frag{{t.x, t.y, t.z, t.w}};
+            }
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            float4v d = {0, 0, 0, 0};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) d = mfma_bf16(hf[s][v], ones, d);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hs[s][i] = d[i];
+        }
+        const int64_t seg_end = std::min<int64_t>(u1, (int64_t)(cur.tile + 1) * upt);
+        for (; u < seg_end; ++u) {
+            float4v acc[NT] = {float4v{0, 0, 0, 0}, float4v{0, 0, 0, 0}};
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                dec_step<NT>(ring[s], hf[s], hs[s], dec_sel(cur, s), acc);
+                dec_fetch<NT>(rq, rs, rm, nxt, s, tile_q, tile_s, ring[s]);  // step s of the next unit
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // partial[slot][col]: tile row 4 g + i is slot lane (4 g + i)'s record entry
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int32_t sl = __shfl(slot_l, 4 * g + i, kWave);
+                if (sl >= 0)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+                        __builtin_amdgcn_raw_buffer_store_b32(
+                            __float_as_uint(cur.nan ? qnan() : acc[t][i]), ry,
+                            ((uint32_t)sl * (uint32_t)a.N + cur.col0 + 16 * t + j) * 4, 0, 0);
+            }
+            cur = nxt;
+            nxt = dec_unit<32>(a, u + 2, upt, rec0, u + 2 < u1);
+        }
+    }
+}
+
+// ---- launchers ----------------------------------------------------------------------------------------------------------
+constexpr int kDecGuWaves = 8, kDecGuAhead = 2;  // waves a block; units of loads in flight ahead of the math
+constexpr int kDecMaxTiles = 1024;               // M <= 16 tokens x A <= 64 slots
+
+// Q4 g128 experts, at most 16 tokens; gate_up: K = 128 * kDecGuWaves * SPW, SPW in 2..4; down: K = 512
+inline bool decode_fits(const GemmArgs &ga, int64_t M, bool swiglu) {
+    if (ga.G != dec::kSpan || M > dec::kMaxTokens || ga.K % dec::kSpan != 0 || ga.S > kDecMaxTiles) return false;
+    if (swiglu) {
+        const int64_t steps = ga.K / dec::kSpan;
+        return steps % kDecGuWaves == 0 && steps / kDecGuWaves >= 2 && steps / kDecGuWaves <= 4 && (ga.N / 2) % 16 == 0;
+    }
+    return ga.K == dec::kSpan * kDecDownSteps && ga.N % 32 == 0;
+}
+
+inline DecodeArgs decode_args(const GemmArgs &ga, int64_t M, bool swiglu) {
+    DecodeArgs d{};
+    d.x = ga.x, d.q = ga.q, d.scale = ga.scale, d.minv = ga.minv;
+    d.N = ga.N, d.K = ga.K, d.E = ga.E, d.A = ga.A, d.M = M, d.S = ga.S, d.ws = ga.ws;
+    d.tiles_bound = std::min(ga.S, ga.S / 16 + ga.E + 2);
+    d.y = ga.y;
+    const int64_t q_bytes = ga.N * ga.E * ga.K / 2, s_bytes = ga.N * ga.E * (ga.K / ga.G) * 2;
+    const int64_t x_bytes = (swiglu ? M : ga.S) * ga.K * 2;
+    const int64_t y_bytes = swiglu ? ga.S * (ga.N / 2) * 2 : ga.S * ga.N * 4;
+    STRIX_CHECK(q_bytes < (1ll << 31) && s_bytes < (1ll << 31) && x_bytes < (1ll << 31) && y_bytes < (1ll << 31),
+                "decode expert kernels: a tensor at or above 2 GiB (32-bit buffer offsets)");
+    d.q_bytes = (uint32_t)q_bytes, d.s_bytes = (uint32_t)s_bytes, d.x_bytes = (uint32_t)x_bytes;
+    d.y_bytes = (uint32_t)y_bytes;
+    return d;
+}
+
+template <int SPW>
+void launch_decode_gate_up_spw(const DecodeArgs &d, const SharedJob &s, hipStream_t stream) {
+    constexpr int W = kDecGuWaves, R = kDecGuAhead;
+    const size_t lds = dec_gu_lds<W, SPW>(kDecMaxTiles);
+    static thread_local bool attr = false;
+    if (!attr) {
+        for (const void *k : {reinterpret_cast<const void *>(decode_gate_up_kernel<W, SPW, R, 0>),
+                              reinterpret_cast<const void *>(decode_gate_up_kernel<W, SPW, R, 1>)})
+            STRIX_HIP_CHECK(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+                            "decode gate_up: LDS of ", lds, " bytes");
+        attr = true;
+    }
+    const unsigned blocks = (unsigned)(device_cus() + s.blocks);
+    if (s.blocks > 0) decode_gate_up_kernel<W, SPW, R, 1><<<blocks, W * kWave, lds, stream>>>(d, s);
+    else decode_gate_up_kernel<W, SPW, R, 0><<<blocks, W * kWave, lds, stream>>>(d, s);
+}
+
+// gate_up + SwiGLU; sh (optional): the shared expert's gate_up finish riding along in leading blocks
+inline void launch_decode_gate_up(const GemmArgs &ga, int64_t M, const SharedJob *sh, hipStream_t stream) {
+    const DecodeArgs d = decode_args(ga, M, true);
+    SharedJob s = sh ? *sh : SharedJob{};
+    s.blocks = sh ? (int)((s.units + kDecGuWaves * kWave - 1) / (kDecGuWaves * kWave)) : 0;
+    switch (ga.K / dec::kSpan / kDecGuWaves) {
+        case 2: launch_decode_gate_up_spw<2>(d, s, stream); break;
+        case 3: launch_decode_gate_up_spw<3>(d, s, stream); break;
+        default: launch_decode_gate_up_spw<4>(d, s, stream); break;
+    }
+}
+
+// down into FP32 partials; sh (optional): the shared expert's down parts riding along in leading blocks
+inline void launch_decode_down(const GemmArgs &ga, int64_t M, const SharedJob *sh, hipStream_t stream) {
+    const DecodeArgs d = decode_args(ga, M, false);
+    const SharedJob s = sh ? *sh : SharedJob{};
+    const int blocks = 2 * device_cus() + s.blocks;  // two waves a SIMD
+    if (sh) decode_down_kernel<2><<<(unsigned)blocks, kThreads, 0, stream>>>(d, s);
+    else decode_down_kernel<0><<<(unsigned)blocks, kThreads, 0, stream>>>(d, s);
+}

@@ -923,6 +923,8 @@ int swiglu_ks(int64_t spans, int D) {
     return ks;
 }
 
+#include "decode_gemv.hpp"
+
 template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH>
 void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, const SharedJob &sh, hipStream_t stream) {
     constexpr bool SWI = EPI == EPI_SWIGLU;
@@ -1073,6 +1075,8 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
             if (h_f16) launch_expert_gemm<8, GROUPED, EPI_SWIGLU, true, true>(a, stream);
             else launch_expert_gemm<8, GROUPED, EPI_SWIGLU, true, false>(a, stream);
         }
+    } else if (!h_f16 && w.bits == 4 && decode_fits(a, M, true)) {
+        launch_decode_gate_up(a, M, nullptr, stream);
     } else if (h_f16) launch_bits<GROUPED, EPI_SWIGLU, false, true, true>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_SWIGLU, false, true, false>(w.bits, a, tiles, stream);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E, " N=", N, " K=", w.K, " G=", w.G, h_f16 ? " (F16 h)" : "");
@@ -1133,6 +1137,8 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
             pb = f16 && launch_expert_gemm2<EPI_BF16, false, g2::H_BF16, false>(a, stream);
             if (!pb) launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
         } else launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
+    } else if (!h_f16 && w.bits == 4 && M <= dec::kMaxTokens && decode_fits(a, M, false)) {
+        launch_decode_down(a, M, nullptr, stream);
     } else if (h_f16) launch_bits<GROUPED, EPI_F32, true, false, false>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_F32, false, false, false>(w.bits, a, tiles, stream);
     combine_reduce(partial, ids, coef, M, A, E, N, static_cast<uint16_t *>(y), shared, nullptr, nullptr, stream,
@@ -1543,7 +1549,8 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         check_grouped(fn, x, gv, E, route, L.route_bytes, M, k, h, Act::BF16, M * k * I * 2, M);
         GemmArgs a = make_args(gv, E, x, h, I);
         a.A = k, a.ws = static_cast<const int32_t *>(route), a.S = M * k;
-        if (q8) launch_gemm<8, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, k, E), stream, &sh_jobs[0]);
+        if (!q8 && decode_fits(a, M, true)) launch_decode_gate_up(a, M, &sh_jobs[0], stream);
+        else if (q8) launch_gemm<8, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, k, E), stream, &sh_jobs[0]);
         else launch_gemm<4, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, k, E), stream, &sh_jobs[0]);
     } else if (q8) {
         linear_q8_experts_gather_grouped_swiglu(x, gu8, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
@@ -1560,6 +1567,8 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         } else if (use_expert_gemm(M * k, E, dv.K, dv.G)) {
             if (q8) launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
             else launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
+        } else if (!q8 && M <= dec::kMaxTokens && decode_fits(a, M, false)) {
+            launch_decode_down(a, M, fold ? &sh_jobs[1] : nullptr, stream);
         } else if (q8) {
             launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream, fold ? &sh_jobs[1] : nullptr);
         } else {

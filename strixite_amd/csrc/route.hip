@@ -18,46 +18,11 @@ namespace {
 using namespace route;
 
 
-// ---- S <= kSmallWaves * kChunk: one block -------------------------------------------------------------------------
+// ---- S <= kFusedSlots: one block, everything in LDS until the final stores (route_small.hpp) ------------------------
 __global__ void __launch_bounds__(1024) route_small_kernel(const int32_t *ids, Layout L, int nbits, int32_t *ws,
                                                            uint32_t *err) {
-    extern __shared__ int lds[];  // [kSmallWaves][E + 1] counters, then [16][3] scan sums, then first_bad
-    const int E = (int)L.E, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    int *h = lds + wave * (E + 1);
-    int *wsum = lds + kSmallWaves * (E + 1);
-    int *bad = wsum + 48;
-    for (int b = lane; b <= E; b += kWave) h[b] = 0;
-    if (threadIdx.x == 0) *bad = INT_MAX;
-    __syncthreads();
-    const int64_t s0 = (int64_t)wave * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
-    if (s0 < L.S) {
-        const int fb = chunk_hist(ids, s0, s1, E, nbits, h);
-        if (lane == 0 && fb != INT_MAX) atomicMin(bad, fb);
-    }
-    __syncthreads();
-    const int t = threadIdx.x;
-    int cnt = 0;
-    if (t <= E)
-        for (int w = 0; w < kSmallWaves; ++w) cnt += lds[w * (E + 1) + t];
-    int v[3] = {cnt, (cnt + kTileRows - 1) / kTileRows, (cnt + kWideRows - 1) / kWideRows}, tot[3];
-    block_scan3(v, wsum, tot);
-    if (t <= E) {
-        write_bucket(t, cnt, v, ws, L);
-        int run = v[0];
-        for (int w = 0; w < kSmallWaves; ++w) {
-            const int c = lds[w * (E + 1) + t];
-            lds[w * (E + 1) + t] = run;
-            run += c;
-        }
-    }
-    if (t == 0) {
-        write_header(ws, L, tot);
-        report_bad(ids, *bad, err);
-    }
-    __syncthreads();
-    if (s0 < L.S) chunk_place(ids, s0, s1, E, nbits, h, ws + L.slots());
-    __syncthreads();
-    fill_tile_slots(ws, L, tot[1], threadIdx.x, blockDim.x);
+    extern __shared__ int lds[];
+    pack_small_body<1, false>(nullptr, 0, ids, 0, (int)L.E, 0, nullptr, nullptr, L, nbits, ws, nullptr, err, lds);
 }
 
 // ---- larger S: chunk histograms, one scan block, placement ----------------------------------------------------------
@@ -173,9 +138,8 @@ void moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void 
     int nbits = 0;
     while ((1ll << nbits) <= E) ++nbits;  // buckets 0..E
     int32_t *w = static_cast<int32_t *>(ws);
-    if (L.nch <= kSmallWaves) {
-        const size_t lds = ((size_t)kSmallWaves * (E + 1) + 48 + 1) * 4;
-        route_small_kernel<<<1, 1024, lds, stream>>>(ids, L, nbits, w, err);
+    if (L.S <= kFusedSlots) {
+        route_small_kernel<<<1, 1024, topk_route_small_lds(L), stream>>>(ids, L, nbits, w, err);
     } else {
         const unsigned blocks = (unsigned)((L.nch + kWavesPerBlock - 1) / kWavesPerBlock);
         const size_t lds = (size_t)kWavesPerBlock * (E + 1) * 4;

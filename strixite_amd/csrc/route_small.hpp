@@ -158,64 +158,70 @@ __device__ inline void report_bad(const int32_t *ids, int first_bad, uint32_t *e
     }
 }
 
-// ---- top-k + packing for small batches (S = M k <= 1024): one 1024-thread block, ids never leave LDS ---------------
-// Phase A: wave w takes tokens w, w + 16, ...: top-k (ids, coef out, and ids into LDS). Phase B: wave w takes slots
-// [64 w, 64 w + 64): histogram, block scan, placement into LDS, then the workspace written from LDS (slots, offsets,
-// tile records). The workspace layout and contents are those of moe_group_routes.
+// ---- top-k + packing for small batches (S = M k <= 1024): one 1024-thread block --------------------------------------
+// Everything stays in LDS until the last phase, which only stores (ids, coefficients, the workspace tables): a
+// barrier after a global store or before a dependent global load costs a memory round trip, and a one-block launch
+// is a chain of them otherwise.
+// Phase A: TOPK - wave w takes tokens w, w + 16, ...: top-k of the logits into LDS; else the ids are read into LDS.
+// B: wave w takes slots [64 w, 64 w + 64): histogram. C: block scan of the bucket counts. D: stable placement.
+// E: the stores. The workspace layout and contents are those of moe_group_routes.
 constexpr int kFusedSlots = 1024;
 
-template <int NV>
-__device__ inline void topk_route_small_body(const float *logits, int64_t ld, int M, int E, int k, int32_t *ids_out,
-                                             float *coef_out, Layout L, int nbits, int32_t *ws, uint32_t *err_router,
-                                             uint32_t *err_route, int *lds) {
+template <int NV, bool TOPK>
+__device__ inline void pack_small_body(const float *logits, int64_t ld, const int32_t *ids_in, int M, int E, int k,
+                                       int32_t *ids_out, float *coef_out, Layout L, int nbits, int32_t *ws,
+                                       uint32_t *err_router, uint32_t *err_route, int *lds) {
     const int S = (int)L.S, nb = E + 1, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, t = threadIdx.x;
+    const int nthr = (int)blockDim.x;
     int *sids = lds;                          // [S] ids by slot
-    int *sl = sids + kFusedSlots;             // [S] slots by position
+    float *scoef = reinterpret_cast<float *>(sids + kFusedSlots);  // [S] coefficients by slot (TOPK)
+    int *sl = sids + 2 * kFusedSlots;         // [S] slots by position
     int *cnt = sl + kFusedSlots;              // [16][E + 1] wave counts, then cursors
     int *bstart = cnt + kSmallWaves * nb;     // [E + 1] bucket start
     int *btile = bstart + nb;                 // [E + 1] bucket's first 16-slot tile
     int *bcount = btile + nb;                 // [E + 1]
-    int *tile_b = bcount + nb;                // [T16] bucket of a tile
+    int *b64 = bcount + nb;                   // [E + 1] bucket's first 64-slot tile
+    int *tile_b = b64 + nb;                   // [T16] bucket of a tile
     int *wsum = tile_b + L.T16;               // [48]
     int *bad = wsum + 48;                     // [1]
-    // A: top-k
-    for (int m = wave; m < M; m += kSmallWaves) {
-        int id;
-        float cf;
-        const int rb = topk::wave_topk<float, NV>(logits + (int64_t)m * ld, E, k, id, cf);
-        if (rb != INT_MAX) {
-            if (lane == 0 && atomicCAS(&err_router[0], 0u, 1u) == 0u) {
-                err_router[1] = (uint32_t)m;
-                err_router[2] = (uint32_t)rb;
-            }
-            id = -1, cf = dev::qnan();
-        }
-        if (lane < k) {
-            ids_out[m * k + lane] = id;
-            coef_out[m * k + lane] = cf;
-            sids[m * k + lane] = id;
-        }
-    }
     // only the waves that hold slots (chunks of 64) count: their counters are the only ones cleared and summed
     const int nw = (S + kWave - 1) / kWave;
-    for (int i = t; i < nw * nb; i += blockDim.x) cnt[i] = 0;
+    for (int i = t; i < nw * nb; i += nthr) cnt[i] = 0;
     if (t == 0) *bad = INT_MAX;
+    // A
+    if constexpr (TOPK) {
+        for (int m = wave; m < M; m += kSmallWaves) {
+            int id;
+            float cf;
+            const int rb = topk::wave_topk<float, NV>(logits + (int64_t)m * ld, E, k, id, cf);
+            if (rb != INT_MAX) {
+                if (lane == 0 && atomicCAS(&err_router[0], 0u, 1u) == 0u) {
+                    err_router[1] = (uint32_t)m;
+                    err_router[2] = (uint32_t)rb;
+                }
+                id = -1, cf = dev::qnan();
+            }
+            if (lane < k) sids[m * k + lane] = id, scoef[m * k + lane] = cf;
+        }
+    } else {
+        for (int i = t; i < S; i += nthr) sids[i] = ids_in[i];
+    }
     __syncthreads();
-    // B: histogram of this wave's chunk
+    // B
     const int s0 = wave * kWave, s1 = min(s0 + kWave, S);
     if (s0 < S) {
         const int fb = chunk_hist(sids, s0, s1, E, nbits, cnt + wave * nb);
         if (lane == 0 && fb != INT_MAX) atomicMin(bad, fb);
     }
     __syncthreads();
+    // C
     int c = 0;
     if (t <= E)
         for (int w = 0; w < nw; ++w) c += cnt[w * nb + t];
     int v[3] = {c, (c + kTileRows - 1) / kTileRows, (c + kWideRows - 1) / kWideRows}, tot[3];
     block_scan3(v, wsum, tot);
     if (t <= E) {
-        write_bucket(t, c, v, ws, L);
-        bstart[t] = v[0], btile[t] = v[1], bcount[t] = c;
+        bstart[t] = v[0], btile[t] = v[1], bcount[t] = c, b64[t] = v[2];
         for (int i = 0; i < (c + kTileRows - 1) / kTileRows; ++i) tile_b[v[1] + i] = t;
         int run = v[0];
         for (int w = 0; w < nw; ++w) {
@@ -224,26 +230,46 @@ __device__ inline void topk_route_small_body(const float *logits, int64_t ld, in
             run += x;
         }
     }
-    if (t == 0) {
-        write_header(ws, L, tot);
-        // the ids live in LDS here: report_bad reads them through this pointer
-        report_bad(sids, *bad, err_route);
-    }
     __syncthreads();
+    // D
     if (s0 < S) chunk_place(sids, s0, s1, E, nbits, cnt + wave * nb, sl);
     __syncthreads();
-    for (int i = t; i < S; i += blockDim.x) ws[L.slots() + i] = sl[i];
-    // tile records' slot lists from LDS: thread per (tile, slot)
-    for (int i = t; i < tot[1] * kTileRows; i += blockDim.x) {
+    // E: stores only
+    if constexpr (TOPK)
+        for (int i = t; i < S; i += nthr) ids_out[i] = sids[i], coef_out[i] = scoef[i];
+    for (int i = t; i < S; i += nthr) ws[L.slots() + i] = sl[i];
+    if (t <= E) {
+        ws[L.offsets() + t] = bstart[t];
+        const int n64 = (bcount[t] + kWideRows - 1) / kWideRows;
+        for (int i = 0; i < n64; ++i)
+            *reinterpret_cast<int4 *>(ws + L.t64_rec() + 4 * (b64[t] + i)) =
+                make_int4(t, bstart[t] + i * kWideRows, min(kWideRows, bcount[t] - i * kWideRows), 0);
+    }
+    // 16-slot tile records {bucket, first, rows, 0, slot[16]}: a thread per (tile, slot entry)
+    for (int i = t; i < tot[1] * kTileRows; i += nthr) {
         const int ti = i / kTileRows, jj = i % kTileRows, b = tile_b[ti], r = ti - btile[b];
         const int rows = min(kTileRows, bcount[b] - r * kTileRows);
-        ws[L.t16_rec() + kRec16 * ti + 4 + jj] = jj < rows ? sl[bstart[b] + r * kTileRows + jj] : -1;
+        int32_t *rec = ws + L.t16_rec() + kRec16 * ti;
+        if (jj == 0) *reinterpret_cast<int4 *>(rec) = make_int4(b, bstart[b] + r * kTileRows, rows, 0);
+        rec[4 + jj] = jj < rows ? sl[bstart[b] + r * kTileRows + jj] : -1;
+    }
+    if (t == 0) {
+        write_header(ws, L, tot);
+        report_bad(sids, *bad, err_route);  // the ids live in LDS here: report_bad reads them through this pointer
     }
 }
 
-// LDS bytes topk_route_small_body needs
+template <int NV>
+__device__ inline void topk_route_small_body(const float *logits, int64_t ld, int M, int E, int k, int32_t *ids_out,
+                                             float *coef_out, Layout L, int nbits, int32_t *ws, uint32_t *err_router,
+                                             uint32_t *err_route, int *lds) {
+    pack_small_body<NV, true>(logits, ld, nullptr, M, E, k, ids_out, coef_out, L, nbits, ws, err_router, err_route,
+                              lds);
+}
+
+// LDS bytes pack_small_body needs
 inline size_t topk_route_small_lds(const Layout &L) {
-    return ((size_t)2 * kFusedSlots + (size_t)kSmallWaves * (L.E + 1) + 3 * (size_t)(L.E + 1) + (size_t)L.T16 + 48 + 1) * 4;
+    return ((size_t)3 * kFusedSlots + (size_t)kSmallWaves * (L.E + 1) + 4 * (size_t)(L.E + 1) + (size_t)L.T16 + 48 + 1) * 4;
 }
 // ballot bits a bucket index 0..E takes
 inline int bucket_bits(int64_t E) {

@@ -342,7 +342,10 @@ def test_decode_kernels_match_perslot(M, A, E):
     ws, _ = moe.moe_group_routes(tid, E)
     hg = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)
     hp = moe.experts_gather(bf16(x), gu, E, tid, err, swiglu=True)
-    assert torch.equal(hg, hp)
+    # the decode gate_up splits K over a block's waves and adds their FP32 parts in K order; the per-slot kernel sums
+    # over all of K in one wave: an h may round to the neighbouring bf16
+    assert rel_err(to_np(hg), to_np(hp)) <= 2.0 ** -8
+    assert (hg == hp).float().mean().item() > 0.95
     b, q, s, m, G = qspec(gu)
     href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G), E, ids)
     assert rel_err(to_np(hg), href) < 1e-2
