@@ -144,6 +144,12 @@ int strix_moe_layer_forward_noalloc(const strix_moe_layer_weights *w, const void
                                     const float *logits_in, void *y, void *x_out, int32_t *ids, float *coef,
                                     uint32_t *err, void *stream);
 
+/* Calibration kernels for the bench (no reference counterpart): dense f16 MFMA chains on `blocks` blocks of 4 waves
+ * for `iters` iterations (returns the flops launched, -1 on error), and a plain streaming read of `bytes` bytes.
+ * Asynchronous on stream; out: one float of device scratch. */
+int64_t strix_calib_mfma_peak(int64_t blocks, int iters, float *out, void *stream);
+int strix_calib_read_peak(const void *p, int64_t bytes, int64_t blocks, float *out, void *stream);
+
 /* Seeded synthetic tensors on the device (no reference counterpart: the bench's input generator). Element i of a
  * tensor is a function of (key, i) only; key = strix_synth_tensor_key(seed, tensor id, layer). */
 uint64_t strix_synth_tensor_key(uint64_t seed, uint32_t tensor, uint32_t layer);

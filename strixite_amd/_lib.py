@@ -66,6 +66,8 @@ _SIGS = {
     "strix_moe_layer_workspace_bytes": (_i64, [C.POINTER(LayerWeights), _i64]),
     "strix_moe_layer_context_create": (_int, [C.POINTER(_p)]),
     "strix_moe_layer_context_destroy": (_int, [_p]),
+    "strix_calib_mfma_peak": (_i64, [_i64, _int, _p, _p]),
+    "strix_calib_read_peak": (_int, [_p, _i64, _i64, _p, _p]),
     "strix_moe_layer_noalloc_max_bytes": (_i64, []),
     "strix_moe_layer_forward_noalloc": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "strix_moe_layer_forward": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _sz, _p, _p, _p]),
