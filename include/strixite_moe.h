@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define STRIX_MOE_ABI_VERSION 2
+#define STRIX_MOE_ABI_VERSION 3
 #define STRIX_E_PRECONDITION 1
 #define STRIX_E_GPU 2
 #define STRIX_E_OTHER 3
@@ -131,9 +131,20 @@ int64_t strix_moe_layer_workspace_bytes(const strix_moe_layer_weights *w, int64_
  * created before any graph capture, used by one host thread at a time; null: the shared expert runs on stream. */
 int strix_moe_layer_context_create(void **ctx);
 int strix_moe_layer_context_destroy(void *ctx);
+/* inject (optional, with x_out null): the hyper-connection residual end, xs[m, s H + n] = stored(fma(w_in[m, s],
+ * y[m, n], xs[..])) in place over `streams` residual streams (strixite kernels/hc.hpp:51-55), in the combine. */
+typedef struct {
+    void *xs;
+    const float *w_in;
+    int64_t streams;
+} strix_moe_inject_t;
 int strix_moe_layer_forward(const strix_moe_layer_weights *w, const void *x, int64_t M, const float *logits_in,
                             void *y, void *x_out, int32_t *ids, float *coef, void *ws, size_t ws_bytes, uint32_t *err,
-                            void *stream, void *ctx);
+                            void *stream, void *ctx, const strix_moe_inject_t *inject);
+
+/* strixite kernels/hc.hpp:51-55 hc_inject: x[t, s d + j] = stored(fma(w_in[t, s], y[t, j], x[...])) in place */
+int strix_hc_inject(void *x, const float *w_in, const void *y, int64_t T, int64_t H, int64_t d, int act,
+                    void *stream);
 
 /* No counterpart in the reference: strix_moe_layer_forward for callers that cannot allocate (graph capture, serving
  * loops, harnesses that forbid hipMalloc). Its scratch is a fixed 16 MiB device array per device, held until the

@@ -43,6 +43,12 @@ void moe_shared_add_inject(void *y, const void *s, const float *gate_logit, int6
                            uint32_t gate_index, void *x, const float *w_in, int64_t H, Act act, uint32_t *err,
                            hipStream_t stream);
 
+// ---- residual injection: strixite kernels/hc.hpp:51-55 -----------------------------------------------------------
+// In place: x[t, s d + j] = stored(fma(w_in[t, s], y[t, j], x[t, s d + j])), one rounding per element; y must not
+// overlap x. (The rest of kernels/hc.hpp, the hc_mix projections, is not part of this library.)
+void hc_inject(void *x, const float *w_in, const void *y, int64_t T, int64_t H, int64_t d, Act act,
+               hipStream_t stream);
+
 // ---- grouping: strixite kernels/moe_grouped.hpp:46-54 ----------------------------------------------------------
 // ws (int32): [n_tiles, S, E, n_wide_tiles], offsets [E + 2] at ws + 4 (bucket b's slots at slots[offsets[b] ..
 // offsets[b + 1]); bucket E = invalid ids; offsets[E + 1] = S), slots [S] after them - the reference's prefix

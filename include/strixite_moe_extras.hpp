@@ -54,13 +54,22 @@ struct MoeLayerContext;
 MoeLayerContext *moe_layer_context_create();  // on the current device
 void moe_layer_context_destroy(MoeLayerContext *ctx);
 
+// The residual end of a layer with hyper-connections (strixite runtime/qwen4exp.cpp:3206-3216): the layer's stored
+// y injected into `streams` residual streams in place, xs[m, st H + n] = stored(fma(w_in[m, st], y[m, n], xs[..]))
+// (strixite kernels/hc.hpp:51-55), folded into the combine's epilogue.
+struct MoeLayerInject {
+    void *xs = nullptr;            // [M, streams * H] BF16, 16-byte aligned
+    const float *w_in = nullptr;   // [M, streams]
+    int64_t streams = 4;
+};
+
 // x [M, H] BF16 in; y [M, H] BF16 (the MoE output), x_out [M, H] (x + y, may be null, may be x). x, y, x_out 16-byte
 // aligned. logits_in (optional, FP32 [M, E (+1)]) bypasses the router projection. ids / coef (optional, [M, k])
-// receive the routing. err: 6 zeroed uint32 (router word, then expert word). Asynchronous on stream; allocates
-// nothing.
+// receive the routing. err: 6 zeroed uint32 (router word, then expert word). inject (optional, with x_out null): the
+// hyper-connection injection instead of the residual write. Asynchronous on stream; allocates nothing.
 void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const float *logits_in, void *y,
                        void *x_out, int32_t *ids, float *coef, void *ws, size_t ws_bytes, uint32_t *err,
-                       hipStream_t stream, MoeLayerContext *ctx = nullptr);
+                       hipStream_t stream, MoeLayerContext *ctx = nullptr, const MoeLayerInject *inject = nullptr);
 
 // No counterpart in the reference: moe_layer_forward for callers that cannot allocate (code under HIP graph capture,
 // serving loops, harnesses that forbid hipMalloc). The scratch is a fixed device array of moe_layer_noalloc_max_bytes()

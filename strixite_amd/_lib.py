@@ -28,6 +28,10 @@ class SharedAdd(C.Structure):  # strix_moe_shared_add_t
     _fields_ = [("s", _p), ("gate_logit", _p), ("gate_ld", _i64), ("gate_index", _u32), ("err", _p)]
 
 
+class InjectArgs(C.Structure):  # strix_moe_inject_t
+    _fields_ = [("xs", _p), ("w_in", _p), ("streams", _i64)]
+
+
 class LayerWeights(C.Structure):  # strix_moe_layer_weights
     _fields_ = [("H", _i64), ("E", _i64), ("k", _i64), ("I", _i64), ("router", _p), ("router_bias", _p),
                 ("routed_bits", _int), ("gate_up", QView), ("down", QView), ("has_shared", _int),
@@ -70,7 +74,9 @@ _SIGS = {
     "strix_calib_read_peak": (_int, [_p, _i64, _i64, _p, _p]),
     "strix_moe_layer_noalloc_max_bytes": (_i64, []),
     "strix_moe_layer_forward_noalloc": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _p]),
-    "strix_moe_layer_forward": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _sz, _p, _p, _p]),
+    "strix_moe_layer_forward": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _sz, _p, _p, _p,
+                                       C.POINTER(InjectArgs)]),
+    "strix_hc_inject": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _p]),
     "strix_synth_tensor_key": (_u64, [_u64, _u32, _u32]),
     "strix_synth_bf16_normal": (_int, [_u64, _f32, _p, _i64, _p]),
     "strix_synth_q_weight": (_int, [_int, _u64, _u64, _i64, _i64, _i64, _p, _p, _p, _p]),

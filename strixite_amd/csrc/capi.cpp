@@ -243,11 +243,18 @@ int strix_moe_layer_context_destroy(void *ctx) {
 
 int strix_moe_layer_forward(const strix_moe_layer_weights *w, const void *x, int64_t M, const float *logits_in,
                             void *y, void *x_out, int32_t *ids, float *coef, void *ws, size_t ws_bytes, uint32_t *err,
-                            void *stream, void *ctx) {
+                            void *stream, void *ctx, const strix_moe_inject_t *inject) {
     return guard([&] {
+        strix::MoeLayerInject inj;
+        if (inject != nullptr) inj.xs = inject->xs, inj.w_in = inject->w_in, inj.streams = inject->streams;
         strix::moe_layer_forward(layer_of(w), x, M, logits_in, y, x_out, ids, coef, ws, ws_bytes, err, st(stream),
-                                 static_cast<strix::MoeLayerContext *>(ctx));
+                                 static_cast<strix::MoeLayerContext *>(ctx), inject ? &inj : nullptr);
     });
+}
+
+int strix_hc_inject(void *x, const float *w_in, const void *y, int64_t T, int64_t H, int64_t d, int act,
+                    void *stream) {
+    return guard([&] { strix::kernels::hc_inject(x, w_in, y, T, H, d, act_of(act), st(stream)); });
 }
 
 int64_t strix_moe_layer_noalloc_max_bytes(void) { return (int64_t)strix::moe_layer_noalloc_max_bytes(); }

@@ -739,6 +739,9 @@ __global__ void __launch_bounds__(1024)
 
 // y[m, n] = sum_a coef[m, a] * partial[m * A + a, n] in slot order (fmaf), rounded once; NaN for a token with an
 // invalid id. SH: y = stored(sum) + sigmoid(gl) * s (strixite kernels/moe_grouped.hip:948-985). RES: x_out = stored(x + y).
+// INJ (instead of RES): the hyper-connection injection of the stored y into the residual streams, in place,
+// xs[m, st N + n] = stored(fma(w_in[m, st], y, xs[m, st N + n])) for st < streams (strixite kernels/hc.hpp:51-55,
+// moe_router.hpp:56-60: bit-identical to the combine followed by hc_inject).
 // 4 columns a thread (N % 4 == 0); every slot's partials are loaded before the ordered sum, so a thread costs one
 // round trip (the kernel is latency-bound at decode sizes).
 // PB: the partials are BF16 (the F16 math's down stores them so, as the reference's does), else FP32
@@ -746,12 +749,17 @@ __global__ void __launch_bounds__(1024)
 // the FP32 partials and the shared expert's parts are read as float4
 constexpr int kCombineVec = 4;
 static_assert(kCombineVec % 4 == 0, "float4 loads of FP32 partials");
-template <bool SH, bool RES, bool PB>
+struct InjectArgs {
+    uint16_t *xs;        // [M, streams N] BF16, updated in place
+    const float *w_in;   // [M, streams]
+    int64_t streams;
+};
+template <bool SH, bool RES, bool PB, bool INJ = false>
 __global__ void __launch_bounds__(kThreads)
     combine_reduce_kernel(const void *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                           int64_t N, uint16_t *y, const uint16_t *s, const float *gate_logit, int64_t gate_ld,
                           uint32_t gate_index, uint32_t *err, const uint16_t *resid, uint16_t *out,
-                          const float *s_part, int s_parts) {
+                          const float *s_part, int s_parts, InjectArgs inj = {}) {
     constexpr int VEC = kCombineVec, W = VEC / 2;  // W: dwords of VEC bf16
     const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * VEC;
     if (i >= M * N) return;
@@ -845,6 +853,18 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int k = 0; k < W; ++k) yw[k] = pack(v[2 * k], v[2 * k + 1]);
     st_bf16(y + i, yw);
+    if constexpr (INJ) {
+        for (int64_t st = 0; st < inj.streams; ++st) {
+            uint16_t *xp = inj.xs + (m * inj.streams + st) * N + n;
+            const float w = inj.w_in[m * inj.streams + st];
+            uint32_t xw[W], ow[W];
+            ld_bf16(xp, xw);
+#pragma unroll
+            for (int k = 0; k < W; ++k)
+                ow[k] = pack(fmaf(w, lo(yw[k]), lo(xw[k])), fmaf(w, hi(yw[k]), hi(xw[k])));
+            st_bf16(xp, ow);
+        }
+    }
     if constexpr (RES) {
         uint32_t ow[W];
 #pragma unroll
@@ -1085,13 +1105,26 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
 // s_part: the shared expert's down as K parts [s_parts][M][N] instead of the stored sh->s
 void combine_reduce(const void *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                     int64_t N, uint16_t *y, const MoeSharedAdd *sh, const uint16_t *resid, uint16_t *out,
-                    hipStream_t stream, const float *s_part = nullptr, int s_parts = 0, bool partial_bf16 = false) {
+                    hipStream_t stream, const float *s_part = nullptr, int s_parts = 0, bool partial_bf16 = false,
+                    const InjectArgs *inj = nullptr) {
     const unsigned blocks = (unsigned)((M * N / kCombineVec + kThreads - 1) / kThreads);
     const uint16_t *s = sh ? static_cast<const uint16_t *>(sh->s) : nullptr;
     const float *gl = sh ? sh->gate_logit : nullptr;
     const int64_t gld = sh ? sh->gate_ld : 0;
     const uint32_t gi = sh ? sh->gate_index : 0;
     uint32_t *err = sh ? sh->err : nullptr;
+    if (inj != nullptr) {  // the injection replaces the residual write
+        auto gi_ = [&](auto shc, auto pbc) {
+            combine_reduce_kernel<decltype(shc)::value, false, decltype(pbc)::value, true>
+                <<<blocks, kThreads, 0, stream>>>(partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, nullptr,
+                                                  nullptr, s_part, s_parts, *inj);
+        };
+        if (sh && partial_bf16) gi_(std::true_type{}, std::true_type{});
+        else if (sh) gi_(std::true_type{}, std::false_type{});
+        else if (partial_bf16) gi_(std::false_type{}, std::true_type{});
+        else gi_(std::false_type{}, std::false_type{});
+        return;
+    }
     auto go = [&](auto shc, auto resc) {
         if (partial_bf16)
             combine_reduce_kernel<decltype(shc)::value, decltype(resc)::value, true><<<blocks, kThreads, 0, stream>>>(
@@ -1390,7 +1423,7 @@ void moe_layer_context_destroy(MoeLayerContext *c) {
 
 void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const float *logits_in, void *y,
                        void *x_out, int32_t *ids_out, float *coef_out, void *ws, size_t ws_bytes, uint32_t *err,
-                       hipStream_t stream, MoeLayerContext *ctx) {
+                       hipStream_t stream, MoeLayerContext *ctx, const MoeLayerInject *inject) {
     using namespace kernels;
     const char *fn = "moe_layer_forward";
     STRIX_CHECK(x != nullptr && y != nullptr && ws != nullptr && err != nullptr, fn, ": null pointer");
@@ -1417,6 +1450,16 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         STRIX_CHECK(disjoint(x_out, act_bytes, ws, (int64_t)ws_bytes) && disjoint(x_out, act_bytes, y, act_bytes) &&
                         (x_out == x || disjoint(x_out, act_bytes, x, act_bytes)),
                     fn, ": x_out overlaps the workspace or y, or partly overlaps x");
+    if (inject != nullptr) {
+        STRIX_CHECK(x_out == nullptr, fn, ": the injection replaces the residual write; x_out must be null");
+        STRIX_CHECK(inject->xs != nullptr && inject->w_in != nullptr && inject->streams >= 1 && inject->streams <= 64,
+                    fn, ": injection with a null pointer or streams = ", inject->streams, " (1..64)");
+        STRIX_CHECK(reinterpret_cast<uintptr_t>(inject->xs) % 16 == 0, fn, ": the streams must be 16-byte aligned");
+        const int64_t xb = act_bytes * inject->streams;
+        STRIX_CHECK(disjoint(inject->xs, xb, y, act_bytes) && disjoint(inject->xs, xb, ws, (int64_t)ws_bytes) &&
+                        disjoint(inject->xs, xb, x, act_bytes),
+                    fn, ": the residual streams overlap y, x or the workspace");
+    }
     char *base = static_cast<char *>(ws);
     const int64_t E = w.E, k = w.k, H = w.H, I = w.I, ld = E + (w.has_shared ? 1 : 0);
     float *logits = reinterpret_cast<float *>(base + L.logits);
@@ -1577,9 +1620,11 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     }
     if (ctx != nullptr && w.has_shared && !fold) STRIX_HIP_CHECK(hipStreamWaitEvent(stream, ctx->join, 0), fn, ": join wait");
     const MoeSharedAdd sh{sh_s, lg + E, ld, (uint32_t)E, err_router};
+    const InjectArgs inj = inject ? InjectArgs{static_cast<uint16_t *>(inject->xs), inject->w_in, inject->streams}
+                                  : InjectArgs{};
     combine_reduce(partial, ids, coef, M, k, E, H, static_cast<uint16_t *>(y), w.has_shared ? &sh : nullptr,
                    static_cast<const uint16_t *>(x), static_cast<uint16_t *>(x_out), stream, fold ? sh_part : nullptr,
-                   fold ? sh_jobs[1].parts : 0, f16p);
+                   fold ? sh_jobs[1].parts : 0, f16p, inject ? &inj : nullptr);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " E=", E, " k=", k);
 }
 
@@ -1626,7 +1671,7 @@ void moe_layer_forward_noalloc(const MoeLayerWeights &w, const void *x, int64_t 
                 " bytes of scratch, more than the fixed ", kNoAllocScratchBytes,
                 " of this entry point; call moe_layer_forward with a caller-owned workspace");
     void *ws = scratch_on_current_device(fn);
-    moe_layer_forward(w, x, M, logits_in, y, x_out, ids, coef, ws, kNoAllocScratchBytes, err, stream, nullptr);
+    moe_layer_forward(w, x, M, logits_in, y, x_out, ids, coef, ws, kNoAllocScratchBytes, err, stream, nullptr, nullptr);
 }
 
 }  // namespace strix

@@ -351,6 +351,16 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
+// strixite kernels/hc.hpp:51-55: x[t, s d + j] = stored(fma(w_in[t, s], y[t, j], x[t, s d + j])), in place
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    hc_inject_kernel(T *x, const float *w_in, const T *y, int64_t T_, int64_t H, int64_t d) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < T_ * H * d; i += (int64_t)gridDim.x * kThreads) {
+        const int64_t t = i / (H * d), s = (i / d) % H, jj = i % d;
+        st_act(x, i, fmaf(w_in[t * H + s], ld_act(y, t * d + jj), ld_act(x, i)));
+    }
+}
+
 unsigned elementwise_blocks(int64_t n) {
     const int64_t b = (n + kThreads - 1) / kThreads;
     return (unsigned)(b < 65536 ? b : 65536);
@@ -465,6 +475,24 @@ void moe_shared_add(void *y, const void *s, const float *gate_logit, int64_t gat
                     uint32_t gate_index, Act act, uint32_t *err, hipStream_t stream) {
     shared_add_common<false>("moe_shared_add", y, s, gate_logit, gate_ld, M, N, gate_index, nullptr, nullptr, 0, act,
                              err, stream);
+}
+
+void hc_inject(void *x, const float *w_in, const void *y, int64_t T, int64_t H, int64_t d, Act act,
+               hipStream_t stream) {
+    const char *fn = "hc_inject";
+    STRIX_CHECK(x != nullptr && w_in != nullptr && y != nullptr, fn, ": null pointer");
+    STRIX_CHECK(T >= 1 && H >= 1 && d >= 1 && T * H * d <= (1ll << 40), fn, ": T = ", T, ", H = ", H, ", d = ", d);
+    STRIX_CHECK(act == Act::F32 || act == Act::BF16, fn, ": unsupported activation dtype ", (int)act);
+    const int64_t es = act == Act::F32 ? 4 : 2;
+    STRIX_CHECK(disjoint(x, T * H * d * es, y, T * d * es), fn, ": y overlaps x");
+    const unsigned blocks = elementwise_blocks(T * H * d);
+    if (act == Act::F32)
+        hc_inject_kernel<float><<<blocks, kThreads, 0, stream>>>(static_cast<float *>(x), w_in,
+                                                                static_cast<const float *>(y), T, H, d);
+    else
+        hc_inject_kernel<uint16_t><<<blocks, kThreads, 0, stream>>>(static_cast<uint16_t *>(x), w_in,
+                                                                   static_cast<const uint16_t *>(y), T, H, d);
+    STRIX_HIP_CHECK_LAUNCH(fn, " ", act_str(act), " T=", T, " H=", H, " d=", d);
 }
 
 void moe_shared_add_inject(void *y, const void *s, const float *gate_logit, int64_t gate_ld, int64_t M, int64_t N,

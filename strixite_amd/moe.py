@@ -285,6 +285,13 @@ def linear_q4(x: torch.Tensor, w: QWeight, out_dtype=torch.bfloat16) -> torch.Te
     return y
 
 
+def hc_inject(x: torch.Tensor, w_in: torch.Tensor, y: torch.Tensor) -> None:
+    """strixite kernels/hc.hpp:51-55, in place: x [T, H d] += w_in [T, H] * y [T, d] per stream, one rounding."""
+    T, Hd = x.shape
+    H = w_in.shape[1]
+    L.check(L.lib().strix_hc_inject(_p(x), _p(w_in), _p(y), T, H, Hd // H, _act(x), _stream()))
+
+
 # ---- the sublayer ----------------------------------------------------------------------------------------------
 class LayerContext:
     """The helper stream (and its fork / join events) on which the sublayer runs the shared expert beside the routing
@@ -361,12 +368,18 @@ class MoeLayer:
         return torch.empty(self.workspace_bytes(M), dtype=torch.uint8, device=device)
 
     def forward(self, x: torch.Tensor, logits_in: torch.Tensor | None = None, ws: torch.Tensor | None = None,
-                out: dict | None = None, ctx: LayerContext | None = None) -> dict:
+                out: dict | None = None, ctx: LayerContext | None = None, inject: tuple | None = None) -> dict:
         """Returns {y, x_out, ids, coef, err[6]} (asynchronous; the tensors are filled on the current stream). ctx: a
-        LayerContext for the shared expert's helper stream at prefill sizes (None: it runs on the current stream)."""
+        LayerContext for the shared expert's helper stream at prefill sizes (None: it runs on the current stream).
+        inject: (xs [M, streams * H] bf16, w_in [M, streams] f32): the hyper-connection injection into xs in place,
+        instead of the x_out residual write."""
         M = x.shape[0]
         if ws is None:
             ws = self.workspace(M, x.device)
+        inj = None
+        if inject is not None:
+            xs, w_in = inject
+            inj = L.InjectArgs(_p(xs), _p(w_in), w_in.shape[1])
         if out is None:
             out = {
                 "y": torch.empty((M, self.H), dtype=torch.bfloat16, device=x.device),
@@ -376,6 +389,8 @@ class MoeLayer:
                 "err": torch.zeros(6, dtype=torch.int32, device=x.device),
             }
         L.check(L.lib().strix_moe_layer_forward(C.byref(self._w), _p(x), M, _p(logits_in), _p(out["y"]),
-                                                _p(out["x_out"]), _p(out["ids"]), _p(out["coef"]), _p(ws), ws.numel(),
-                                                _p(out["err"]), _stream(), ctx.handle if ctx is not None else None))
+                                                _p(out["x_out"]) if inj is None else None, _p(out["ids"]),
+                                                _p(out["coef"]), _p(ws), ws.numel(),
+                                                _p(out["err"]), _stream(), ctx.handle if ctx is not None else None,
+                                                C.byref(inj) if inj is not None else None))
         return out

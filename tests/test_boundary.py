@@ -18,7 +18,7 @@ def test_library_exports_every_declared_symbol():
     assert len(declared) >= 25
     missing = [n for n in declared if not hasattr(L, n)]
     assert not missing, missing
-    assert L.strix_moe_abi_version() == 2
+    assert L.strix_moe_abi_version() == 3
 
 
 def test_cpp_header_declares_reference_signatures():

@@ -600,3 +600,31 @@ def test_layer_config5_stack_decode_then_prefill():
             assert rel_err(to_np(outs[l]["y"])[rows], o["y"]) < 1e-2, (M, l)
             assert rel_err(to_np(outs[l]["x_out"])[rows], o["out"]) < 1e-2, (M, l)
             assert to_np(outs[l]["err"])[0] == 0 and to_np(outs[l]["err"])[3] == 0
+
+
+@pytest.mark.parametrize("M", [16, 600])
+def test_layer_hyperconnection_inject(M):
+    """The layer's residual end with hyper-connections (strixite runtime/qwen4exp.cpp:3206-3216): the stored y injected
+    into 4 residual streams in place by the combine's epilogue equals the layer without it followed by the standalone
+    hc_inject bit for bit, and hc_inject equals its closed form xs + w_in * y (one FP32 fma, one bf16 rounding)."""
+    say("hc inject", M)
+    layer = moe.MoeLayer.synth(1024, 64, 8, 256, seed=8)
+    x = moe.synth_bf16_normal(8, "x", 1, (M, 1024), 1.0)
+    rng = np.random.default_rng(M)
+    xs0 = orc.f32_to_bf16(rng.standard_normal((M, 4 * 1024)).astype(np.float32))
+    w_in = torch.from_numpy((2 / (1 + np.exp(-rng.standard_normal((M, 4))))).astype(np.float32)).to(DEV)
+    xs = bf16(xs0.copy())
+    out = layer.forward(x, inject=(xs, w_in))
+    ref = layer.forward(x)
+    xr = bf16(xs0.copy())
+    moe.hc_inject(xr, w_in, ref["y"])
+    torch.cuda.synchronize()
+    assert torch.equal(out["y"], ref["y"]) and torch.equal(out["ids"], ref["ids"])
+    assert torch.equal(xs, xr)
+    # closed form: fma in float64 (exact product), rounded to FP32, then to bf16
+    yv = orc.bf16_to_f32(to_np(ref["y"])).astype(np.float64)
+    wv = to_np(w_in).astype(np.float64)
+    cf = (wv[:, :, None] * yv[:, None, :] + orc.bf16_to_f32(xs0).reshape(M, 4, 1024)).astype(np.float32)
+    want = orc.f32_to_bf16(cf.reshape(M, 4 * 1024))
+    got = to_np(xs)
+    assert np.mean(got == want) > 0.9999 and np.abs(got.astype(np.int32) - want.astype(np.int32)).max() <= 1
