@@ -124,6 +124,7 @@ typedef struct {
     strix_qview gate_up, down;
     int has_shared;
     strix_qview sh_gate_up, sh_down;
+    int shared_stacked; /* the shared expert is expert E of gate_up / down, routed as slot k (ids / coef [M, k + 1]) */
 } strix_moe_layer_weights;
 
 int64_t strix_moe_layer_workspace_bytes(const strix_moe_layer_weights *w, int64_t M);

@@ -41,6 +41,10 @@ struct MoeLayerWeights {
     Q4DeviceView gate_up, down;          // stacked [E * 2I, H], [E * H, I]; a Q8 view uses the same fields
     bool has_shared = false;
     Q8DeviceView sh_gate_up, sh_down;    // [2I, H], [H, I]
+    // The shared expert stacked as expert E of gate_up / down (the converter's default layout, strixite
+    // formats/merge_plan.cpp:31-41; has_shared false): the views then hold E + 1 experts, and every token routes to
+    // it as slot k (id E, coefficient sigmoid(its gate logit, router row E)), so ids / coef are [M, k + 1].
+    bool shared_stacked = false;
 };
 
 // Bytes of caller-owned device scratch for moe_layer_forward at up to M tokens.

@@ -313,7 +313,7 @@ def combine(partial, ids, coef, E, N, s=None, gate_logit=None, gate_ld=1, resid=
 class _Layer(C.Structure):
     _fields_ = [("M", _i64), ("H", _i64), ("E", _i64), ("k", _i64), ("I", _i64), ("x", _p), ("router", _p),
                 ("router_bias", _p), ("logits_in", _p), ("ld_in", _i64), ("gate_up", QView), ("down", QView),
-                ("has_shared", C.c_int), ("sh_gate_up", QView), ("sh_down", QView)]
+                ("has_shared", C.c_int), ("sh_gate_up", QView), ("sh_down", QView), ("shared_stacked", C.c_int)]
 
 
 class _LayerOut(C.Structure):
@@ -324,12 +324,15 @@ class _LayerOut(C.Structure):
 
 def moe_layer(w: dict, x: np.ndarray, logits_in: np.ndarray | None = None, threads: int | None = None) -> dict:
     """The whole MoE sublayer on the CPU. ``w`` holds numpy arrays: router [E(+1), H] bf16 bits, router_bias
-    (optional), gu/dn = (bits, q, s, m, G) for the stacked routed experts, sh_gu/sh_dn likewise (optional)."""
+    (optional), gu/dn = (bits, q, s, m, G) for the stacked routed experts, sh_gu/sh_dn likewise (optional);
+    shared_stacked: the shared expert is expert E of gu/dn, routed as slot k (ids / coef then [M, k + 1])."""
     M, H = x.shape
     E, k, I = w["E"], w["k"], w["I"]
     has_sh = "sh_gu" in w
-    ld = E + (1 if has_sh else 0)
-    A = k
+    stacked = bool(w.get("shared_stacked")) and not has_sh
+    ld = E + (1 if has_sh or stacked else 0)
+    A = k + (1 if stacked else 0)
+    Es = E + (1 if stacked else 0)
     keep = []
 
     def qv(spec, N, K):
@@ -344,15 +347,16 @@ def moe_layer(w: dict, x: np.ndarray, logits_in: np.ndarray | None = None, threa
     L.router_bias = _ptr(w.get("router_bias"))
     L.logits_in = _ptr(logits_in)
     L.ld_in = 0 if logits_in is None else logits_in.shape[1]
-    L.gate_up = qv(w["gu"], E * 2 * I, H)
-    L.down = qv(w["dn"], E * H, I)
+    L.gate_up = qv(w["gu"], Es * 2 * I, H)
+    L.down = qv(w["dn"], Es * H, I)
     L.has_shared = 1 if has_sh else 0
+    L.shared_stacked = 1 if stacked else 0
     if has_sh:
         L.sh_gate_up = qv(w["sh_gu"], 2 * I, H)
         L.sh_down = qv(w["sh_dn"], H, I)
     o = {
         "logits": np.empty((M, ld), np.float32), "ids": np.empty((M, A), np.int32),
-        "coef": np.empty((M, A), np.float32), "offsets": np.empty(E + 2, np.int32),
+        "coef": np.empty((M, A), np.float32), "offsets": np.empty(Es + 2, np.int32),
         "slots": np.empty(M * A, np.int32), "h": np.empty((M * A, I), np.uint16),
         "partial": np.empty((M * A, H), np.float32), "sh_h": np.empty((M, I), np.uint16),
         "sh_s": np.empty((M, H), np.uint16), "y": np.empty((M, H), np.uint16), "out": np.empty((M, H), np.uint16),

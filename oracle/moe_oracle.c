@@ -504,8 +504,9 @@ void orc_combine(const float *partial, const int32_t *ids, const float *coef, in
  * SwiGLU, down + ordered combine, shared expert (dense projections, its gated add folded into the combine),
  * then the residual write */
 int orc_moe_layer(const orc_layer *L, orc_layer_out *o, int threads) {
-    const int64_t M = L->M, H = L->H, E = L->E, k = L->k, I = L->I, A = k;
-    const int64_t ld = E + (L->has_shared ? 1 : 0);
+    const int stacked = L->shared_stacked && !L->has_shared;
+    const int64_t M = L->M, H = L->H, E = L->E, k = L->k, I = L->I, A = k + (stacked ? 1 : 0);
+    const int64_t ld = E + (L->has_shared || stacked ? 1 : 0), Es = E + (stacked ? 1 : 0);
     const orc_qview *views[4] = {&L->gate_up, &L->down, &L->sh_gate_up, &L->sh_down};
     for (int i = 0; i < (L->has_shared ? 4 : 2); ++i)
         if (!group_ok(views[i]->N, views[i]->K, views[i]->G) || views[i]->K < views[i]->G) return -1;
@@ -516,14 +517,16 @@ int orc_moe_layer(const orc_layer *L, orc_layer_out *o, int threads) {
     } else {
         orc_router_logits(L->x, L->router, M, ld, H, L->router_bias, L->router_bias ? E : 0, o->logits, threads);
     }
-    if (orc_topk(o->logits, ld, M, E, k, NULL, 0, 0, o->ids, o->coef, o->err_router) != 0) return -1;
+    if (orc_topk(o->logits, ld, M, E, k, stacked ? o->logits + E : NULL, ld, (int32_t)E, o->ids, o->coef,
+                 o->err_router) != 0)
+        return -1;
     /* the shared gate logit is checked as the router does (moe_shared_add's error) */
     if (L->has_shared)
         for (int64_t m = 0; m < M && o->err_router[0] == 0; ++m)
             if (!isfinite(o->logits[m * ld + E])) o->err_router[0] = 1, o->err_router[1] = (uint32_t)m, o->err_router[2] = (uint32_t)E;
-    orc_group_routes(o->ids, M, A, E, o->offsets, o->slots, o->err_route);
-    orc_experts_gate_up_swiglu(L->x, &L->gate_up, E, o->ids, M, A, o->h, threads);
-    orc_experts_down(o->h, &L->down, E, o->ids, M, A, o->partial, threads);
+    orc_group_routes(o->ids, M, A, Es, o->offsets, o->slots, o->err_route);
+    orc_experts_gate_up_swiglu(L->x, &L->gate_up, Es, o->ids, M, A, o->h, threads);
+    orc_experts_down(o->h, &L->down, Es, o->ids, M, A, o->partial, threads);
     if (L->has_shared) {
         float *gu = (float *)malloc((size_t)(M * 2 * I) * 4);
         orc_dense(L->x, &L->sh_gate_up, M, gu, threads);
@@ -536,7 +539,7 @@ int orc_moe_layer(const orc_layer *L, orc_layer_out *o, int threads) {
         for (int64_t i = 0; i < M * H; ++i) o->sh_s[i] = orc_f32_to_bf16(sf[i]);
         free(sf);
     }
-    orc_combine(o->partial, o->ids, o->coef, M, A, E, H, L->has_shared ? o->sh_s : NULL,
+    orc_combine(o->partial, o->ids, o->coef, M, A, Es, H, L->has_shared ? o->sh_s : NULL,
                 L->has_shared ? o->logits + E : NULL, ld, o->y, L->x, o->out);
     return 0;
 }

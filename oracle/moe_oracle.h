@@ -115,16 +115,20 @@ typedef struct {
     orc_qview gate_up, down;    /* routed experts, stacked */
     int has_shared;
     orc_qview sh_gate_up, sh_down;
+    /* the shared expert stacked as expert E of gate_up / down (strixite formats/merge_plan.cpp:31-41; has_shared
+     * 0): routed as slot k of every token, id E, coef sigmoid(logit E) (moe_router's shared slot,
+     * kernels/moe_router.hip:108-111), so A = k + 1 and the expert views hold E + 1 experts */
+    int shared_stacked;
 } orc_layer;
 
 typedef struct {
-    float *logits;      /* [M, E + has_shared] */
-    int32_t *ids;       /* [M, k] */
-    float *coef;        /* [M, k] */
-    int32_t *offsets;   /* [E + 2] */
-    int32_t *slots;     /* [M * k] */
-    uint16_t *h;        /* [M * k, I] */
-    float *partial;     /* [M * k, H] */
+    float *logits;      /* [M, E + (has_shared or shared_stacked)] */
+    int32_t *ids;       /* [M, A], A = k (+ 1 stacked) */
+    float *coef;        /* [M, A] */
+    int32_t *offsets;   /* [E' + 2], E' = E (+ 1 stacked) */
+    int32_t *slots;     /* [M * A] */
+    uint16_t *h;        /* [M * A, I] */
+    float *partial;     /* [M * A, H] */
     uint16_t *sh_h;     /* [M, I] (has_shared) */
     uint16_t *sh_s;     /* [M, H] (has_shared) */
     uint16_t *y;        /* [M, H] MoE output */

@@ -35,7 +35,7 @@ class InjectArgs(C.Structure):  # strix_moe_inject_t
 class LayerWeights(C.Structure):  # strix_moe_layer_weights
     _fields_ = [("H", _i64), ("E", _i64), ("k", _i64), ("I", _i64), ("router", _p), ("router_bias", _p),
                 ("routed_bits", _int), ("gate_up", QView), ("down", QView), ("has_shared", _int),
-                ("sh_gate_up", QView), ("sh_down", QView)]
+                ("sh_gate_up", QView), ("sh_down", QView), ("shared_stacked", _int)]
 
 
 _SIGS = {

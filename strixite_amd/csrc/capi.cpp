@@ -70,6 +70,7 @@ strix::MoeLayerWeights layer_of(const strix_moe_layer_weights *w) {
     L.gate_up = q4(&w->gate_up), L.down = q4(&w->down);
     L.has_shared = w->has_shared != 0;
     if (L.has_shared) L.sh_gate_up = q8(&w->sh_gate_up), L.sh_down = q8(&w->sh_down);
+    L.shared_stacked = w->shared_stacked != 0;
     return L;
 }
 }  // namespace

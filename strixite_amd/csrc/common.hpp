@@ -12,21 +12,23 @@
 
 namespace strix {
 
-// Internal entry (route.hip), used by the layer forward for small batches: top-k of FP32 logits (no shared-expert
-// slot) and the packing of moe_group_routes in one launch, M k <= 1024.
+// Internal entry (route.hip), used by the layer forward for small batches: top-k of FP32 logits (shared_slot: plus
+// the shared expert as slot k, id E, its gate logit at column E) and the packing of moe_group_routes (over E + 1
+// experts with the shared slot) in one launch, M A <= 1024.
 namespace kernels {
 // "F32" / "BF16" for messages (strixite's act_name lives in its kernels/norm.hip; this library does not export one)
 const char *act_str(Act a);
 void moe_topk_group_routes_small(const float *logits, int64_t ld, int64_t M, int64_t E, int64_t k, int32_t *ids,
                                  float *coef, void *ws, size_t ws_bytes, uint32_t *err_router, uint32_t *err_route,
-                                 hipStream_t stream);
+                                 hipStream_t stream, bool shared_slot = false);
 // Internal entry (router_prefill.hip), used by the layer forward for prefill-size batches: router projection (+ the
 // optional FP32 bias) and top-k with the canonical order's exact routing via bf16 MFMA plus exact recomputation of the
 // candidates. logits: [4][M][E (+1)] floats (the layer's logits are part 0); norms: 4 (M + E (+1)) floats of
-// scratch. Returns false (nothing launched) for shapes it does not take.
+// scratch. shared_slot (with shared): the shared expert routed as slot k of every token (id E, coefficient
+// sigmoid(its gate logit)): ids / coef [M, k + 1]. Returns false (nothing launched) for shapes it does not take.
 bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
                         int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
-                        hipStream_t stream);
+                        hipStream_t stream, bool shared_slot = false);
 }  // namespace kernels
 
 // ---- host-side checks -----------------------------------------------------------------------------------------

@@ -1360,7 +1360,8 @@ struct LayerWs {
 int64_t al(int64_t b) { return (b + 255) / 256 * 256; }
 LayerWs layer_ws(const MoeLayerWeights &w, int64_t M) {
     LayerWs L{};
-    const int64_t E = w.E, k = w.k, H = w.H, I = w.I, ld = E + (w.has_shared ? 1 : 0);
+    const int64_t E = w.E, H = w.H, I = w.I, ld = E + (w.has_shared || w.shared_stacked ? 1 : 0);
+    const int64_t k = w.k + (w.shared_stacked ? 1 : 0), Es = E + (w.shared_stacked ? 1 : 0);  // slots a token
     int64_t o = 0;
     // the prefill router's K parts of approximate logits (the layer's logits are part 0) and their squared norms
     // (room for up to 4 parts)
@@ -1368,7 +1369,7 @@ LayerWs layer_ws(const MoeLayerWeights &w, int64_t M) {
     L.norms = o, o += al(4 * (M + ld) * 4);
     L.ids = o, o += al(M * k * 4);
     L.coef = o, o += al(M * k * 4);
-    L.route_bytes = kernels::moe_route_workspace_bytes(M, k, E);
+    L.route_bytes = kernels::moe_route_workspace_bytes(M, k, Es);
     L.route = o, o += al((int64_t)L.route_bytes);
     L.x16 = o, o += al(M * k >= 1024 ? M * H * 2 : 0);  // prefill sizes: x as F16 for the Q4 experts' F16 math
     L.h = o, o += al(M * k * I * 2);
@@ -1430,9 +1431,13 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     STRIX_CHECK(logits_in != nullptr || w.router != nullptr, fn, ": no router weight and no logits");
     STRIX_CHECK(w.gate_up_bits == 4 || w.gate_up_bits == 8, fn, ": routed expert bits ", w.gate_up_bits);
     STRIX_CHECK(w.down_bits == w.gate_up_bits, fn, ": gate_up and down must share a format");
-    STRIX_CHECK(w.gate_up.N == w.E * 2 * w.I && w.gate_up.K == w.H && w.down.N == w.E * w.H && w.down.K == w.I, fn,
+    STRIX_CHECK(!(w.has_shared && w.shared_stacked), fn, ": the shared expert is either separate or stacked, not both");
+    // the stacked shared expert is expert E of the routed views, routed as slot k of every token
+    const int64_t Es = w.E + (w.shared_stacked ? 1 : 0);
+    STRIX_CHECK(w.gate_up.N == Es * 2 * w.I && w.gate_up.K == w.H && w.down.N == Es * w.H && w.down.K == w.I, fn,
                 ": weight shapes [", w.gate_up.N, ", ", w.gate_up.K, "] / [", w.down.N, ", ", w.down.K,
-                "] do not match E = ", w.E, ", H = ", w.H, ", I = ", w.I);
+                "] do not match ", Es, " experts (E = ", w.E, w.shared_stacked ? " + the stacked shared expert" : "",
+                "), H = ", w.H, ", I = ", w.I);
     if (w.has_shared)
         STRIX_CHECK(w.sh_gate_up.N == 2 * w.I && w.sh_gate_up.K == w.H && w.sh_down.N == w.H && w.sh_down.K == w.I, fn,
                     ": shared expert shapes do not match H = ", w.H, ", I = ", w.I);
@@ -1461,7 +1466,9 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
                     fn, ": the residual streams overlap y, x or the workspace");
     }
     char *base = static_cast<char *>(ws);
-    const int64_t E = w.E, k = w.k, H = w.H, I = w.I, ld = E + (w.has_shared ? 1 : 0);
+    const bool stacked = w.shared_stacked;
+    const int64_t E = w.E, k = w.k, H = w.H, I = w.I, ld = E + (w.has_shared || stacked ? 1 : 0);
+    const int64_t A = k + (stacked ? 1 : 0);  // slots a token: the top-k (+ the stacked shared expert)
     float *logits = reinterpret_cast<float *>(base + L.logits);
     int32_t *ids = ids_out ? ids_out : reinterpret_cast<int32_t *>(base + L.ids);
     float *coef = coef_out ? coef_out : reinterpret_cast<float *>(base + L.coef);
@@ -1475,7 +1482,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     // shared expert (dense Q8): at decode sizes folded into the routed gate_up and down launches (no second stream,
     // whose join would cost more than the shared expert's few MB); otherwise on the helper stream: gate_up + SwiGLU ->
     // sh_h, down -> sh_s
-    const bool fold = w.has_shared && M <= 16 && M * k <= 1024;
+    const bool fold = w.has_shared && M <= 16 && M * A <= 1024;
     SharedJob sh_jobs[2]{};  // ride along in the routed gate_up and down launches
     GemmArgs sh_gu{};        // its gate_up parts ride along in the top-k launch
     int sh_gu_spp = 0, sh_gu_parts = 0;
@@ -1543,9 +1550,9 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     if (!lg) {
         lg = logits;
         // prefill sizes: bf16 MFMA projection + exact recomputation of the candidates (the same routing bits)
-        routed = M >= 256 && moe_router_prefill(x, w.router, w.router_bias, M, H, E, k, w.has_shared, logits,
+        routed = M >= 256 && moe_router_prefill(x, w.router, w.router_bias, M, H, E, k, w.has_shared || stacked, logits,
                                                 reinterpret_cast<float *>(base + L.norms), ids, coef, err_router,
-                                                stream);
+                                                stream, stacked);
         if (!routed) {
             linear_bf16w(x, w.router, logits, M, ld, H, Act::BF16, Act::F32, stream);
             if (w.router_bias) {
@@ -1557,16 +1564,17 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         }
     }
     if (routed) {
-        moe_group_routes(ids, M, k, E, route, L.route_bytes, err_expert, stream);
-    } else if (M * k <= 1024) {  // one launch: top-k and packing with the ids kept in LDS
+        moe_group_routes(ids, M, A, Es, route, L.route_bytes, err_expert, stream);
+    } else if (M * A <= 1024) {  // one launch: top-k and packing with the ids kept in LDS
         if (fold)
             launch_topk_route_shared(lg, ld, M, E, k, ids, coef, route, L.route_bytes, err_router, err_expert, sh_gu,
                                      sh_gu_spp, sh_gu_parts, sh_part, stream);
         else
-            moe_topk_group_routes_small(lg, ld, M, E, k, ids, coef, route, L.route_bytes, err_router, err_expert, stream);
+            moe_topk_group_routes_small(lg, ld, M, E, k, ids, coef, route, L.route_bytes, err_router, err_expert, stream,
+                                        stacked);
     } else {
-        moe_router(lg, ld, M, E, k, nullptr, 0, 0, ids, coef, Act::F32, err_router, stream);
-        moe_group_routes(ids, M, k, E, route, L.route_bytes, err_expert, stream);
+        moe_router(lg, ld, M, E, k, stacked ? lg + E : nullptr, ld, (int32_t)E, ids, coef, Act::F32, err_router, stream);
+        moe_group_routes(ids, M, A, Es, route, L.route_bytes, err_expert, stream);
     }
     // routed experts: gate_up + SwiGLU -> h, down -> partial
     const bool q8 = w.gate_up_bits == 8;
@@ -1575,54 +1583,54 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     // Q4 experts at prefill sizes run the reference's F16 math (MoeMath::WmmaF16): x converted to F16 once, h kept
     // in F16 (the F16 form of its BF16 rounding), both in the GEMM's paired k order, and the down's partials stored in
     // BF16 (strixite kernels/moe_grouped.hpp:84)
-    GemmArgs gu2 = make_args(qv(w.gate_up), E, base + L.x16, h, I);
-    gu2.A = k, gu2.ws = static_cast<const int32_t *>(route), gu2.S = M * k;
-    GemmArgs dn2 = make_args(qv(w.down), E, h, partial, H);
-    dn2.A = k, dn2.ws = static_cast<const int32_t *>(route), dn2.S = M * k;
-    const bool f16p = !q8 && !fold && use_expert_gemm(M * k, E, H, w.gate_up.G) &&
-                      use_expert_gemm(M * k, E, I, w.down.G) && expert_gemm2_fits<EPI_SWIGLU>(gu2) &&
+    GemmArgs gu2 = make_args(qv(w.gate_up), Es, base + L.x16, h, I);
+    gu2.A = A, gu2.ws = static_cast<const int32_t *>(route), gu2.S = M * A;
+    GemmArgs dn2 = make_args(qv(w.down), Es, h, partial, H);
+    dn2.A = A, dn2.ws = static_cast<const int32_t *>(route), dn2.S = M * A;
+    const bool f16p = !q8 && !fold && use_expert_gemm(M * A, Es, H, w.gate_up.G) &&
+                      use_expert_gemm(M * A, Es, I, w.down.G) && expert_gemm2_fits<EPI_SWIGLU>(gu2) &&
                       expert_gemm2_fits<EPI_BF16>(dn2) && H % 8 == 0 && I % 8 == 0;
     // otherwise h in bf16: the oracle's rounding of silu(g) * u, with bf16's range
     if (f16p) {
-        check_grouped(fn, x, qv(w.gate_up), E, route, L.route_bytes, M, k, h, Act::BF16, M * k * I * 2, M);
+        check_grouped(fn, x, qv(w.gate_up), Es, route, L.route_bytes, M, A, h, Act::BF16, M * A * I * 2, M);
         bf16_to_f16_paired(x, base + L.x16, M, H, stream);
         STRIX_CHECK((launch_expert_gemm2<EPI_SWIGLU, true, g2::H_F16P, true>(gu2, stream)), fn, ": F16 gate_up");
     } else if (fold) {
         const QV gv = q8 ? qv(gu8) : qv(w.gate_up);
-        check_grouped(fn, x, gv, E, route, L.route_bytes, M, k, h, Act::BF16, M * k * I * 2, M);
-        GemmArgs a = make_args(gv, E, x, h, I);
-        a.A = k, a.ws = static_cast<const int32_t *>(route), a.S = M * k;
+        check_grouped(fn, x, gv, Es, route, L.route_bytes, M, A, h, Act::BF16, M * A * I * 2, M);
+        GemmArgs a = make_args(gv, Es, x, h, I);
+        a.A = A, a.ws = static_cast<const int32_t *>(route), a.S = M * A;
         if (!q8 && decode_fits(a, M, true)) launch_decode_gate_up(a, M, &sh_jobs[0], stream);
-        else if (q8) launch_gemm<8, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, k, E), stream, &sh_jobs[0]);
-        else launch_gemm<4, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, k, E), stream, &sh_jobs[0]);
+        else if (q8) launch_gemm<8, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, A, Es), stream, &sh_jobs[0]);
+        else launch_gemm<4, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, A, Es), stream, &sh_jobs[0]);
     } else if (q8) {
-        linear_q8_experts_gather_grouped_swiglu(x, gu8, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
+        linear_q8_experts_gather_grouped_swiglu(x, gu8, Es, route, L.route_bytes, M, A, h, Act::BF16, MoeMath::WmmaF16, stream, false);
     } else {
-        linear_q4_experts_gather_grouped_swiglu(x, w.gate_up, E, route, L.route_bytes, M, k, h, Act::BF16, MoeMath::WmmaF16, stream, false);
+        linear_q4_experts_gather_grouped_swiglu(x, w.gate_up, Es, route, L.route_bytes, M, A, h, Act::BF16, MoeMath::WmmaF16, stream, false);
     }
     {
         const QV dv = q8 ? qv(dn8) : qv(w.down);
-        check_view(fn, dv, E);
-        GemmArgs a = make_args(dv, E, h, partial, H);
-        a.A = k, a.ws = static_cast<const int32_t *>(route), a.S = M * k;
+        check_view(fn, dv, Es);
+        GemmArgs a = make_args(dv, Es, h, partial, H);
+        a.A = A, a.ws = static_cast<const int32_t *>(route), a.S = M * A;
         if (f16p) {
             STRIX_CHECK((launch_expert_gemm2<EPI_BF16, false, g2::H_BF16, true>(dn2, stream)), fn, ": F16 down");
-        } else if (use_expert_gemm(M * k, E, dv.K, dv.G)) {
+        } else if (use_expert_gemm(M * A, Es, dv.K, dv.G)) {
             if (q8) launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
             else launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
         } else if (!q8 && M <= dec::kMaxTokens && decode_fits(a, M, false)) {
             launch_decode_down(a, M, fold ? &sh_jobs[1] : nullptr, stream);
         } else if (q8) {
-            launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream, fold ? &sh_jobs[1] : nullptr);
+            launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, A, Es), stream, fold ? &sh_jobs[1] : nullptr);
         } else {
-            launch_gemm<4, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, k, E), stream, fold ? &sh_jobs[1] : nullptr);
+            launch_gemm<4, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, A, Es), stream, fold ? &sh_jobs[1] : nullptr);
         }
     }
     if (ctx != nullptr && w.has_shared && !fold) STRIX_HIP_CHECK(hipStreamWaitEvent(stream, ctx->join, 0), fn, ": join wait");
     const MoeSharedAdd sh{sh_s, lg + E, ld, (uint32_t)E, err_router};
     const InjectArgs inj = inject ? InjectArgs{static_cast<uint16_t *>(inject->xs), inject->w_in, inject->streams}
                                   : InjectArgs{};
-    combine_reduce(partial, ids, coef, M, k, E, H, static_cast<uint16_t *>(y), w.has_shared ? &sh : nullptr,
+    combine_reduce(partial, ids, coef, M, A, Es, H, static_cast<uint16_t *>(y), w.has_shared ? &sh : nullptr,
                    static_cast<const uint16_t *>(x), static_cast<uint16_t *>(x_out), stream, fold ? sh_part : nullptr,
                    fold ? sh_jobs[1].parts : 0, f16p, inject ? &inj : nullptr);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " E=", E, " k=", k);

@@ -108,9 +108,11 @@ __global__ void __launch_bounds__(256) route_tiles_kernel(Layout L, int32_t *ws)
 template <int NV>
 __global__ void __launch_bounds__(1024)
     topk_route_small_kernel(const float *logits, int64_t ld, int M, int E, int k, int32_t *ids_out, float *coef_out,
-                            Layout L, int nbits, int32_t *ws, uint32_t *err_router, uint32_t *err_route) {
+                            Layout L, int nbits, int32_t *ws, uint32_t *err_router, uint32_t *err_route,
+                            bool shared_slot) {
     extern __shared__ int lds[];
-    topk_route_small_body<NV>(logits, ld, M, E, k, ids_out, coef_out, L, nbits, ws, err_router, err_route, lds);
+    topk_route_small_body<NV>(logits, ld, M, E, k, ids_out, coef_out, L, nbits, ws, err_router, err_route, lds,
+                              shared_slot);
 }
 
 
@@ -155,20 +157,23 @@ void moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void 
 
 void moe_topk_group_routes_small(const float *logits, int64_t ld, int64_t M, int64_t E, int64_t k, int32_t *ids,
                                  float *coef, void *ws, size_t ws_bytes, uint32_t *err_router, uint32_t *err_route,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, bool shared_slot) {
     const char *fn = "moe_topk_group_routes_small";
-    STRIX_CHECK(M >= 1 && k >= 1 && k <= 64 && k <= E && E <= kMoeMaxExperts && M * k <= kFusedSlots, fn,
-                ": M = ", M, ", E = ", E, ", k = ", k, " (M k <= ", kFusedSlots, ")");
-    STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, k, E) && reinterpret_cast<uintptr_t>(ws) % 16 == 0, fn,
-                ": workspace of ", ws_bytes, " bytes, needs ", moe_route_workspace_bytes(M, k, E), ", 16-byte aligned");
-    const route::Layout L = route::layout(M, k, E);
+    const int64_t A = k + (shared_slot ? 1 : 0), Es = E + (shared_slot ? 1 : 0);  // slots; experts packed
+    STRIX_CHECK(M >= 1 && k >= 1 && A <= 64 && k <= E && Es <= kMoeMaxExperts && M * A <= kFusedSlots, fn,
+                ": M = ", M, ", E = ", E, ", k = ", k, shared_slot ? " + the shared slot" : "", " (M A <= ",
+                kFusedSlots, ")");
+    STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, A, Es) && reinterpret_cast<uintptr_t>(ws) % 16 == 0, fn,
+                ": workspace of ", ws_bytes, " bytes, needs ", moe_route_workspace_bytes(M, A, Es), ", 16-byte aligned");
+    const route::Layout L = route::layout(M, A, Es);
     int nbits = 0;
-    while ((1ll << nbits) <= E) ++nbits;
+    while ((1ll << nbits) <= Es) ++nbits;
     const size_t lds = route::topk_route_small_lds(L);
     const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
     auto go = [&](auto nvc) {
         topk_route_small_kernel<decltype(nvc)::value><<<1, 1024, lds, stream>>>(
-            logits, ld, (int)M, (int)E, (int)k, ids, coef, L, nbits, static_cast<int32_t *>(ws), err_router, err_route);
+            logits, ld, (int)M, (int)Es, (int)k, ids, coef, L, nbits, static_cast<int32_t *>(ws), err_router, err_route,
+            shared_slot);
     };
     switch (nv) {
         case 1: go(std::integral_constant<int, 1>{}); break;

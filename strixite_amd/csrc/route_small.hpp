@@ -167,11 +167,15 @@ __device__ inline void report_bad(const int32_t *ids, int first_bad, uint32_t *e
 // E: the stores. The workspace layout and contents are those of moe_group_routes.
 constexpr int kFusedSlots = 1024;
 
+// TOPK with shared_slot: each token's slot k is the shared expert (id E_top, coefficient sigmoid(its gate logit at
+// column E_top of the logits); a non-finite one is bad index E_top, strixite kernels/moe_router.hip:108-111), and the
+// packing runs over L.E = E_top + 1 experts. E: the packing's expert count (L.E).
 template <int NV, bool TOPK>
 __device__ inline void pack_small_body(const float *logits, int64_t ld, const int32_t *ids_in, int M, int E, int k,
                                        int32_t *ids_out, float *coef_out, Layout L, int nbits, int32_t *ws,
-                                       uint32_t *err_router, uint32_t *err_route, int *lds) {
+                                       uint32_t *err_router, uint32_t *err_route, int *lds, bool shared_slot = false) {
     const int S = (int)L.S, nb = E + 1, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave, t = threadIdx.x;
+    const int Etop = shared_slot ? E - 1 : E, A = k + (shared_slot ? 1 : 0);
     const int nthr = (int)blockDim.x;
     int *sids = lds;                          // [S] ids by slot
     float *scoef = reinterpret_cast<float *>(sids + kFusedSlots);  // [S] coefficients by slot (TOPK)
@@ -193,7 +197,12 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
         for (int m = wave; m < M; m += kSmallWaves) {
             int id;
             float cf;
-            const int rb = topk::wave_topk<float, NV>(logits + (int64_t)m * ld, E, k, id, cf);
+            int rb = topk::wave_topk<float, NV>(logits + (int64_t)m * ld, Etop, k, id, cf);
+            float sl = 0.f;
+            if (shared_slot) {
+                sl = logits[(int64_t)m * ld + Etop];
+                if (!isfinite(sl) && Etop < rb) rb = Etop;
+            }
             if (rb != INT_MAX) {
                 if (lane == 0 && atomicCAS(&err_router[0], 0u, 1u) == 0u) {
                     err_router[1] = (uint32_t)m;
@@ -201,7 +210,10 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
                 }
                 id = -1, cf = dev::qnan();
             }
-            if (lane < k) sids[m * k + lane] = id, scoef[m * k + lane] = cf;
+            if (lane < k) sids[m * A + lane] = id, scoef[m * A + lane] = cf;
+            if (shared_slot && lane == k)
+                sids[m * A + k] = rb != INT_MAX ? -1 : Etop,
+                scoef[m * A + k] = rb != INT_MAX ? dev::qnan() : 1.0f / (1.0f + expf(-sl));
         }
     } else {
         for (int i = t; i < S; i += nthr) sids[i] = ids_in[i];
@@ -262,9 +274,9 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
 template <int NV>
 __device__ inline void topk_route_small_body(const float *logits, int64_t ld, int M, int E, int k, int32_t *ids_out,
                                              float *coef_out, Layout L, int nbits, int32_t *ws, uint32_t *err_router,
-                                             uint32_t *err_route, int *lds) {
+                                             uint32_t *err_route, int *lds, bool shared_slot = false) {
     pack_small_body<NV, true>(logits, ld, nullptr, M, E, k, ids_out, coef_out, L, nbits, ws, err_router, err_route,
-                              lds);
+                              lds, shared_slot);
 }
 
 // LDS bytes pack_small_body needs

@@ -199,8 +199,8 @@ __device__ __forceinline__ void rounds(uint32_t (&key)[NV], int k, int &id, uint
 template <int NV, int NCH>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     router_select_kernel(const uint16_t *x, const uint16_t *w, const float *bias, float *logits, int64_t ld,
-                         int64_t M, int E, int k, bool shared, const float *nx2, const float *nw2, int32_t *ids,
-                         float *coef, uint32_t *err) {
+                         int64_t M, int E, int k, bool shared, bool shared_slot, const float *nx2, const float *nw2,
+                         int32_t *ids, float *coef, uint32_t *err) {
     __shared__ int cand_lds[kThreads / kWave][1040];  // a wave's candidate list (at most E + 1 <= 1025)
     const int lane = threadIdx.x % kWave;
     const int64_t m = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
@@ -273,6 +273,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
             c[i] = *reinterpret_cast<const uint4 *>(w + (int64_t)e * K + (lane + i * kWave) * 8);
     };
     uint4 cur[NCH], nxt[NCH];
+    float sd = 0.f;  // the shared gate logit (wave-uniform)
     int ec = __builtin_amdgcn_readfirstlane(cl[0]);
     load(ec, cur);
     for (int s2 = 0; s2 < nc; ++s2) {
@@ -282,6 +283,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
         for (int off = kWave / 2; off > 0; off >>= 1) d = d + __shfl_xor(d, off, kWave);
         if (ec == E) {
+            sd = d;
             if (lane == 0) row[E] = d;  // the shared gate logit, unbiased
         } else {
             const float vb = bias ? d + bias[ec] : d;  // one FP32 add, as the unfused path
@@ -305,14 +307,18 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
         for (int off = kWave / 2; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off, kWave));
     }
-    int32_t *id_row = ids + m * k;
-    float *coef_row = coef + m * k;
+    // shared_slot: the shared expert routed as slot k, id E, coefficient sigmoid(its gate logit) (strixite
+    // kernels/moe_router.hip:108-111); a non-finite gate logit is bad index E
+    const int A = k + (shared_slot ? 1 : 0);
+    if (shared_slot && !isfinite(sd)) bad = min(bad, E);
+    int32_t *id_row = ids + m * A;
+    float *coef_row = coef + m * A;
     if (bad != INT_MAX) {  // strixite kernels/moe_router.hip:40-67: the token's ids -1, coefficients NaN, err
         if (lane == 0 && atomicCAS(&err[0], 0u, 1u) == 0u) {
             err[1] = (uint32_t)m;
             err[2] = (uint32_t)bad;
         }
-        if (lane < k) id_row[lane] = -1, coef_row[lane] = qnan();
+        if (lane < A) id_row[lane] = -1, coef_row[lane] = qnan();
         return;
     }
 #pragma unroll
@@ -325,13 +331,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, kWave);
     if (lane < k) id_row[lane] = id, coef_row[lane] = e0 / sum;
+    if (shared_slot && lane == 0) id_row[k] = E, coef_row[k] = 1.0f / (1.0f + expf(-sd));
 }
 
 }  // namespace
 
 bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
                         int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
-                        hipStream_t stream) {
+                        hipStream_t stream, bool shared_slot) {
     const int64_t nch = H / 512, ld = E + (shared ? 1 : 0);
     if (H % 512 != 0 || nch < 1 || nch > 8 || E > 1024 || k > 32 || k > E || (H / kParts) % kBK != 0 ||
         reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
@@ -345,7 +352,8 @@ bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int
     const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
     auto go = [&](auto nvc, auto nchc) {
         router_select_kernel<decltype(nvc)::value, decltype(nchc)::value><<<g2, kThreads, 0, stream>>>(
-            static_cast<const uint16_t *>(x), w, bias, logits, ld, M, (int)E, (int)k, shared, nx, nw, ids, coef, err);
+            static_cast<const uint16_t *>(x), w, bias, logits, ld, M, (int)E, (int)k, shared, shared && shared_slot, nx, nw,
+            ids, coef, err);
     };
     auto by_nch = [&](auto nvc) {
         switch (nch) {

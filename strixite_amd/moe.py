@@ -317,8 +317,13 @@ class MoeLayer:
     """One MoE FFN sublayer's weights on the device and its forward (strixite runtime/qwen4exp.cpp:3143-3217)."""
 
     def __init__(self, H, E, k, I, router, gate_up: QWeight, down: QWeight, router_bias=None,
-                 shared_gate_up: QWeight | None = None, shared_down: QWeight | None = None):
+                 shared_gate_up: QWeight | None = None, shared_down: QWeight | None = None,
+                 shared_stacked: bool = False):
+        """shared_stacked: the shared expert is expert E of gate_up / down (E + 1 experts there, router row E its
+        gate), routed as slot k of every token; ids / coef are then [M, k + 1]."""
         self.H, self.E, self.k, self.I = H, E, k, I
+        self.shared_stacked = shared_stacked
+        self.A = k + (1 if shared_stacked else 0)
         self.router, self.router_bias = router, router_bias
         self.gate_up, self.down = gate_up, down
         self.shared_gate_up, self.shared_down = shared_gate_up, shared_down
@@ -332,6 +337,7 @@ class MoeLayer:
         w.has_shared = 1 if shared_gate_up is not None else 0
         if shared_gate_up is not None:
             w.sh_gate_up, w.sh_down = shared_gate_up.view(), shared_down.view()
+        w.shared_stacked = 1 if shared_stacked else 0
 
     @property
     def has_shared(self) -> bool:
@@ -347,11 +353,16 @@ class MoeLayer:
     @staticmethod
     def synth(H, E, k, I, seed=0, layer=0, routed_bits=4, routed_G=None, shared=True, shared_G=64,
               router_bias=None, device="cuda") -> "MoeLayer":
-        """Seeded synthetic layer (router N(0, 0.02), Q4 / Q8 experts as the bench configs describe)."""
+        """Seeded synthetic layer (router N(0, 0.02), Q4 / Q8 experts as the bench configs describe). shared: True (a
+        separate Q8 shared expert), False, or "stacked" (the shared expert as expert E of the routed stacks)."""
         G = routed_G or (128 if routed_bits == 4 else 64)
+        stacked = shared == "stacked"
+        Es = E + (1 if stacked else 0)
         router = synth_bf16_normal(seed, "router", layer, (E + (1 if shared else 0), H), 0.02, device)
-        gu = QWeight.synth(routed_bits, seed, "gu_q", "gu_s", layer, E * 2 * I, H, G, device)
-        dn = QWeight.synth(routed_bits, seed, "dn_q", "dn_s", layer, E * H, I, G, device)
+        gu = QWeight.synth(routed_bits, seed, "gu_q", "gu_s", layer, Es * 2 * I, H, G, device)
+        dn = QWeight.synth(routed_bits, seed, "dn_q", "dn_s", layer, Es * H, I, G, device)
+        if stacked:
+            return MoeLayer(H, E, k, I, router, gu, dn, router_bias, shared_stacked=True)
         sgu = sdn = None
         if shared:
             sgu = QWeight.synth(8, seed, "sh_gu_q", "sh_gu_s", layer, 2 * I, H, shared_G, device)
@@ -384,8 +395,8 @@ class MoeLayer:
             out = {
                 "y": torch.empty((M, self.H), dtype=torch.bfloat16, device=x.device),
                 "x_out": torch.empty((M, self.H), dtype=torch.bfloat16, device=x.device),
-                "ids": torch.empty((M, self.k), dtype=torch.int32, device=x.device),
-                "coef": torch.empty((M, self.k), dtype=torch.float32, device=x.device),
+                "ids": torch.empty((M, self.A), dtype=torch.int32, device=x.device),
+                "coef": torch.empty((M, self.A), dtype=torch.float32, device=x.device),
                 "err": torch.zeros(6, dtype=torch.int32, device=x.device),
             }
         L.check(L.lib().strix_moe_layer_forward(C.byref(self._w), _p(x), M, _p(logits_in), _p(out["y"]),

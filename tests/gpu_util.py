@@ -27,6 +27,8 @@ def oracle_weights(layer: moe.MoeLayer) -> dict:
         w["router_bias"] = to_np(layer.router_bias)
     if layer.has_shared:
         w["sh_gu"], w["sh_dn"] = qspec(layer.shared_gate_up), qspec(layer.shared_down)
+    if layer.shared_stacked:
+        w["shared_stacked"] = True
     return w
 
 

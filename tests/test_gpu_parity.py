@@ -628,3 +628,52 @@ def test_layer_hyperconnection_inject(M):
     want = orc.f32_to_bf16(cf.reshape(M, 4 * 1024))
     got = to_np(xs)
     assert np.mean(got == want) > 0.9999 and np.abs(got.astype(np.int32) - want.astype(np.int32)).max() <= 1
+
+
+@pytest.mark.parametrize("M", [16, 120, 512])
+def test_layer_stacked_shared_expert(M):
+    """The converter's default layout (strixite formats/merge_plan.cpp:31-41): the shared expert is expert E of the
+    stacked routed tensors, routed as slot k of every token with coefficient sigmoid(router row E) (strixite
+    kernels/moe_router.hip:108-111). Decode-size (one-launch top-k + packing), mid-size (moe_router) and prefill-size
+    (the MFMA router) batches: ids and coefficients against the oracle, every token; output on seeded tokens."""
+    say("stacked shared", M)
+    H, E, k, I = 1024, 64, 8, 256
+    layer = moe.MoeLayer.synth(H, E, k, I, seed=9, shared="stacked")
+    x = moe.synth_bf16_normal(9, "x", M, (M, H), 1.0)
+    out = layer.forward(x)
+    torch.cuda.synchronize()
+    w = oracle_weights(layer)
+    xn = to_np(x)
+    rows = np.arange(M) if M <= 16 else np.sort(np.random.default_rng(M).choice(M, 24, replace=False))
+    o = orc.moe_layer(w, np.ascontiguousarray(xn[rows]))
+    ids = to_np(out["ids"])
+    assert ids.shape == (M, k + 1) and np.all(ids[:, k] == E)
+    lg = orc.router_logits(xn, w["router"])
+    rids, rcoef, _ = orc.topk(lg, E, k, shared=np.ascontiguousarray(lg[:, E:]), shared_ld=1, shared_id=E)
+    assert np.array_equal(ids, rids)
+    assert np.allclose(to_np(out["coef"]), rcoef, rtol=2e-6, atol=1e-7)
+    assert np.array_equal(ids[rows], o["ids"])
+    assert rel_err(to_np(out["y"])[rows], o["y"]) < 1e-2
+    assert rel_err(to_np(out["x_out"])[rows], o["out"]) < 1e-2
+    assert to_np(out["err"])[0] == 0 and to_np(out["err"])[3] == 0
+
+
+def test_layer_stacked_shared_nonfinite_gate():
+    """A non-finite shared-expert gate logit marks the token as the reference's router does: every slot -1, its
+    coefficients NaN, the router error naming expert E; the other tokens route normally."""
+    say("stacked shared nonfinite")
+    H, E, k, I, M = 1024, 64, 8, 256, 6
+    layer = moe.MoeLayer.synth(H, E, k, I, seed=10, shared="stacked")
+    lg = np.random.default_rng(2).standard_normal((M, E + 1)).astype(np.float32)
+    lg[3, E] = np.inf
+    x = moe.synth_bf16_normal(10, "x", 0, (M, H), 1.0)
+    out = layer.forward(x, logits_in=torch.from_numpy(lg).to(DEV))
+    torch.cuda.synchronize()
+    ids = to_np(out["ids"])
+    assert np.all(ids[3] == -1) and np.all(np.isnan(to_np(out["coef"])[3]))
+    e = to_np(out["err"]).view(np.uint32)
+    assert e[0] == 1 and e[1] == 3 and e[2] == E
+    rids, _, _ = orc.topk(lg, E, k, shared=np.ascontiguousarray(lg[:, E:]), shared_ld=1, shared_id=E)
+    assert np.array_equal(ids, rids)
+    ok = np.arange(M) != 3
+    assert not np.isnan(orc.bf16_to_f32(to_np(out["y"])[ok])).any()

@@ -239,6 +239,41 @@ def test_layer_closed_form(orc):
     assert np.abs(out - (xf + got)).max() <= np.abs(xf + got).max() * 2 ** -8
 
 
+def test_layer_stacked_shared_closed_form(orc):
+    """Shared expert stacked as expert E of the routed tensors and routed as slot k: the same float64 sum, with the
+    shared term taken from rows E of gate_up / down and the id / coefficient of slot k checked as E / sigmoid(g)."""
+    E, k, I, H, M, seed = 4, 2, 128, 256, 5, 4
+    key = lambda t: orc.tensor_key(seed, t)  # noqa: E731
+    w = {"E": E, "k": k, "I": I, "shared_stacked": True}
+    w["router"] = orc.gen_bf16_normal(key("router"), 0.02, (E + 1, H))
+    w["gu"] = (4, *orc.gen_q(4, key("gu_q"), key("gu_s"), (E + 1) * 2 * I, H, 128), 128)
+    w["dn"] = (4, *orc.gen_q(4, key("dn_q"), key("dn_s"), (E + 1) * H, I, 128), 128)
+    x = orc.gen_bf16_normal(key("x"), 1.0, (M, H))
+    o = orc.moe_layer(w, x)
+    assert o["ids"].shape == (M, k + 1) and np.all(o["ids"][:, k] == E)
+    xf = orc.bf16_to_f32(x).astype(np.float64)
+    gu, dn = _deq(orc, w["gu"], (E + 1) * 2 * I, H), _deq(orc, w["dn"], (E + 1) * H, I)
+    lg = xf @ orc.bf16_to_f32(w["router"]).astype(np.float64).T
+    assert np.allclose(o["coef"][:, k], 1 / (1 + np.exp(-lg[:, E])), rtol=1e-5)
+    y = np.zeros((M, H))
+    for m in range(M):
+        assert list(o["ids"][m, :k]) == _topk_brute(o["logits"][m, :E], k)
+        for a in range(k + 1):
+            e = o["ids"][m, a]
+            g = gu[e * 2 * I:e * 2 * I + I] @ xf[m]
+            u = gu[e * 2 * I + I:(e + 1) * 2 * I] @ xf[m]
+            y[m] += o["coef"][m, a] * (dn[e * H:(e + 1) * H] @ (_silu(g) * u))
+    got = orc.bf16_to_f32(o["y"]).astype(np.float64)
+    assert np.abs(got - y).max() / np.abs(y).max() < 1e-2
+    # dropping the shared term must be visible at this tolerance
+    ysh = np.zeros((M, H))
+    for m in range(M):
+        g = gu[E * 2 * I:E * 2 * I + I] @ xf[m]
+        u = gu[E * 2 * I + I:(E + 1) * 2 * I] @ xf[m]
+        ysh[m] = o["coef"][m, k] * (dn[E * H:(E + 1) * H] @ (_silu(g) * u))
+    assert np.abs(ysh).max() / np.abs(y).max() > 5e-2
+
+
 def test_experts_down_and_dense(orc):
     w, x = _tiny_layer(orc, shared=True, M=3)
     E, I = w["E"], w["I"]
