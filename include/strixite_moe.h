@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define STRIX_MOE_ABI_VERSION 3
+#define STRIX_MOE_ABI_VERSION 4
 #define STRIX_E_PRECONDITION 1
 #define STRIX_E_GPU 2
 #define STRIX_E_OTHER 3
@@ -155,6 +155,59 @@ int64_t strix_moe_layer_noalloc_max_bytes(void);
 int strix_moe_layer_forward_noalloc(const strix_moe_layer_weights *w, const void *x, int64_t M,
                                     const float *logits_in, void *y, void *x_out, int32_t *ids, float *coef,
                                     uint32_t *err, void *stream);
+
+/* strixw, the converted-weights file (strixite formats/strixw.hpp) and its load into HBM (strixite
+ * runtime/strixw_loader.hpp:36-88, Device placement). Handles are opaque; names are NUL-terminated. The file, its
+ * tensors and metadata stay valid until strix_strixw_close. role: 0 data, 1 q, 2 scale, 3 min (StrixwRole);
+ * encoding: StrixwEncoding's values (1 q4 ... 9 q5). */
+/* strixite formats/strixw.hpp:58 strix_hash64 */
+uint64_t strix_strixw_hash64(const void *p, size_t n);
+typedef struct {
+    const char *name;
+    int encoding, ndim;
+    int64_t shape[8];
+    int64_t group_size, experts, nparts;
+    int ncomponents;
+    int role[4];
+    uint64_t offset[4], bytes[4], hash[4];
+} strix_strixw_tensor_info;
+/* strixite formats/strixw.hpp:111-130 StrixwFile */
+int strix_strixw_open(const char *path, void **file);
+int strix_strixw_close(void *file);
+int strix_strixw_info(void *file, uint64_t *file_bytes, uint64_t *data_offset, uint32_t *version, int64_t *ntensors,
+                      int64_t *nmeta);
+int strix_strixw_tensor(void *file, int64_t i, strix_strixw_tensor_info *out);
+int strix_strixw_find(void *file, const char *name, int64_t *index); /* index -1 when absent */
+int strix_strixw_part(void *file, int64_t tensor, int64_t part, const char **source, int64_t *row_offset,
+                      int64_t *rows);
+int strix_strixw_meta(void *file, int64_t i, const char **key, const char **value);
+int strix_strixw_verify(void *file, int threads);
+/* strixite formats/strixw.hpp:82-109 StrixwWriter: plan (name, encoding, shape, group size, experts, and the
+ * checkpoint tensors its rows came from: nparts sources of part_rows[i] rows each, consecutive), write each
+ * component once, finish. */
+typedef struct {
+    const char *name;
+    int encoding, ndim;
+    int64_t shape[8];
+    int64_t group_size, experts;
+    int64_t nparts;
+    const char *const *part_sources;
+    const int64_t *part_rows;
+} strix_strixw_plan_t;
+int strix_strixw_writer_create(const char *path, int64_t nmeta, const char *const *keys, const char *const *values,
+                               int64_t ntensors, const strix_strixw_plan_t *plan, void **writer);
+int strix_strixw_writer_write(void *writer, int64_t tensor, int role, const void *data, size_t bytes);
+int strix_strixw_writer_finish(void *writer);
+int strix_strixw_writer_destroy(void *writer);
+/* strixite runtime/strixw_loader.hpp:42-60 StrixwDevice (the data region in one HBM allocation on the current
+ * device); ptr: the device address of a tensor's component. */
+int strix_strixw_device_load(const char *path, int read_threads, void **dev);
+int strix_strixw_device_free(void *dev);
+int strix_strixw_device_info(void *dev, uint64_t *device_bytes, double *load_seconds);
+int strix_strixw_device_ptr(void *dev, const char *name, int role, const void **ptr);
+/* the MoE sublayer's weights of one decoder layer (strixite runtime/qwen4exp.cpp:147-156): prefix
+ * "model.language_model.layers.N."; the views point into dev's allocation. */
+int strix_strixw_moe_layer(void *dev, const char *prefix, int64_t top_k, strix_moe_layer_weights *out);
 
 /* Calibration kernels for the bench (no reference counterpart): dense f16 MFMA chains on `blocks` blocks of 4 waves
  * for `iters` iterations (returns the flops launched, -1 on error), and a plain streaming read of `bytes` bytes.

@@ -45,6 +45,8 @@ def lib() -> C.CDLL:
             build()
         L = C.CDLL(_LIB)
         L.orc_f32_to_bf16.restype = C.c_uint16
+        L.orc_strixw_hash64.restype = _u64
+        L.orc_strixw_hash64.argtypes = [_p, _u64]
         L.orc_f32_to_bf16.argtypes = [_f32]
         L.orc_bf16_to_f32.restype = _f32
         L.orc_bf16_to_f32.argtypes = [C.c_uint16]

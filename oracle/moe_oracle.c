@@ -543,3 +543,37 @@ int orc_moe_layer(const orc_layer *L, orc_layer_out *o, int threads) {
                 L->has_shared ? o->logits + E : NULL, ld, o->y, L->x, o->out);
     return 0;
 }
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* strixw hash (strixite formats/strixw.cpp:24-38 mix, :204-246 StrixHasher / strix_hash64), restated one shot */
+static uint64_t orc_hmix(uint64_t h, uint64_t w) {
+    h ^= w * 0x9e3779b97f4a7c15ull;
+    return (h ^ (h >> 31)) * 0xd6e8feb86659fd93ull;
+}
+
+uint64_t orc_strixw_hash64(const void *data, uint64_t n) {
+    const uint8_t *p = (const uint8_t *)data;
+    const uint64_t a = 0x9e3779b97f4a7c15ull, b = 0xd6e8feb86659fd93ull;
+    uint64_t h[4] = {n ^ a, n ^ b, ~n ^ a, ~n ^ b}, w;
+    uint64_t blocks = n / 32, i;
+    for (i = 0; i < blocks; ++i)
+        for (int l = 0; l < 4; ++l) {
+            memcpy(&w, p + 32 * i + 8 * l, 8);
+            h[l] = orc_hmix(h[l], w);
+        }
+    const uint8_t *t = p + 32 * blocks;
+    const uint64_t rest = n - 32 * blocks;
+    uint64_t j = 0;
+    for (int l = 0; j + 8 <= rest; j += 8, ++l) {
+        memcpy(&w, t + j, 8);
+        h[l] = orc_hmix(h[l], w);
+    }
+    if (j < rest) {
+        w = 0;
+        memcpy(&w, t + j, rest - j);
+        h[0] = orc_hmix(h[0], w ^ ((rest - j) << 56));
+    }
+    uint64_t r = orc_hmix(orc_hmix(orc_hmix(h[0], h[1]), h[2]), h[3]);
+    r = (r ^ (r >> 33)) * a;
+    return r ^ (r >> 29);
+}

@@ -138,6 +138,10 @@ typedef struct {
 
 int orc_moe_layer(const orc_layer *L, orc_layer_out *o, int threads);
 
+/* strixw's component / header / index hash, one shot (strixite formats/strixw.cpp:204-246: four lanes seeded by the
+ * length, 32-byte blocks, the tail's 8-byte words then its last bytes tagged with their count, a fold and a finish). */
+uint64_t orc_strixw_hash64(const void *p, uint64_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,18 @@ class LayerWeights(C.Structure):  # strix_moe_layer_weights
                 ("sh_gate_up", QView), ("sh_down", QView), ("shared_stacked", _int)]
 
 
+class StrixwTensorInfo(C.Structure):  # strix_strixw_tensor_info
+    _fields_ = [("name", C.c_char_p), ("encoding", _int), ("ndim", _int), ("shape", _i64 * 8), ("group_size", _i64),
+                ("experts", _i64), ("nparts", _i64), ("ncomponents", _int), ("role", _int * 4),
+                ("offset", _u64 * 4), ("bytes", _u64 * 4), ("hash", _u64 * 4)]
+
+
+class StrixwPlan(C.Structure):  # strix_strixw_plan_t
+    _fields_ = [("name", C.c_char_p), ("encoding", _int), ("ndim", _int), ("shape", _i64 * 8), ("group_size", _i64),
+                ("experts", _i64), ("nparts", _i64), ("part_sources", C.POINTER(C.c_char_p)),
+                ("part_rows", C.POINTER(_i64))]
+
+
 _SIGS = {
     "strix_moe_abi_version": (_int, []),
     "strix_moe_last_error": (C.c_char_p, []),
@@ -77,6 +89,26 @@ _SIGS = {
     "strix_moe_layer_forward": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _sz, _p, _p, _p,
                                        C.POINTER(InjectArgs)]),
     "strix_hc_inject": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _p]),
+    "strix_strixw_hash64": (_u64, [_p, _sz]),
+    "strix_strixw_open": (_int, [C.c_char_p, C.POINTER(_p)]),
+    "strix_strixw_close": (_int, [_p]),
+    "strix_strixw_info": (_int, [_p, C.POINTER(_u64), C.POINTER(_u64), C.POINTER(_u32), C.POINTER(_i64),
+                                 C.POINTER(_i64)]),
+    "strix_strixw_tensor": (_int, [_p, _i64, C.POINTER(StrixwTensorInfo)]),
+    "strix_strixw_find": (_int, [_p, C.c_char_p, C.POINTER(_i64)]),
+    "strix_strixw_part": (_int, [_p, _i64, _i64, C.POINTER(C.c_char_p), C.POINTER(_i64), C.POINTER(_i64)]),
+    "strix_strixw_meta": (_int, [_p, _i64, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p)]),
+    "strix_strixw_verify": (_int, [_p, _int]),
+    "strix_strixw_writer_create": (_int, [C.c_char_p, _i64, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), _i64,
+                                          C.POINTER(StrixwPlan), C.POINTER(_p)]),
+    "strix_strixw_writer_write": (_int, [_p, _i64, _int, _p, _sz]),
+    "strix_strixw_writer_finish": (_int, [_p]),
+    "strix_strixw_writer_destroy": (_int, [_p]),
+    "strix_strixw_device_load": (_int, [C.c_char_p, _int, C.POINTER(_p)]),
+    "strix_strixw_device_free": (_int, [_p]),
+    "strix_strixw_device_info": (_int, [_p, C.POINTER(_u64), C.POINTER(C.c_double)]),
+    "strix_strixw_device_ptr": (_int, [_p, C.c_char_p, _int, C.POINTER(_p)]),
+    "strix_strixw_moe_layer": (_int, [_p, C.c_char_p, _i64, C.POINTER(LayerWeights)]),
     "strix_synth_tensor_key": (_u64, [_u64, _u32, _u32]),
     "strix_synth_bf16_normal": (_int, [_u64, _f32, _p, _i64, _p]),
     "strix_synth_q_weight": (_int, [_int, _u64, _u64, _i64, _i64, _i64, _p, _p, _p, _p]),

@@ -2,8 +2,12 @@
 #include "strixite_moe.h"
 
 #include "common.hpp"
+#include "strixite_strixw.hpp"
 
+#include <iterator>
+#include <map>
 #include <string>
+#include <vector>
 
 namespace strix::synth {
 uint64_t tensor_key(uint64_t seed, uint32_t tensor, uint32_t layer);
@@ -279,6 +283,195 @@ int strix_synth_q_weight(int bits, uint64_t key_codes, uint64_t key_scales, int6
 }
 int strix_synth_uniform_pm1(uint64_t key, float *out, int64_t n, void *stream) {
     return guard([&] { strix::synth::uniform_pm1(key, out, n, st(stream)); });
+}
+
+}  // extern "C"
+
+// ---- strixw ---------------------------------------------------------------------------------------------------
+namespace {
+strix::StrixwFile *file_of(void *f) {
+    STRIX_CHECK(f != nullptr, "null strixw file handle");
+    return static_cast<strix::StrixwFile *>(f);
+}
+strix::StrixwDevice *device_of(void *d) {
+    STRIX_CHECK(d != nullptr, "null strixw device handle");
+    return static_cast<strix::StrixwDevice *>(d);
+}
+strix::StrixwRole role_of(int r) {
+    STRIX_CHECK(r >= 0 && r <= 3, "strixw role code ", r, " (0 data, 1 q, 2 scale, 3 min)");
+    return static_cast<strix::StrixwRole>(r);
+}
+strix_moe_layer_weights c_layer(const strix::MoeLayerWeights &L) {
+    strix_moe_layer_weights w{};
+    w.H = L.H, w.E = L.E, w.k = L.k, w.I = L.I;
+    w.router = L.router, w.router_bias = L.router_bias;
+    w.routed_bits = L.gate_up_bits;
+    w.gate_up = {L.gate_up.q, L.gate_up.scale, L.gate_up.minv, L.gate_up.N, L.gate_up.K, L.gate_up.G};
+    w.down = {L.down.q, L.down.scale, L.down.minv, L.down.N, L.down.K, L.down.G};
+    w.has_shared = L.has_shared ? 1 : 0;
+    if (L.has_shared) {
+        w.sh_gate_up = {L.sh_gate_up.q, L.sh_gate_up.scale, L.sh_gate_up.minv, L.sh_gate_up.N, L.sh_gate_up.K,
+                        L.sh_gate_up.G};
+        w.sh_down = {L.sh_down.q, L.sh_down.scale, L.sh_down.minv, L.sh_down.N, L.sh_down.K, L.sh_down.G};
+    }
+    w.shared_stacked = L.shared_stacked ? 1 : 0;
+    return w;
+}
+}  // namespace
+
+extern "C" {
+
+uint64_t strix_strixw_hash64(const void *p, size_t n) { return strix::strix_hash64(p, n); }
+
+int strix_strixw_open(const char *path, void **file) {
+    return guard([&] {
+        STRIX_CHECK(path != nullptr && file != nullptr, "strix_strixw_open: null argument");
+        *file = nullptr;
+        *file = new strix::StrixwFile(path);
+    });
+}
+int strix_strixw_close(void *file) {
+    return guard([&] { delete file_of(file); });
+}
+int strix_strixw_info(void *file, uint64_t *file_bytes, uint64_t *data_offset, uint32_t *version, int64_t *ntensors,
+                      int64_t *nmeta) {
+    return guard([&] {
+        const strix::StrixwFile *f = file_of(file);
+        if (file_bytes) *file_bytes = f->file_bytes();
+        if (data_offset) *data_offset = f->data_offset();
+        if (version) *version = f->version();
+        if (ntensors) *ntensors = (int64_t)f->tensors().size();
+        if (nmeta) *nmeta = (int64_t)f->meta().size();
+    });
+}
+int strix_strixw_tensor(void *file, int64_t i, strix_strixw_tensor_info *out) {
+    return guard([&] {
+        const strix::StrixwFile *f = file_of(file);
+        STRIX_CHECK(out != nullptr && i >= 0 && i < (int64_t)f->tensors().size(), "strix_strixw_tensor: index ", i,
+                    " of ", f->tensors().size());
+        const strix::StrixwTensor &t = f->tensors()[(size_t)i];
+        *out = strix_strixw_tensor_info{};
+        out->name = t.name.c_str();
+        out->encoding = (int)t.encoding;
+        out->ndim = (int)t.shape.size();
+        for (size_t d = 0; d < t.shape.size(); ++d) out->shape[d] = t.shape[d];
+        out->group_size = t.group_size, out->experts = t.experts, out->nparts = (int64_t)t.parts.size();
+        out->ncomponents = (int)t.components.size();
+        for (size_t c = 0; c < t.components.size() && c < 4; ++c) {
+            out->role[c] = (int)t.components[c].role;
+            out->offset[c] = t.components[c].offset, out->bytes[c] = t.components[c].bytes;
+            out->hash[c] = t.components[c].hash;
+        }
+    });
+}
+int strix_strixw_find(void *file, const char *name, int64_t *index) {
+    return guard([&] {
+        const strix::StrixwFile *f = file_of(file);
+        STRIX_CHECK(name != nullptr && index != nullptr, "strix_strixw_find: null argument");
+        const strix::StrixwTensor *t = f->find(name);
+        *index = t ? (int64_t)(t - f->tensors().data()) : -1;
+    });
+}
+int strix_strixw_part(void *file, int64_t tensor, int64_t part, const char **source, int64_t *row_offset,
+                      int64_t *rows) {
+    return guard([&] {
+        const strix::StrixwFile *f = file_of(file);
+        STRIX_CHECK(tensor >= 0 && tensor < (int64_t)f->tensors().size(), "strix_strixw_part: tensor ", tensor);
+        const auto &ps = f->tensors()[(size_t)tensor].parts;
+        STRIX_CHECK(part >= 0 && part < (int64_t)ps.size(), "strix_strixw_part: part ", part, " of ", ps.size());
+        if (source) *source = ps[(size_t)part].source.c_str();
+        if (row_offset) *row_offset = ps[(size_t)part].row_offset;
+        if (rows) *rows = ps[(size_t)part].rows;
+    });
+}
+int strix_strixw_meta(void *file, int64_t i, const char **key, const char **value) {
+    return guard([&] {
+        const strix::StrixwFile *f = file_of(file);
+        STRIX_CHECK(i >= 0 && i < (int64_t)f->meta().size(), "strix_strixw_meta: index ", i, " of ", f->meta().size());
+        auto it = f->meta().begin();
+        std::advance(it, i);
+        if (key) *key = it->first.c_str();
+        if (value) *value = it->second.c_str();
+    });
+}
+int strix_strixw_verify(void *file, int threads) {
+    return guard([&] { file_of(file)->verify_hashes(threads); });
+}
+
+int strix_strixw_writer_create(const char *path, int64_t nmeta, const char *const *keys, const char *const *values,
+                               int64_t ntensors, const strix_strixw_plan_t *plan, void **writer) {
+    return guard([&] {
+        STRIX_CHECK(path != nullptr && writer != nullptr && nmeta >= 0 && ntensors >= 1 && plan != nullptr &&
+                        (nmeta == 0 || (keys != nullptr && values != nullptr)),
+                    "strix_strixw_writer_create: bad arguments");
+        *writer = nullptr;
+        std::map<std::string, std::string> meta;
+        for (int64_t i = 0; i < nmeta; ++i) meta[keys[i]] = values[i];
+        std::vector<strix::StrixwTensor> ts((size_t)ntensors);
+        for (int64_t i = 0; i < ntensors; ++i) {
+            const strix_strixw_plan_t &p = plan[i];
+            STRIX_CHECK(p.name != nullptr && p.ndim >= 1 && p.ndim <= 8 && p.encoding >= 1 && p.encoding <= 9,
+                        "strix_strixw_writer_create: plan ", i, " (ndim ", p.ndim, ", encoding ", p.encoding, ")");
+            strix::StrixwTensor &t = ts[(size_t)i];
+            t.name = p.name;
+            t.encoding = static_cast<strix::StrixwEncoding>(p.encoding);
+            t.shape.assign(p.shape, p.shape + p.ndim);
+            t.group_size = p.group_size, t.experts = p.experts;
+            STRIX_CHECK(p.nparts >= 0 && (p.nparts == 0 || (p.part_sources != nullptr && p.part_rows != nullptr)),
+                        "strix_strixw_writer_create: plan ", i, " parts");
+            for (int64_t j = 0, row = 0; j < p.nparts; row += p.part_rows[j], ++j) {
+                STRIX_CHECK(p.part_sources[j] != nullptr, "strix_strixw_writer_create: plan ", i, " part ", j);
+                t.parts.push_back({p.part_sources[j], row, p.part_rows[j]});
+            }
+        }
+        *writer = new strix::StrixwWriter(path, std::move(meta), std::move(ts));
+    });
+}
+int strix_strixw_writer_write(void *writer, int64_t tensor, int role, const void *data, size_t bytes) {
+    return guard([&] {
+        STRIX_CHECK(writer != nullptr && tensor >= 0, "strix_strixw_writer_write: bad arguments");
+        static_cast<strix::StrixwWriter *>(writer)->write((size_t)tensor, role_of(role), data, bytes);
+    });
+}
+int strix_strixw_writer_finish(void *writer) {
+    return guard([&] {
+        STRIX_CHECK(writer != nullptr, "strix_strixw_writer_finish: null writer");
+        static_cast<strix::StrixwWriter *>(writer)->finish();
+    });
+}
+int strix_strixw_writer_destroy(void *writer) {
+    return guard([&] { delete static_cast<strix::StrixwWriter *>(writer); });
+}
+
+int strix_strixw_device_load(const char *path, int read_threads, void **dev) {
+    return guard([&] {
+        STRIX_CHECK(path != nullptr && dev != nullptr, "strix_strixw_device_load: null argument");
+        *dev = nullptr;
+        *dev = new strix::StrixwDevice(path, read_threads);
+    });
+}
+int strix_strixw_device_free(void *dev) {
+    return guard([&] { delete static_cast<strix::StrixwDevice *>(dev); });
+}
+int strix_strixw_device_info(void *dev, uint64_t *device_bytes, double *load_seconds) {
+    return guard([&] {
+        const strix::StrixwDevice *d = device_of(dev);
+        if (device_bytes) *device_bytes = d->device_bytes();
+        if (load_seconds) *load_seconds = d->load_seconds();
+    });
+}
+int strix_strixw_device_ptr(void *dev, const char *name, int role, const void **ptr) {
+    return guard([&] {
+        const strix::StrixwDevice *d = device_of(dev);
+        STRIX_CHECK(name != nullptr && ptr != nullptr, "strix_strixw_device_ptr: null argument");
+        *ptr = d->ptr(d->file().get(name), role_of(role));
+    });
+}
+int strix_strixw_moe_layer(void *dev, const char *prefix, int64_t top_k, strix_moe_layer_weights *out) {
+    return guard([&] {
+        STRIX_CHECK(prefix != nullptr && out != nullptr, "strix_strixw_moe_layer: null argument");
+        *out = c_layer(strix::strixw_moe_layer(*device_of(dev), prefix, top_k));
+    });
 }
 
 }  // extern "C"

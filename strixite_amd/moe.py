@@ -339,9 +339,23 @@ class MoeLayer:
             w.sh_gate_up, w.sh_down = shared_gate_up.view(), shared_down.view()
         w.shared_stacked = 1 if shared_stacked else 0
 
+    @staticmethod
+    def from_view(w: "L.LayerWeights", owner=None) -> "MoeLayer":
+        """A layer over weights that live elsewhere in device memory (e.g. a strixw file loaded into HBM); owner is
+        kept alive with the layer."""
+        m = MoeLayer.__new__(MoeLayer)
+        m.H, m.E, m.k, m.I = w.H, w.E, w.k, w.I
+        m.shared_stacked = bool(w.shared_stacked)
+        m.A = m.k + (1 if m.shared_stacked else 0)
+        m.router = m.router_bias = m.gate_up = m.down = m.shared_gate_up = m.shared_down = None
+        m._has_shared_view = bool(w.has_shared)
+        m._owner = owner
+        m._w = w
+        return m
+
     @property
     def has_shared(self) -> bool:
-        return self.shared_gate_up is not None
+        return getattr(self, "_has_shared_view", False) or self.shared_gate_up is not None
 
     @property
     def weight_bytes(self) -> int:

@@ -18,7 +18,7 @@ def test_library_exports_every_declared_symbol():
     assert len(declared) >= 25
     missing = [n for n in declared if not hasattr(L, n)]
     assert not missing, missing
-    assert L.strix_moe_abi_version() == 3
+    assert L.strix_moe_abi_version() == 4
 
 
 def test_cpp_header_declares_reference_signatures():
@@ -151,3 +151,25 @@ def test_exports_match_reference_declarations():
     missing = [sig for name, sig in decls if name not in NOT_BUILT and sig not in exported]
     assert not missing, missing
     assert not any("act_name" in e for e in exported)
+
+
+def test_strixw_exports_reference_names():
+    """The strixw reader / writer / loader export the names strixite formats/strixw.hpp and runtime/strixw_loader.hpp
+    declare (the Device placement's subset of StrixwDevice), so the engine's loading code links unchanged."""
+    import subprocess
+
+    from strixite_amd import _lib
+
+    nm = subprocess.run(["nm", "-DC", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                        check=True).stdout
+    exported = [line.split(" ", 2)[2] for line in nm.splitlines() if " T " in line or " W " in line]
+    for name in ["strix::strixw_encoding_name", "strix::strixw_role_name", "strix::strixw_components",
+                 "strix::strix_hash64", "strix::StrixHasher::StrixHasher", "strix::StrixHasher::update",
+                 "strix::StrixHasher::final", "strix::StrixwTensor::numel", "strix::StrixwTensor::bytes",
+                 "strix::StrixwWriter::StrixwWriter", "strix::StrixwWriter::write", "strix::StrixwWriter::finish",
+                 "strix::StrixwFile::StrixwFile", "strix::StrixwFile::meta", "strix::StrixwFile::find",
+                 "strix::StrixwFile::get", "strix::StrixwFile::data", "strix::StrixwFile::verify_hashes",
+                 "strix::StrixwDevice::StrixwDevice", "strix::StrixwDevice::tensor", "strix::StrixwDevice::ptr",
+                 "strix::StrixwDevice::q4", "strix::StrixwDevice::q8", "strix::StrixwDevice::f32",
+                 "strix::StrixwDevice::bf16"]:
+        assert any(e.startswith(name + "(") for e in exported), name
