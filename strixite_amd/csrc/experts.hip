@@ -41,11 +41,46 @@ constexpr int kWave = 64, kWaves = 4, kThreads = kWave * kWaves;
 enum Mode { GROUPED = 0, DENSE = 1, PERSLOT = 2 };
 enum Epi { EPI_SWIGLU = 0, EPI_BF16 = 1, EPI_F32 = 2 };
 
-template <int BITS> struct QFmt {
-    static constexpr int CPL = BITS == 4 ? 32 : 16;  // codes per lane per 16-byte load
-    static constexpr int SPAN = 4 * CPL;             // codes per row per K step
+// A K step covers SP codes of a row: 4 lane groups x CPL codes, one quantization group at most, so each step has one
+// scale and min. SP is the 16-byte load's span (Q4: 128 codes, Q8: 64) unless the group size G is smaller: then
+// SP = G and a lane loads 8 or 4 bytes a step.
+template <int BITS> constexpr int max_span() { return BITS == 4 ? 128 : 64; }
+template <int BITS, int SP = max_span<BITS>()> struct QFmt {
+    static_assert(SP == 32 || SP == 64 || (SP == 128 && BITS == 4), "K step: 32, 64 or (Q4) 128 codes");
+    static constexpr int SPAN = SP;                  // codes per row per K step
+    static constexpr int CPL = SP / 4;               // codes per lane per step
+    static constexpr int LB = CPL * BITS / 8;        // bytes per lane per step: 16, 8 or 4
+    static constexpr int SB = 4 * LB;                // bytes of a row per step
     static constexpr int NT = CPL / 8;               // MFMAs per K step
 };
+// the K step for group size G
+inline int span_of(int bits, int64_t G) { return (int)std::min<int64_t>(G, bits == 4 ? 128 : 64); }
+
+// LB bytes of codes (16, 8 or 4) at byte offset voff + soff, in the low dwords of a uint4
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+template <int LB> __device__ __forceinline__ uint4 bld_codes(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    uint4 c;
+    if constexpr (LB == 16) {
+        const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+        c = make_uint4(v.x, v.y, v.z, v.w);
+    } else if constexpr (LB == 8) {
+        typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+        const u32x2v v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+        c.x = v.x, c.y = v.y;
+    } else {
+        c.x = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    }
+    return c;
+}
+template <int LB> __device__ __forceinline__ uint4 ld_codes(const uint8_t *p) {
+    uint4 c;
+    if constexpr (LB == 16) c = *reinterpret_cast<const uint4 *>(p);
+    else if constexpr (LB == 8) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        c.x = v.x, c.y = v.y;
+    } else c.x = *reinterpret_cast<const uint32_t *>(p);
+    return c;
+}
 
 struct GemmArgs {
     const uint16_t *x;  // A rows (bf16, or f16 bits when XF16), row stride K
@@ -89,10 +124,10 @@ template <> __device__ __forceinline__ void store1<float>(float *p, float v) { *
 
 // One 16-token x RT 16-row wave tile over the K steps [s0, s1): acc[rt][r] = token 4g + r, weight column
 // (lane % 16) of tile rt. Loads run two K steps ahead of the math.
-template <int BITS, int RT, bool XF16>
+template <int BITS, int SP, int RT, bool XF16>
 __device__ __forceinline__ void wave_gemm(const GemmArgs &a, const uint16_t *xrow, const int64_t (&tile_row)[RT],
                                           int64_t s0, int64_t s1, float4v (&acc)[RT]) {
-    using F = QFmt<BITS>;
+    using F = QFmt<BITS, SP>;
     const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
     const int64_t row_bytes = a.K * BITS / 8, groups = a.K / a.G;
     const uint8_t *qp[RT];
@@ -100,7 +135,7 @@ __device__ __forceinline__ void wave_gemm(const GemmArgs &a, const uint16_t *xro
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const int64_t r = tile_row[rt] + j;
-        qp[rt] = a.q + r * row_bytes + g * 16;
+        qp[rt] = a.q + r * row_bytes + g * F::LB;
         sp[rt] = a.scale + r * groups;
         mp[rt] = a.minv + r * groups;
         acc[rt] = float4v{0, 0, 0, 0};
@@ -114,7 +149,7 @@ __device__ __forceinline__ void wave_gemm(const GemmArgs &a, const uint16_t *xro
         const int64_t gi = s * F::SPAN / a.G;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-            b.q[rt] = ld16(qp[rt] + s * 64);
+            b.q[rt] = ld_codes<F::LB>(qp[rt] + s * F::SB);
             b.s[rt] = sp[rt][gi];
             b.m[rt] = mp[rt][gi];
         }
@@ -178,7 +213,6 @@ __device__ __forceinline__ void wave_gemm(const GemmArgs &a, const uint16_t *xro
 // token gets an offset past the activation buffer's end, and the hardware returns zeros.
 // The per-step activation sums (the min term) come from one more MFMA against an all-ones B operand: its D rows are
 // the token sums, already in the lanes that hold those tokens' outputs.
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
     return make_uint4(v.x, v.y, v.z, v.w);
@@ -240,7 +274,7 @@ __device__ __forceinline__ RawItem load_raw(const GemmArgs &a, int64_t item, int
     return r;
 }
 
-template <int BITS, int MODE, bool SWI, int RT, bool XROW_DIV>
+template <int BITS, int SP, int MODE, bool SWI, int RT, bool XROW_DIV>
 __device__ __forceinline__ Item<RT> make_item(const GemmArgs &a, const RawItem &raw, int64_t item, int64_t n_items,
                                               int64_t col_blocks, bool report, uint32_t x_bytes) {
     const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
@@ -258,12 +292,12 @@ __device__ __forceinline__ Item<RT> make_item(const GemmArgs &a, const RawItem &
         }
     }
     it.xoff = raw.my >= 0 ? ((XROW_DIV ? (uint32_t)raw.my / (uint32_t)a.A : (uint32_t)raw.my) * (uint32_t)a.K +
-                             g * QFmt<BITS>::CPL) * 2
+                             g * QFmt<BITS, SP>::CPL) * 2
                           : x_bytes;
     it.my = raw.my;
     it.c0 = (int32_t)(cb * 16 * (SWI ? RT / 2 : RT));
     const uint32_t row = expert * (uint32_t)a.N + it.c0 + j;
-    it.qoff = row * (uint32_t)(a.K * BITS / 8) + g * 16;
+    it.qoff = row * (uint32_t)(a.K * BITS / 8) + g * QFmt<BITS, SP>::LB;
     const uint32_t e = row * (uint32_t)(a.K / a.G);
     it.par = e & 1u;
     it.soff = (e - it.par) * 2;
@@ -320,31 +354,31 @@ __device__ __forceinline__ int step_source(const Stream<RT> &st, const Item<RT> 
 
 // Every step issues the same loads - with no source, at offsets past the buffers' ends, which read zeros -, so no
 // branch changes the compiler's wait counts.
-template <int BITS, int RT>
+template <int BITS, int SP, int RT>
 __device__ __forceinline__ void fetch_x(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt, int t,
                                         uint4 *xs) {
     bool in_cur, in_nxt;
     const int s = step_source(st, nxt, t, in_cur, in_nxt);
     const uint32_t xo = in_cur ? cur.xoff : in_nxt ? nxt.xoff : st.x_bytes;
 #pragma unroll
-    for (int u = 0; u < QFmt<BITS>::NT; ++u)
-        lds_load16(st.rx, xs + u * kWave, xo, (uint32_t)(s * QFmt<BITS>::SPAN + 8 * u) * 2);
+    for (int u = 0; u < QFmt<BITS, SP>::NT; ++u)
+        lds_load16(st.rx, xs + u * kWave, xo, (uint32_t)(s * SP + 8 * u) * 2);
 }
 
-template <int BITS, int RT, bool SST>
+template <int BITS, int SP, int RT, bool SST>
 __device__ __forceinline__ void fetch_codes(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt, int t,
                                             Codes<RT, SST> &c) {
     bool in_cur, in_nxt;
     const int s = step_source(st, nxt, t, in_cur, in_nxt);
     // group gi = s * SPAN / G: the dword holding element 2k and 2k + 1 lies at 4k, one dword further for an odd
     // gi when the row's parity is odd
-    const uint32_t gi = (uint32_t)((s * QFmt<BITS>::SPAN) >> st.gsh), g1 = gi & 1u;
+    const uint32_t gi = (uint32_t)((s * SP) >> st.gsh), g1 = gi & 1u;
     const uint32_t goff = (gi - g1) * 2;
     const uint32_t qo = in_cur ? cur.qoff : in_nxt ? nxt.qoff : st.q_bytes;
     const uint32_t so = in_cur ? cur.soff + 4 * (cur.par & g1) : in_nxt ? nxt.soff + 4 * (nxt.par & g1) : st.s_bytes;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        c.q[rt] = bld16(st.rq, qo, (uint32_t)s * 64 + st.dq[rt]);
+        c.q[rt] = bld_codes<QFmt<BITS, SP>::LB>(st.rq, qo, (uint32_t)s * QFmt<BITS, SP>::SB + st.dq[rt]);
         if constexpr (!SST) {
             c.s[rt] = bld4(st.rs, so, goff + st.dsm[rt]);
             c.m[rt] = bld4(st.rm, so, goff + st.dsm[rt]);
@@ -354,11 +388,11 @@ __device__ __forceinline__ void fetch_codes(const Stream<RT> &st, const Item<RT>
 
 // One K step of cur from ring position q % D (codes cb, activations xs); the activations of step q + D - 1 go to
 // xfree (the slot of step q - 1), the codes of step q + D to cb once consumed.
-template <int BITS, int RT, bool XF16, int D, bool SST>
+template <int BITS, int SP, int RT, bool XF16, int D, bool SST>
 __device__ __forceinline__ void stream_step(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt,
                                             Codes<RT, SST> &cb, const uint4 *xs, uint4 *xfree, int q,
                                             float4v (&acc)[RT], int lane, const uint16_t *sl) {
-    constexpr int NT = QFmt<BITS>::NT;
+    constexpr int NT = QFmt<BITS, SP>::NT;
     const Frag ones{{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}};
     Frag af[NT];
 #pragma unroll
@@ -366,7 +400,7 @@ __device__ __forceinline__ void stream_step(const Stream<RT> &st, const Item<RT>
         const uint4 v = xs[u * kWave + lane];
         af[u] = a_frag<BITS>(XF16 ? f16x8_to_bf16x8(v) : v);
     }
-    fetch_x<BITS, RT>(st, cur, nxt, q + D - 1, xfree);
+    fetch_x<BITS, SP, RT>(st, cur, nxt, q + D - 1, xfree);
     float4v d[RT], dx = {0, 0, 0, 0};
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) d[rt] = float4v{0, 0, 0, 0};
@@ -377,7 +411,7 @@ __device__ __forceinline__ void stream_step(const Stream<RT> &st, const Item<RT>
         dx = mfma_bf16(af[u], ones, dx);
         __builtin_amdgcn_sched_barrier(0);  // decode each group's codes just before its MFMAs (register pressure)
     }
-    const uint32_t gi = (uint32_t)(((st.s0 + q) * QFmt<BITS>::SPAN) >> st.gsh);
+    const uint32_t gi = (uint32_t)(((st.s0 + q) * SP) >> st.gsh);
     float sc[RT], mn[RT];
     if constexpr (SST) {
         // staged in LDS as [group][scale, min][tile][row]: sl points at this lane's row of group 0. A padding step
@@ -401,7 +435,7 @@ __device__ __forceinline__ void stream_step(const Stream<RT> &st, const Item<RT>
             mn[rt] = BITS == 4 ? fmaf(-128.0f, sc[rt], m) : m;
         }
     }
-    fetch_codes<BITS, RT, SST>(st, cur, nxt, q + D, cb);
+    fetch_codes<BITS, SP, RT, SST>(st, cur, nxt, q + D, cb);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -409,14 +443,14 @@ __device__ __forceinline__ void stream_step(const Stream<RT> &st, const Item<RT>
 }
 
 // Ring positions I..D-1 of one trip, expanded at compile time (the slots are fixed registers and LDS arrays).
-template <int BITS, int RT, bool XF16, int D, bool SST, int I>
+template <int BITS, int SP, int RT, bool XF16, int D, bool SST, int I>
 __device__ __forceinline__ void stream_trip(const Stream<RT> &st, const Item<RT> &cur, const Item<RT> &nxt,
                                             Codes<RT, SST> (&c)[D], uint4 *(&xr)[D], int q, float4v (&acc)[RT],
                                             int lane, const uint16_t *sl) {
     if constexpr (I < D) {
-        stream_step<BITS, RT, XF16, D, SST>(st, cur, nxt, c[I], xr[I], xr[(I + D - 1) % D], q + I, acc, lane, sl);
+        stream_step<BITS, SP, RT, XF16, D, SST>(st, cur, nxt, c[I], xr[I], xr[(I + D - 1) % D], q + I, acc, lane, sl);
         __builtin_amdgcn_sched_barrier(0);  // no interleaving of steps: it only raises register pressure
-        stream_trip<BITS, RT, XF16, D, SST, I + 1>(st, cur, nxt, c, xr, q, acc, lane, sl);
+        stream_trip<BITS, SP, RT, XF16, D, SST, I + 1>(st, cur, nxt, c, xr, q, acc, lane, sl);
     }
 }
 
@@ -470,14 +504,14 @@ __device__ __forceinline__ void stage_store(const Stage<RT> &sg, int tid, int nt
 //   combine launch: the down's finish, s = bf16(sum over the parts in order), read where the stored s was.
 // A unit of the split-K projection: wave w computes rows tile * 16 .. + 15 over K steps [part * spp, (part + 1) * spp)
 // for all M tokens and writes its FP32 sums to part[part][m][n].
-template <int BITS>
+template <int BITS, int SP = max_span<BITS>()>
 __device__ __forceinline__ void dense_part_unit(const GemmArgs &a, int spp, int parts, float *part, int64_t w) {
     const int lane = threadIdx.x % kWave, g = lane / 16, j = lane % 16;
     const int64_t tile = w / parts, pt = w % parts;
-    const int64_t spans = a.K / QFmt<BITS>::SPAN, s0 = pt * spp, s1 = s0 + spp < spans ? s0 + spp : spans;
+    const int64_t spans = a.K / SP, s0 = pt * spp, s1 = s0 + spp < spans ? s0 + spp : spans;
     const int64_t tile_row[1] = {tile * 16};
     float4v acc[1];
-    wave_gemm<BITS, 1, false>(a, j < a.M ? a.x + j * a.K : nullptr, tile_row, s0, s1, acc);
+    wave_gemm<BITS, SP, 1, false>(a, j < a.M ? a.x + j * a.K : nullptr, tile_row, s0, s1, acc);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
         if (4 * g + r < a.M) part[(pt * a.M + 4 * g + r) * a.N + tile * 16 + j] = acc[0][r];
@@ -506,11 +540,11 @@ struct SharedJob {
 };
 
 // SH: the shared expert's projection riding along (0 none, 1 the Q8 gate_up + SwiGLU, 2 the Q8 down)
-template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH>
+template <int BITS, int SP, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<EPI == EPI_SWIGLU>())))
     expert_stream_kernel(GemmArgs a, int64_t tiles_bound, int64_t col_blocks, int ks, uint32_t q_bytes,
                          uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes, SharedJob sh) {
-    using F = QFmt<BITS>;
+    using F = QFmt<BITS, SP>;
     int bid = (int)blockIdx.x, nblk = (int)gridDim.x;  // this block among the routed blocks
     if constexpr (SH != 0) {
         if (bid < sh.blocks) {  // a shared-expert block: its units, then done (no barrier in this branch)
@@ -567,14 +601,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     st.s0 = KS > 1 ? spans * wave / ks : 0;
     st.spw = KS > 1 ? spans * (wave + 1) / ks - st.s0 : spans;
     st.spe = (st.spw + D - 1) / D * D;
-    st.gsh = a.G == 128 ? 7 : 6;
+    st.gsh = a.G == 128 ? 7 : a.G == 64 ? 6 : 5;
     st.groups = (uint32_t)(a.K / a.G);
     const __amdgpu_buffer_rsrc_t ry = rsrc(a.y, y_bytes);
 
     // three items in flight: cur (streaming), nxt (offsets ready, its first steps prefetched), raw (loads issued)
-    Item<RT> cur = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, load_raw<MODE>(a, first, n_tiles, col_blocks), first,
+    Item<RT> cur = make_item<BITS, SP, MODE, SWI, RT, XROW_DIV>(a, load_raw<MODE>(a, first, n_tiles, col_blocks), first,
                                                             n_items, col_blocks, report, x_bytes);
-    Item<RT> nxt = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, load_raw<MODE>(a, first + stride, n_tiles, col_blocks),
+    Item<RT> nxt = make_item<BITS, SP, MODE, SWI, RT, XROW_DIV>(a, load_raw<MODE>(a, first + stride, n_tiles, col_blocks),
                                                             first + stride, n_items, col_blocks, report, x_bytes);
     RawItem raw = load_raw<MODE>(a, first + 2 * stride, n_tiles, col_blocks);
     const int groups = (int)(a.K / a.G), tid = SWI ? wave * kWave + lane : lane, nthr = SWI ? ks * kWave : kWave;
@@ -595,8 +629,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     if constexpr (D > 3) xr[3] = &xr3[wave][0][0];
 #pragma unroll
     for (int t = 0; t < D; ++t) {
-        if (t < D - 1) fetch_x<BITS, RT>(st, cur, nxt, t, xr[t]);
-        fetch_codes<BITS, RT, SST>(st, cur, nxt, t, c[t]);
+        if (t < D - 1) fetch_x<BITS, SP, RT>(st, cur, nxt, t, xr[t]);
+        fetch_codes<BITS, SP, RT, SST>(st, cur, nxt, t, c[t]);
     }
     int parity = 0;
     for (int64_t item = first; item < n_items; item += stride) {
@@ -604,7 +638,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
         for (int rt = 0; rt < RT; ++rt) acc[rt] = float4v{0, 0, 0, 0};
         int q = 0;
         do {  // spe >= D: at least one trip (the wait counts after the loop rely on its loads)
-            stream_trip<BITS, RT, XF16, D, SST, 0>(st, cur, nxt, c, xr, q, acc, lane, sl);
+            stream_trip<BITS, SP, RT, XF16, D, SST, 0>(st, cur, nxt, c, xr, q, acc, lane, sl);
             q += D;
         } while (q < st.spe);
         // the item's end: K parts meet (SwiGLU), outputs stored
@@ -663,7 +697,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
             }
         }
         cur = nxt;
-        nxt = make_item<BITS, MODE, SWI, RT, XROW_DIV>(a, raw, item + 2 * stride, n_items, col_blocks, report, x_bytes);
+        nxt = make_item<BITS, SP, MODE, SWI, RT, XROW_DIV>(a, raw, item + 2 * stride, n_items, col_blocks, report, x_bytes);
         raw = load_raw<MODE>(a, item + 3 * stride, n_tiles, col_blocks);
         if constexpr (SST) stage_load<RT, SWI>(st, a, nxt, tid, nthr, groups, sg);
     }
@@ -675,7 +709,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
 // Per-slot combine (strixite kernels/linear_q4.hip:283-322): y[m, n] = sum_a coef[m, a] * (h[m, a, :] . Wd[id] row n),
 // the slot dots in FP32 from the MFMA (token row 0 of the tile), summed over a in order with fmaf, rounded once.
 // Two 16-row tiles a wave. Any invalid id of the token: NaN row, err.
-template <int BITS, bool XF16>
+template <int BITS, int SP, bool XF16>
 __global__ void __launch_bounds__(kThreads) perslot_combine_kernel(GemmArgs a, const float *coef) {
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int g = lane / 16, j = lane % 16;
@@ -700,8 +734,8 @@ __global__ void __launch_bounds__(kThreads) perslot_combine_kernel(GemmArgs a, c
             const int64_t e = a.ids[m * a.A + s];
             const int64_t tile_row[2] = {e * a.N + c0, e * a.N + (c0 + 16 < a.N ? c0 + 16 : c0)};
             float4v acc[2];
-            wave_gemm<BITS, 2, XF16>(a, j == 0 ? a.x + (m * a.A + s) * a.K : nullptr, tile_row, 0,
-                                     a.K / QFmt<BITS>::SPAN, acc);
+            wave_gemm<BITS, SP, 2, XF16>(a, j == 0 ? a.x + (m * a.A + s) * a.K : nullptr, tile_row, 0, a.K / SP,
+                                         acc);
             const float c = coef[m * a.A + s];
             out[0] = fmaf(c, acc[0][0], out[0]);
             out[1] = fmaf(c, acc[1][0], out[1]);
@@ -908,10 +942,7 @@ QV qv(const Q8DeviceView &w) { return {w.q, w.scale, w.minv, w.N, w.K, w.G, 8}; 
 void check_view(const char *fn, const QV &w, int64_t E) {
     STRIX_CHECK(w.q != nullptr && w.scale != nullptr && w.minv != nullptr, fn, ": null weight pointer (q=",
                 (const void *)w.q, ", scale=", (const void *)w.scale, ", min=", (const void *)w.minv, ")");
-    const int span = w.bits == 4 ? 128 : 64;
     STRIX_CHECK(w.G == 32 || w.G == 64 || w.G == 128, fn, ": group size ", w.G, " unsupported (32, 64 or 128)");
-    STRIX_CHECK(w.G % span == 0, fn, ": Q", w.bits, " group size ", w.G, " is below this path's K step of ", span,
-                " codes (supported: Q4 G = 128; Q8 G = 64 or 128)");
     STRIX_CHECK(w.K >= w.G && w.K % w.G == 0 && w.K <= (1 << 24), fn, ": K = ", w.K,
                 " must be a positive multiple of G = ", w.G, " and <= 2^24");
     STRIX_CHECK(E >= 1 && w.N % E == 0 && (w.N / E) % 16 == 0, fn, ": ", w.N, " weight rows for E = ", E,
@@ -945,18 +976,18 @@ int swiglu_ks(int64_t spans, int D) {
 
 #include "decode_gemv.hpp"
 
-template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH>
+template <int BITS, int SP, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH>
 void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, const SharedJob &sh, hipStream_t stream) {
     constexpr bool SWI = EPI == EPI_SWIGLU;
     constexpr int RT = wave_tiles<SWI>();
-    const int64_t spans = a.K / QFmt<BITS>::SPAN;
+    const int64_t spans = a.K / SP;
     const int ks = SWI ? swiglu_ks(spans, ring_depth<SWI>()) : 1;  // otherwise one wave per item over all of K
     // SwiGLU: two stage buffers for the block; otherwise one a wave
     const size_t lds = SST ? (size_t)(SWI ? 2 : kWaves) * 2 * RT * 16 * (a.K / a.G) * 2 : 0;
     const int threads = SWI ? ks * kWave : kThreads;
     const int64_t col_blocks = SWI ? (a.N / 2 + 16 * RT / 2 - 1) / (16 * RT / 2) : (a.N + 16 * RT - 1) / (16 * RT);
     const int64_t items = tiles_bound * col_blocks, per_block = SWI ? 1 : kWaves;
-    auto kernel = expert_stream_kernel<BITS, MODE, EPI, XF16, XROW_DIV, HF16, SST, SH>;
+    auto kernel = expert_stream_kernel<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, SST, SH>;
     // resident blocks a CU, cached for the last (block size, LDS) this instantiation was launched with
     static thread_local int occ_threads = -1, occ = 1;
     static thread_local size_t occ_lds = 0;
@@ -981,24 +1012,37 @@ void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, const SharedJob &sh, 
 }
 
 // sh: the shared expert's projection to run in the same launch (GROUPED bf16 activations only), or null
-template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
-void launch_gemm(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream, const SharedJob *sh = nullptr) {
+template <int BITS, int SP, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
+void launch_gemm_s(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream, const SharedJob *sh) {
     // scale staging when an item's scales fit kStageMax dwords a lane of the item's waves
     constexpr bool SWI = EPI == EPI_SWIGLU;
     constexpr int SHK = SWI ? 1 : 2;
-    const int lanes = (SWI ? swiglu_ks(a.K / QFmt<BITS>::SPAN, ring_depth<true>()) : 1) * kWave;
+    const int lanes = (SWI ? swiglu_ks(a.K / SP, ring_depth<true>()) : 1) * kWave;
     const int64_t per_tensor = wave_tiles<SWI>() * 8 * (a.K / a.G);  // dwords
     const bool sst = (per_tensor + lanes - 1) / lanes * 2 <= kStageMax;
     const SharedJob none{};
     if constexpr (MODE == GROUPED && !XF16 && (EPI == EPI_SWIGLU || EPI == EPI_F32)) {
         if (sh != nullptr) {
-            if (sst) return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, true, SHK>(a, tiles_bound, *sh, stream);
-            return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, false, SHK>(a, tiles_bound, *sh, stream);
+            if (sst) return launch_gemm_v<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, true, SHK>(a, tiles_bound, *sh, stream);
+            return launch_gemm_v<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, false, SHK>(a, tiles_bound, *sh, stream);
         }
     }
     STRIX_CHECK(sh == nullptr, "expert kernels: a shared projection rides along only with a grouped gate_up or down");
-    if (sst) return launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, true, 0>(a, tiles_bound, none, stream);
-    launch_gemm_v<BITS, MODE, EPI, XF16, XROW_DIV, HF16, false, 0>(a, tiles_bound, none, stream);
+    if (sst) return launch_gemm_v<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, true, 0>(a, tiles_bound, none, stream);
+    launch_gemm_v<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, false, 0>(a, tiles_bound, none, stream);
+}
+
+// the K step for the view's group size (Q4: G 128, 64, 32; Q8: G >= 64, 32)
+template <int BITS, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
+void launch_gemm(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream, const SharedJob *sh = nullptr) {
+    switch (span_of(BITS, a.G)) {
+        case 128:
+            if constexpr (BITS == 4) return launch_gemm_s<BITS, 128, MODE, EPI, XF16, XROW_DIV, HF16>(a, tiles_bound, stream, sh);
+            break;
+        case 64: return launch_gemm_s<BITS, 64, MODE, EPI, XF16, XROW_DIV, HF16>(a, tiles_bound, stream, sh);
+        default: break;
+    }
+    launch_gemm_s<BITS, 32, MODE, EPI, XF16, XROW_DIV, HF16>(a, tiles_bound, stream, sh);
 }
 
 template <int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16>
@@ -1276,7 +1320,11 @@ void linear_q4_experts_combine(const void *h, const Q4DeviceView &w, int64_t E, 
     GemmArgs a = make_args(v, E, h, y, N);
     a.A = A, a.M = M, a.ids = ids, a.err = err;
     dim3 grid((unsigned)((N + 32 * kWaves - 1) / (32 * kWaves)), (unsigned)M), block(kThreads);
-    perslot_combine_kernel<4, false><<<grid, block, 0, stream>>>(a, coef);
+    switch (span_of(4, a.G)) {
+        case 128: perslot_combine_kernel<4, 128, false><<<grid, block, 0, stream>>>(a, coef); break;
+        case 64: perslot_combine_kernel<4, 64, false><<<grid, block, 0, stream>>>(a, coef); break;
+        default: perslot_combine_kernel<4, 32, false><<<grid, block, 0, stream>>>(a, coef); break;
+    }
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E);
 }
 
@@ -1482,7 +1530,8 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     // shared expert (dense Q8): at decode sizes folded into the routed gate_up and down launches (no second stream,
     // whose join would cost more than the shared expert's few MB); otherwise on the helper stream: gate_up + SwiGLU ->
     // sh_h, down -> sh_s
-    const bool fold = w.has_shared && M <= 16 && M * A <= 1024;
+    // (the ride-along units stream Q8 in 64-code steps: a shared expert with G = 32 runs on its own instead)
+    const bool fold = w.has_shared && M <= 16 && M * A <= 1024 && w.sh_gate_up.G >= 64 && w.sh_down.G >= 64;
     SharedJob sh_jobs[2]{};  // ride along in the routed gate_up and down launches
     GemmArgs sh_gu{};        // its gate_up parts ride along in the top-k launch
     int sh_gu_spp = 0, sh_gu_parts = 0;
@@ -1493,14 +1542,14 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         check_view(fn, dv, 1);
         // K parts of at least 4 steps, at most kSharedParts: hundreds of waves stream each projection's rows at once
         auto split = [&](int64_t K, int &spp, int &parts) {
-            const int64_t spans = K / QFmt<8>::SPAN;
+            const int64_t spans = K / max_span<8>();
             parts = (int)std::max<int64_t>(1, std::min<int64_t>(kSharedParts, spans / 4));
             spp = (int)((spans + parts - 1) / parts);
         };
         sh_gu = make_args(gv, 1, x, nullptr, 0);
         sh_gu.M = M;
         split(gv.K, sh_gu_spp, sh_gu_parts);
-        const int ks = swiglu_ks(w.gate_up.K / (w.gate_up_bits == 4 ? QFmt<4>::SPAN : QFmt<8>::SPAN), ring_depth<true>());
+        const int ks = swiglu_ks(w.gate_up.K / span_of(w.gate_up_bits, w.gate_up.G), ring_depth<true>());
         SharedJob &j0 = sh_jobs[0];
         j0.a.M = M, j0.a.N = gv.N;
         j0.pin = sh_part, j0.out = sh_h, j0.parts = sh_gu_parts;

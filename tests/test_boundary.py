@@ -63,8 +63,8 @@ def test_preconditions_raise_before_launch():
     # overlapping output / input of the router projection
     rc = L.strix_linear_bf16w(p, p, p + 8, 1, 4, 64, 1, 0, None)
     assert rc == 1 and b"overlaps" in L.strix_moe_last_error()
-    # a Q4 group size the K step does not divide
-    v = _lib.QView(p, p, p, 64, 256, 64)
+    # a group size outside the format's 32 / 64 / 128
+    v = _lib.QView(p, p, p, 64, 256, 16)
     rc = L.strix_linear_q4_experts_gather_grouped_swiglu(p, C.byref(v), 2, p, 1 << 20, 4, 2, p + 2048, 1, 2, None, 0)
     assert rc == 1 and b"group size" in L.strix_moe_last_error()
     # too small a workspace

@@ -677,3 +677,69 @@ def test_layer_stacked_shared_nonfinite_gate():
     assert np.array_equal(ids, rids)
     ok = np.arange(M) != 3
     assert not np.isnan(orc.bf16_to_f32(to_np(out["y"])[ok])).any()
+
+
+# ---- quantization groups below the 16-byte K step (Q4 G 64 / 32, Q8 G 32) ----------------------------------------
+@pytest.mark.parametrize("bits,G,M,A,E,H,I", [(4, 64, 16, 10, 64, 512, 256), (4, 32, 16, 10, 64, 512, 256),
+                                              (8, 32, 5, 8, 32, 512, 128), (4, 64, 300, 8, 16, 256, 128),
+                                              (4, 32, 300, 8, 16, 256, 128)])
+def test_grouped_small_groups(bits, G, M, A, E, H, I):
+    """G = 64 is the converter's default Q4 layout (strixite formats/convert_qwen4exp.hpp:37, default=q4g64). With G
+    below the load's span the K step is one group; decode (M 16: the stream kernels) and prefill sizes (M 300: the
+    exact-weight GEMM at G 64, the stream kernels at G 32): h and the FP32 down partials against the oracle."""
+    say("small groups", bits, G, M, A, E, H, I)
+    gu = moe.QWeight.synth(bits, 17, "gu_q", "gu_s", 0, E * 2 * I, H, G)
+    dn = moe.QWeight.synth(bits, 17, "dn_q", "dn_s", 0, E * H, I, G)
+    x = orc.gen_bf16_normal(orc.tensor_key(17, "x"), 1.0, (M, H))
+    ids = np.stack([np.random.default_rng(300 + m).permutation(E)[:A] for m in range(M)]).astype(np.int32)
+    tid = torch.from_numpy(ids).to(DEV)
+    ws, _ = moe.moe_group_routes(tid, E)
+    h = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)
+    b, q, s, m, G_ = qspec(gu)
+    href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G_), E, ids)
+    assert G_ == G and rel_err(to_np(h), href) < 1e-2
+    coef = torch.from_numpy(np.random.default_rng(6).random((M, A)).astype(np.float32)).to(DEV)
+    pt = torch.empty((M * A, H), dtype=torch.float32, device=DEV)
+    y = moe.experts_combine_grouped(h, dn, E, tid, coef, ws, M, A, partial=pt)
+    b, q, s, m, _ = qspec(dn)
+    part = orc.experts_down(to_np(h), orc.qview(b, q, s, m, dn.N, I, G), E, ids)
+    assert rel_err(pt.cpu().numpy(), part) < 1e-4
+    yref, _ = orc.combine(part, ids, to_np(coef), E, H)
+    assert rel_err(to_np(y), yref) < 1e-2
+    if bits == 4 and M <= 16:  # the per-slot kernels: the same per-slot MFMA sequence as the grouped ones
+        err = moe.zero_err()
+        hp = moe.experts_gather(bf16(x), gu, E, tid, err, swiglu=True)
+        assert torch.equal(hp, h)
+        yp = moe.experts_combine(h, dn, E, tid, coef, err)
+        assert rel_err(to_np(yp), to_np(y)) <= 2.0 ** -8
+        assert to_np(err)[0] == 0
+
+
+@pytest.mark.parametrize("bits,G", [(4, 64), (4, 32), (8, 32)])
+def test_dense_small_groups(bits, G):
+    say("dense small groups", bits, G)
+    M, N, K = 7, 320, 1024
+    w = moe.QWeight.synth(bits, 18, "gu_q", "gu_s", 1, N, K, G)
+    x = orc.gen_bf16_normal(orc.tensor_key(18, "x"), 1.0, (M, K))
+    spec = qspec(w)
+    ref = orc.dense(x, orc.qview(*spec[:4], N, K, G))
+    f = moe.linear_q4 if bits == 4 else moe.linear_q8
+    yf = f(bf16(x), w, out_dtype=torch.float32)
+    assert rel_err(yf.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("G,shared_G,M", [(64, 64, 16), (64, 64, 600), (32, 32, 16), (32, 64, 200)])
+def test_layer_small_groups(G, shared_G, M):
+    """The whole sublayer with Q4 G 64 / 32 routed experts (a Q8 G 32 shared expert runs beside the routed launches
+    rather than riding along): routing bit-exact, output within 1e-2 of the oracle on seeded rows."""
+    say("layer small groups", G, shared_G, M)
+    H, E, k, I = 1024, 64, 8, 256
+    layer = moe.MoeLayer.synth(H, E, k, I, seed=21, routed_G=G, shared_G=shared_G)
+    x = moe.synth_bf16_normal(21, "x", M, (M, H), 1.0)
+    out = layer.forward(x)
+    torch.cuda.synchronize()
+    rows = np.arange(M) if M <= 16 else np.sort(np.random.default_rng(M).choice(M, 24, replace=False))
+    o = orc.moe_layer(oracle_weights(layer), np.ascontiguousarray(to_np(x)[rows]))
+    assert np.array_equal(to_np(out["ids"])[rows], o["ids"])
+    assert rel_err(to_np(out["y"])[rows], o["y"]) < 1e-2
+    assert not to_np(out["err"]).any()
