@@ -788,7 +788,9 @@ struct InjectArgs {
     const float *w_in;   // [M, streams]
     int64_t streams;
 };
-template <bool SH, bool RES, bool PB, bool INJ = false>
+// UNI: no wave straddles two tokens (N a multiple of 64 VEC): the token index is wave-uniform, so the per-slot ids and
+// coefficients are scalar loads instead of a broadcast vector load each (half the kernel's vector memory traffic)
+template <bool SH, bool RES, bool PB, bool INJ = false, bool UNI = false>
 __global__ void __launch_bounds__(kThreads)
     combine_reduce_kernel(const void *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                           int64_t N, uint16_t *y, const uint16_t *s, const float *gate_logit, int64_t gate_ld,
@@ -797,7 +799,7 @@ __global__ void __launch_bounds__(kThreads)
     constexpr int VEC = kCombineVec, W = VEC / 2;  // W: dwords of VEC bf16
     const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * VEC;
     if (i >= M * N) return;
-    const int64_t m = i / N, n = i % N;
+    const int64_t m = UNI ? (int64_t)__builtin_amdgcn_readfirstlane((int)(i / N)) : i / N, n = i % N;
     auto ld_bf16 = [](const uint16_t *q, uint32_t (&w)[W]) {
         if constexpr (W == 4) {
             const uint4 u = *reinterpret_cast<const uint4 *>(q);
@@ -1157,11 +1159,18 @@ void combine_reduce(const void *partial, const int32_t *ids, const float *coef, 
     const int64_t gld = sh ? sh->gate_ld : 0;
     const uint32_t gi = sh ? sh->gate_index : 0;
     uint32_t *err = sh ? sh->err : nullptr;
+    // (M N < 2^31 elements: the uniform token index fits an int)
+    const bool uni = N % (kWave * kCombineVec) == 0 && M * N < (1ll << 31);
     if (inj != nullptr) {  // the injection replaces the residual write
         auto gi_ = [&](auto shc, auto pbc) {
-            combine_reduce_kernel<decltype(shc)::value, false, decltype(pbc)::value, true>
-                <<<blocks, kThreads, 0, stream>>>(partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, nullptr,
-                                                  nullptr, s_part, s_parts, *inj);
+            if (uni)
+                combine_reduce_kernel<decltype(shc)::value, false, decltype(pbc)::value, true, true>
+                    <<<blocks, kThreads, 0, stream>>>(partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, nullptr,
+                                                      nullptr, s_part, s_parts, *inj);
+            else
+                combine_reduce_kernel<decltype(shc)::value, false, decltype(pbc)::value, true, false>
+                    <<<blocks, kThreads, 0, stream>>>(partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, nullptr,
+                                                      nullptr, s_part, s_parts, *inj);
         };
         if (sh && partial_bf16) gi_(std::true_type{}, std::true_type{});
         else if (sh) gi_(std::true_type{}, std::false_type{});
@@ -1170,12 +1179,13 @@ void combine_reduce(const void *partial, const int32_t *ids, const float *coef, 
         return;
     }
     auto go = [&](auto shc, auto resc) {
-        if (partial_bf16)
-            combine_reduce_kernel<decltype(shc)::value, decltype(resc)::value, true><<<blocks, kThreads, 0, stream>>>(
-                partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, resid, out, s_part, s_parts);
-        else
-            combine_reduce_kernel<decltype(shc)::value, decltype(resc)::value, false><<<blocks, kThreads, 0, stream>>>(
-                partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, resid, out, s_part, s_parts);
+        constexpr bool SHV = decltype(shc)::value, RV = decltype(resc)::value;
+        auto k = partial_bf16 ? (uni ? combine_reduce_kernel<SHV, RV, true, false, true>
+                                     : combine_reduce_kernel<SHV, RV, true, false, false>)
+                              : (uni ? combine_reduce_kernel<SHV, RV, false, false, true>
+                                     : combine_reduce_kernel<SHV, RV, false, false, false>);
+        k<<<blocks, kThreads, 0, stream>>>(partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, resid, out, s_part,
+                                           s_parts, InjectArgs{});
     };
     if (sh && out) go(std::true_type{}, std::true_type{});
     else if (sh) go(std::true_type{}, std::false_type{});

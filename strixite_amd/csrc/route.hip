@@ -25,67 +25,88 @@ __global__ void __launch_bounds__(1024) route_small_kernel(const int32_t *ids, L
     pack_small_body<1, false>(nullptr, 0, ids, 0, (int)L.E, 0, nullptr, nullptr, L, nbits, ws, nullptr, err, lds);
 }
 
-// ---- larger S: chunk histograms, one scan block, placement ----------------------------------------------------------
-constexpr int kWavesPerBlock = 4;
+// ---- larger S: range histograms, one scan block, placement ------------------------------------------------------------
+// A histogram block takes a range of kRangeChunks chunks, a wave each: the chunk counts meet in LDS, and the block
+// writes each chunk's position within the range and the range's bucket counts. The scan block then has only the
+// ranges' counts to read (the chunks' would be a long chain of round trips on one CU at prefill sizes); it turns
+// them into each range's first position; a chunk's cursor is its range's first position plus its position in the
+// range.
+constexpr int kRangeChunks = Layout::kRangeChunks;
 
-__global__ void __launch_bounds__(kWavesPerBlock * kWave) route_hist_kernel(const int32_t *ids, Layout L, int nbits,
-                                                                           int32_t *ws) {
-    extern __shared__ int lds[];  // [kWavesPerBlock][E + 1]
-    const int E = (int)L.E, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int64_t ch = (int64_t)blockIdx.x * kWavesPerBlock + wave;
-    if (ch >= L.nch) return;  // whole wave; no barrier in this kernel
-    int *h = lds + wave * (E + 1);
-    for (int b = lane; b <= E; b += kWave) h[b] = 0;
-    const int64_t s0 = ch * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
-    const int fb = chunk_hist(ids, s0, s1, E, nbits, h);
-    int32_t *gh = ws + L.hist() + ch * (E + 1);
-    for (int b = lane; b <= E; b += kWave) gh[b] = h[b];
-    if (lane == 0) ws[L.bad() + ch] = fb;
+__global__ void __launch_bounds__(kRangeChunks * kWave) route_hist_kernel(const int32_t *ids, Layout L, int nbits,
+                                                                          int32_t *ws) {
+    extern __shared__ int lds[];  // [kRangeChunks][E + 1]
+    const int E = (int)L.E, nb = E + 1, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int64_t r = blockIdx.x, ch0 = r * kRangeChunks;
+    for (int i = threadIdx.x; i < kRangeChunks * nb; i += blockDim.x) lds[i] = 0;
+    __syncthreads();
+    const int64_t ch = ch0 + wave;
+    if (ch < L.nch) {
+        const int64_t s0 = ch * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
+        const int fb = chunk_hist(ids, s0, s1, E, nbits, lds + wave * nb);
+        if (lane == 0) ws[L.bad() + ch] = fb;
+    }
+    __syncthreads();
+    const int nc = (int)(L.nch - ch0 < kRangeChunks ? L.nch - ch0 : kRangeChunks);
+    for (int t = threadIdx.x; t < nb; t += blockDim.x) {
+        int run = 0;
+        for (int w = 0; w < nc; ++w) {
+            ws[L.hist() + (ch0 + w) * nb + t] = run;
+            run += lds[w * nb + t];
+        }
+        ws[L.rsum() + r * nb + t] = run;
+    }
 }
 
 __global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, Layout L, int32_t *ws, uint32_t *err) {
     __shared__ int wsum[48];
     __shared__ int bad_lds;
     const int E = (int)L.E, t = threadIdx.x;
+    const int64_t R = L.nrange();
     if (t == 0) bad_lds = INT_MAX;
     __syncthreads();
     int fb = INT_MAX;
     for (int64_t c = t; c < L.nch; c += blockDim.x) fb = min(fb, ws[L.bad() + c]);
     if (fb != INT_MAX) atomicMin(&bad_lds, fb);
-    // the chunk histograms are read 16 at a time (independent loads in flight together: a round trip per 16 chunks
-    // instead of one per chunk)
+    // the ranges' counts are read 16 at a time (independent loads in flight together)
     constexpr int B = 16;
     int cnt = 0;
     if (t <= E)
-        for (int64_t c0 = 0; c0 < L.nch; c0 += B) {
+        for (int64_t r0 = 0; r0 < R; r0 += B) {
             int h[B];
 #pragma unroll
-            for (int b = 0; b < B; ++b) h[b] = c0 + b < L.nch ? ws[L.hist() + (c0 + b) * (E + 1) + t] : 0;
+            for (int b = 0; b < B; ++b) h[b] = r0 + b < R ? ws[L.rsum() + (r0 + b) * (E + 1) + t] : 0;
 #pragma unroll
             for (int b = 0; b < B; ++b) cnt += h[b];
         }
     int v[3] = {cnt, (cnt + kTileRows - 1) / kTileRows, (cnt + kWideRows - 1) / kWideRows}, tot[3];
     block_scan3(v, wsum, tot);
     if (t <= E) {
-        write_bucket(t, cnt, v, ws, L);
+        ws[L.offsets() + t] = v[0];
+        ws[L.tstart() + t] = v[1];
+        ws[L.tstart() + (E + 2) + t] = v[2];
         int run = v[0];
-        for (int64_t c0 = 0; c0 < L.nch; c0 += B) {
+        for (int64_t r0 = 0; r0 < R; r0 += B) {
             int h[B];
 #pragma unroll
-            for (int b = 0; b < B; ++b) h[b] = c0 + b < L.nch ? ws[L.hist() + (c0 + b) * (E + 1) + t] : 0;
+            for (int b = 0; b < B; ++b) h[b] = r0 + b < R ? ws[L.rsum() + (r0 + b) * (E + 1) + t] : 0;
 #pragma unroll
             for (int b = 0; b < B; ++b)
-                if (c0 + b < L.nch) {
-                    ws[L.hist() + (c0 + b) * (E + 1) + t] = run;
+                if (r0 + b < R) {
+                    ws[L.rsum() + (r0 + b) * (E + 1) + t] = run;
                     run += h[b];
                 }
         }
     }
     if (t == 0) {
         write_header(ws, L, tot);
+        ws[L.tstart() + E + 1] = tot[1];
+        ws[L.tstart() + (E + 2) + E + 1] = tot[2];
         report_bad(ids, bad_lds, err);
     }
 }
+
+constexpr int kWavesPerBlock = 4;
 
 __global__ void __launch_bounds__(kWavesPerBlock * kWave) route_place_kernel(const int32_t *ids, Layout L, int nbits,
                                                                             int32_t *ws) {
@@ -94,14 +115,50 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave) route_place_kernel(con
     const int64_t ch = (int64_t)blockIdx.x * kWavesPerBlock + wave;
     if (ch >= L.nch) return;
     int *c = lds + wave * (E + 1);
-    const int32_t *gh = ws + L.hist() + ch * (E + 1);
-    for (int b = lane; b <= E; b += kWave) c[b] = gh[b];
+    const int32_t *gh = ws + L.hist() + ch * (E + 1), *rs = ws + L.rsum() + (ch / kRangeChunks) * (E + 1);
+    for (int b = lane; b <= E; b += kWave) c[b] = gh[b] + rs[b];
     const int64_t s0 = ch * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
     chunk_place(ids, s0, s1, E, nbits, c, ws + L.slots());
 }
 
+// The tile records, after placement, a thread per (16-slot tile, entry) and per 64-slot tile: a tile's bucket is the
+// last whose first tile is at or before it (binary search over the buckets' first tiles, staged in LDS; empty buckets
+// share their successor's first tile and are passed over).
 __global__ void __launch_bounds__(256) route_tiles_kernel(Layout L, int32_t *ws) {
-    fill_tile_slots(ws, L, ws[0], (int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x);
+    extern __shared__ int tl[];  // [3][E + 2]: first 16-slot tiles, first 64-slot tiles, bucket offsets
+    const int nb = (int)L.E + 2;
+    for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+        tl[i] = ws[L.tstart() + i];
+        tl[nb + i] = ws[L.tstart() + nb + i];
+        tl[2 * nb + i] = ws[L.offsets() + i];
+    }
+    __syncthreads();
+    auto bucket_of_tile = [&](const int *st, int ti) {
+        int lo = 0, hi = nb - 1;  // st[lo] <= ti < st[hi]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) / 2;
+            if (st[mid] <= ti) lo = mid;
+            else hi = mid;
+        }
+        return lo;
+    };
+    const int n16 = tl[nb - 1], n64 = tl[2 * nb - 1];
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (int64_t)n16 * kTileRows; i += stride) {
+        const int ti = (int)(i / kTileRows), jj = (int)(i % kTileRows);
+        const int b = bucket_of_tile(tl, ti), r = ti - tl[b];
+        const int first = tl[2 * nb + b] + r * kTileRows;
+        const int rows = min(kTileRows, tl[2 * nb + b + 1] - first);
+        int32_t *rec = ws + L.t16_rec() + kRec16 * ti;
+        if (jj == 0) *reinterpret_cast<int4 *>(rec) = make_int4(b, first, rows, 0);
+        rec[4 + jj] = jj < rows ? ws[L.slots() + first + jj] : -1;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n64; i += stride) {
+        const int ti = (int)i, b = bucket_of_tile(tl + nb, ti), r = ti - tl[nb + b];
+        const int first = tl[2 * nb + b] + r * kWideRows;
+        *reinterpret_cast<int4 *>(ws + L.t64_rec() + 4 * ti) =
+            make_int4(b, first, min(kWideRows, tl[2 * nb + b + 1] - first), 0);
+    }
 }
 
 
@@ -145,11 +202,12 @@ void moe_group_routes(const int32_t *ids, int64_t M, int64_t A, int64_t E, void 
     } else {
         const unsigned blocks = (unsigned)((L.nch + kWavesPerBlock - 1) / kWavesPerBlock);
         const size_t lds = (size_t)kWavesPerBlock * (E + 1) * 4;
-        route_hist_kernel<<<blocks, kWavesPerBlock * kWave, lds, stream>>>(ids, L, nbits, w);
+        route_hist_kernel<<<(unsigned)L.nrange(), kRangeChunks * kWave, (size_t)kRangeChunks * (E + 1) * 4, stream>>>(
+            ids, L, nbits, w);
         route_scan_kernel<<<1, 1024, 0, stream>>>(ids, L, w, err);
         route_place_kernel<<<blocks, kWavesPerBlock * kWave, lds, stream>>>(ids, L, nbits, w);
         const int64_t tb = (L.T16 * kTileRows + 255) / 256;
-        route_tiles_kernel<<<(unsigned)(tb < 4096 ? tb : 4096), 256, 0, stream>>>(L, w);
+        route_tiles_kernel<<<(unsigned)(tb < 4096 ? tb : 4096), 256, (size_t)3 * (E + 2) * 4, stream>>>(L, w);
     }
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E);
 }

@@ -26,9 +26,16 @@ struct Layout {
     // expert kernel needs about a tile in independent loads; 64-slot tiles {bucket, first index, rows, 0}
     __host__ __device__ int64_t t16_rec() const { return (slots() + S + 3) / 4 * 4; }
     __host__ __device__ int64_t t64_rec() const { return t16_rec() + kRec16 * T16; }
-    __host__ __device__ int64_t hist() const { return t64_rec() + 4 * T64; }       // [nch][E + 1]
-    __host__ __device__ int64_t bad() const { return hist() + nch * (E + 1); }    // [nch]
-    __host__ __device__ int64_t ints() const { return bad() + nch; }
+    // the large-S path: chunk positions within their range of kRangeChunks chunks [nch][E + 1], the ranges' bucket
+    // counts and then their first positions [nrange][E + 1], each chunk's first invalid slot [nch]
+    __host__ __device__ int64_t hist() const { return t64_rec() + 4 * T64; }
+    __host__ __device__ int64_t rsum() const { return hist() + nch * (E + 1); }
+    __host__ __device__ int64_t bad() const { return rsum() + nrange() * (E + 1); }
+    // each bucket's first 16-slot and 64-slot tile, with the totals at E + 1: [2][E + 2]
+    __host__ __device__ int64_t tstart() const { return bad() + nch; }
+    __host__ __device__ int64_t ints() const { return tstart() + 2 * (E + 2); }
+    __host__ __device__ int64_t nrange() const { return (nch + kRangeChunks - 1) / kRangeChunks; }
+    static constexpr int kRangeChunks = 16;  // chunks a histogram block (a wave each)
 };
 
 inline Layout layout(int64_t M, int64_t A, int64_t E) {
@@ -118,29 +125,6 @@ __device__ inline void block_scan3(int (&v)[3], int *wsum /* [16][3] LDS */, int
 #pragma unroll
     for (int j = 0; j < 3; ++j) v[j] = before[j] + inc[j] - v[j];
     __syncthreads();
-}
-
-// Bucket t's offsets and tile tables, given its exclusive prefixes (slots, 16-slot tiles, 64-slot tiles).
-__device__ inline void write_bucket(int t, int cnt, const int (&pre)[3], int32_t *ws, const Layout &L) {
-    int32_t *offsets = ws + L.offsets();
-    offsets[t] = pre[0];
-    const int n16 = (cnt + kTileRows - 1) / kTileRows, n64 = (cnt + kWideRows - 1) / kWideRows;
-    for (int i = 0; i < n16; ++i)
-        *reinterpret_cast<int4 *>(ws + L.t16_rec() + kRec16 * (pre[1] + i)) =
-            make_int4(t, pre[0] + i * kTileRows, min(kTileRows, cnt - i * kTileRows), 0);
-    for (int i = 0; i < n64; ++i)
-        *reinterpret_cast<int4 *>(ws + L.t64_rec() + 4 * (pre[2] + i)) =
-            make_int4(t, pre[0] + i * kWideRows, min(kWideRows, cnt - i * kWideRows), 0);
-}
-
-// After placement: each 16-slot tile record gets its slots (-1 past its rows). Threads t, t + nthreads, ... of the
-// caller copy entries [t, n_tiles * 16).
-__device__ inline void fill_tile_slots(int32_t *ws, const Layout &L, int64_t n_tiles, int64_t t, int64_t nthreads) {
-    for (int64_t i = t; i < n_tiles * kTileRows; i += nthreads) {
-        int32_t *rec = ws + L.t16_rec() + kRec16 * (i / kTileRows);
-        const int jj = (int)(i % kTileRows);
-        rec[4 + jj] = jj < rec[2] ? ws[L.slots() + rec[1] + jj] : -1;
-    }
 }
 
 __device__ inline void write_header(int32_t *ws, const Layout &L, const int (&tot)[3]) {
