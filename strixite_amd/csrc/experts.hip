@@ -1111,13 +1111,15 @@ void check_grouped(const char *fn, const void *x, const QV &w, int64_t E, const 
 // every tile holds at least one slot, and the tables hold at most S / 16 + E + 2 of them
 int64_t grouped_tiles(int64_t M, int64_t A, int64_t E) { return std::min(M * A, M * A / 16 + E + 2); }
 
-// Prefill-size batches (at least 1024 slots and 8 a bucket on average) take the LDS-tiled GEMM: its 64-slot tiles
-// read an expert's weights a quarter as often as the 16-slot stream tiles and keep the matrix cores busy.
+// Prefill-size batches (at least 1024 slots and 16 a bucket on average) take the LDS-tiled GEMM: its 64-slot tiles
+// read an expert's weights a quarter as often as the 16-slot stream tiles and keep the matrix cores busy. Below 16
+// slots an expert the GEMM's tiles are mostly empty and the weight stream sets the time; the stream kernels keep
+// more bytes in flight (MI355X, 512 tokens x top-10 over 512 experts: 455 us a layer against 538).
 // the reference's F16 matrix-unit kinds (x and the dequantized Q4 weights in F16) against the exact-weight ones
 bool f16_math(MoeMath m) { return m >= MoeMath::WmmaF16; }
 
 bool use_expert_gemm(int64_t S, int64_t E, int64_t K, int64_t G) {
-    return S >= 1024 && S >= 8 * E && K % gemm::BK == 0 && G % gemm::BK == 0 && K / G <= gemm::kMaxGroups;
+    return S >= 1024 && S >= 16 * E && K % gemm::BK == 0 && G % gemm::BK == 0 && K / G <= gemm::kMaxGroups;
 }
 
 template <typename V>

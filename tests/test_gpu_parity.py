@@ -161,8 +161,8 @@ def _bf16_partials(pt: torch.Tensor) -> np.ndarray:
 
 
 def _expert_gemm_size(S, E):
-    """The grouped projections' GEMM kernels take over at S >= 1024 slots and >= 8 slots an expert."""
-    return S >= 1024 and S >= 8 * E
+    """The grouped projections' GEMM kernels take over at S >= 1024 slots and >= 16 slots an expert."""
+    return S >= 1024 and S >= 16 * E
 
 
 @pytest.mark.parametrize("bits,M,A,E,H,I", [(4, 16, 10, 64, 512, 256), (8, 1, 8, 64, 512, 128),
