@@ -1385,8 +1385,20 @@ void dense_projection(const char *fn, const QV &v, const void *x, void *y, int64
     STRIX_CHECK(disjoint(y, M * v.N * oes, x, M * v.K * 2), fn, ": y overlaps x");
     GemmArgs a = make_args(v, 1, x, y, v.N);
     a.M = M;
-    if (out_act == Act::F32) launch_bits<DENSE, EPI_F32, false, false, false>(v.bits, a, (M + 15) / 16, stream);
-    else launch_bits<DENSE, EPI_BF16, false, false, false>(v.bits, a, (M + 15) / 16, stream);
+    // prefill-size batches on the matrix-core GEMM (exact weights, 64-token tiles), decode sizes on the stream kernel
+    if (M >= 128 && v.K % gemm::BK == 0 && v.G % gemm::BK == 0 && v.K / v.G <= gemm::kMaxGroups) {
+        auto go = [&](auto bits) {
+            constexpr int B = decltype(bits)::value;
+            if (out_act == Act::F32) launch_expert_gemm<B, DENSE, EPI_F32, false, false>(a, stream);
+            else launch_expert_gemm<B, DENSE, EPI_BF16, false, false>(a, stream);
+        };
+        if (v.bits == 4) go(std::integral_constant<int, 4>{});
+        else go(std::integral_constant<int, 8>{});
+    } else if (out_act == Act::F32) {
+        launch_bits<DENSE, EPI_F32, false, false, false>(v.bits, a, (M + 15) / 16, stream);
+    } else {
+        launch_bits<DENSE, EPI_BF16, false, false, false>(v.bits, a, (M + 15) / 16, stream);
+    }
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " N=", v.N, " K=", v.K, " G=", v.G);
 }
 }  // namespace

@@ -378,7 +378,7 @@ def test_linear_q8_and_swiglu():
     assert np.abs(to_np(h).astype(np.int32) - href.astype(np.int32)).max() <= 1  # expf ulps
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 1024, 3072), (16, 3072, 512), (37, 160, 1024)])
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 3072), (16, 3072, 512), (37, 160, 1024), (300, 1024, 3072)])
 def test_linear_q4_dense(M, N, K):
     """The dense Q4 projection (strixite kernels/linear_q4.hpp:23-31) against the oracle's dequantize-then-dot, FP32
     and BF16 outputs."""
@@ -715,10 +715,12 @@ def test_grouped_small_groups(bits, G, M, A, E, H, I):
         assert to_np(err)[0] == 0
 
 
-@pytest.mark.parametrize("bits,G", [(4, 64), (4, 32), (8, 32)])
-def test_dense_small_groups(bits, G):
-    say("dense small groups", bits, G)
-    M, N, K = 7, 320, 1024
+@pytest.mark.parametrize("bits,G,M", [(4, 64, 7), (4, 32, 7), (8, 32, 7), (4, 64, 200), (8, 64, 200), (8, 32, 200)])
+def test_dense_small_groups(bits, G, M):
+    """Decode sizes on the stream kernels, prefill sizes (M >= 128) on the matrix-core GEMM (G 64 / 128) or the stream
+    kernels (G 32)."""
+    say("dense small groups", bits, G, M)
+    N, K = 320, 1024
     w = moe.QWeight.synth(bits, 18, "gu_q", "gu_s", 1, N, K, G)
     x = orc.gen_bf16_normal(orc.tensor_key(18, "x"), 1.0, (M, K))
     spec = qspec(w)
