@@ -44,3 +44,23 @@ def zipf_bias(seed: int, E: int, beta: float, s: float = 1.1) -> np.ndarray:
     rng = np.random.default_rng(orc.tensor_key(seed, "zipf") & 0xFFFFFFFF)
     rank = rng.permutation(E) + 1
     return (-beta * s * np.log(rank.astype(np.float64))).astype(np.float32)
+
+
+# The configs' shared Q8 expert (codes uniform in [-127, 127]) outweighs the routed Q4 experts ~16x per projection,
+# so its term in y is ~10^3x the routed sum's and a bf16 y cannot resolve the routed experts. Layer tests therefore
+# also run each layer with the shared expert's scales and mins times SHARED_BALANCE (exact on bf16 bits), which
+# brings the two terms to the same size (tests/test_mutations.py shows a routed bug that only this pass catches).
+SHARED_BALANCE = 2.0 ** -4
+
+
+def balanced(layer: moe.MoeLayer) -> moe.MoeLayer:
+    """The same layer (same routed weights, router and bias tensors) with the separate shared expert's scales and
+    mins scaled by SHARED_BALANCE."""
+    assert layer.shared_gate_up is not None, "balanced(): a layer with a separate shared expert"
+
+    def sc(w: moe.QWeight) -> moe.QWeight:
+        f = lambda t: (t.view(torch.bfloat16) * SHARED_BALANCE).view(torch.int16)  # noqa: E731
+        return moe.QWeight(w.bits, w.q, f(w.scale), f(w.minv), w.N, w.K, w.G)
+
+    return moe.MoeLayer(layer.H, layer.E, layer.k, layer.I, layer.router, layer.gate_up, layer.down,
+                        layer.router_bias, sc(layer.shared_gate_up), sc(layer.shared_down))

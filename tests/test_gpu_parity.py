@@ -14,7 +14,7 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 import oracle as orc  # noqa: E402
-from gpu_util import oracle_weights, qspec, rel_err, to_np, zipf_bias  # noqa: E402
+from gpu_util import balanced, oracle_weights, qspec, rel_err, to_np, zipf_bias  # noqa: E402
 from strixite_amd import moe  # noqa: E402
 
 DEV = "cuda"
@@ -441,6 +441,14 @@ def _layer_parity(layer, M, seed, logits_in=None, sample=None):
     assert e < 1e-2, e
     assert rel_err(to_np(out["x_out"])[rows], o["out"]) < 1e-2
     assert to_np(out["err"])[0] == 0 and to_np(out["err"])[3] == 0
+    if layer.shared_gate_up is not None:  # the routed experts made visible in y
+        lb = balanced(layer)
+        ob = lb.forward(x, logits_in=logits_in)
+        torch.cuda.synchronize()
+        rb = orc.moe_layer(oracle_weights(lb), np.ascontiguousarray(xn[rows]), logits_in=lg)
+        assert np.array_equal(to_np(ob["ids"])[rows], rb["ids"])
+        eb = rel_err(to_np(ob["y"])[rows], rb["y"])
+        assert eb < 1e-2, ("balanced shared expert", eb)
     return out, o, e
 
 
@@ -600,6 +608,16 @@ def test_layer_config5_stack_decode_then_prefill():
             assert rel_err(to_np(outs[l]["y"])[rows], o["y"]) < 1e-2, (M, l)
             assert rel_err(to_np(outs[l]["x_out"])[rows], o["out"]) < 1e-2, (M, l)
             assert to_np(outs[l]["err"])[0] == 0 and to_np(outs[l]["err"])[3] == 0
+    # the routed experts made visible in y: the first layer again, balanced, at both sizes
+    for M in (16, 4096):
+        lb = balanced(layers[0])
+        x = steps[M][0][0]
+        ob = lb.forward(x, ctx=ctx)
+        torch.cuda.synchronize()
+        rows = np.arange(M) if M <= 16 else np.sort(np.random.default_rng(7).choice(M, 32, replace=False))
+        rb = orc.moe_layer(oracle_weights(lb), np.ascontiguousarray(to_np(x)[rows]))
+        assert np.array_equal(to_np(ob["ids"])[rows], rb["ids"])
+        assert rel_err(to_np(ob["y"])[rows], rb["y"]) < 1e-2, ("balanced", M)
 
 
 @pytest.mark.parametrize("M", [16, 600])
