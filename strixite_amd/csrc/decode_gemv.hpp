@@ -23,6 +23,7 @@
 // over one quantization group, acc += s * D + (m - 128 s) * sum(x over the group) on the FP32 accumulator.
 #pragma once
 
+constexpr int kDecMaxTilesL = 1024;  // tile records a decode launch holds in LDS (M <= 16 tokens x A <= 64 slots)
 namespace dec {
 constexpr int kSpan = 128;         // Q4 codes of a row per K step: 4 lane groups x 32 (one quantization group)
 constexpr int kMaxTokens = 16;     // the MFMA's A rows
@@ -373,6 +374,235 @@ __global__ void __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per
     wait_vmcnt<0>();  // no load still landing when the wave ends
 }
 
+// ---- gate_up + SwiGLU through per-wave LDS rings ---------------------------------------------------------------------
+// The units, ranges and arithmetic of decode_gate_up_kernel; the weights reach the matrix cores through LDS, so the
+// HBM side reads whole 128-byte lines. A load of the register-fed kernel covers 16 rows x 64 bytes (the MFMA's B
+// layout: every 128-byte line requested in two halves), which streams at ~4 TB/s on MI355X; here a load covers
+// 8 rows x 128 bytes and the block's waves together read whole rows.
+// W = K / 256 waves a block (12 at K = 3072), one block a CU; wave w owns quantization groups 2 w, 2 w + 1 (bytes
+// 128 w .. 128 w + 127 of every row) of every unit. A stage is one 16-row tile of a unit (the gate tile, then the up
+// tile): the wave's 2 KB of it go by two direct-to-LDS loads into the wave's own ring of kGuStages buffers, so a wave
+// waits only for its own loads and streams independently of the others; the block meets once a unit, when the waves'
+// K parts are summed in LDS. With a unit's gate tile the wave also loads, into the same ring position, the dwords of
+// the unit's scales and mins it needs (rows 0..31, groups 2 w, 2 w + 1). Nothing is loaded into registers inside the
+// loop (a register still being loaded at the loop's back edge makes the compiler wait for every load in flight
+// there), and the streaming waves store nothing (loads and stores may complete out of order, so a store among the
+// loads would make a count of outstanding operations name no particular load): one more wave, the finisher, meets the
+// block at every unit's end and turns the unit's K parts into h (SwiGLU, the stores), while the streaming waves go
+// on with the next unit. The slots of the tiles the block's units lie in are read into LDS once, before the loop.
+// LDS layout of a code stage: [2 loads][lane] 16 bytes, lane l holding row 8 load + l / 8's 16-byte chunk
+// p = c ^ (row % 8) ^ (row / 8) at position l % 8: a read of chunk c of the 16 rows then hits 16 different 16-byte
+// bank groups.
+namespace gul {
+constexpr int kGuStages = 4;     // per-wave code ring (even: a position holds gate tiles or up tiles only)
+constexpr int kGuMaxWaves = 12;  // K <= 3072 (LDS: rings, two unit reductions, the tile tables)
+constexpr int kGuMaxBlockTiles = 32;  // tiles a block's unit range may touch (their slots live in LDS)
+}  // namespace gul
+
+template <int W, int SH>
+__global__ void __launch_bounds__((W + 1) * kWave) decode_gate_up_lds_kernel(DecodeArgs a, SharedJob sh) {
+    constexpr int NS = gul::kGuStages, G = 2 * W;
+    static_assert(W >= 1 && W <= gul::kGuMaxWaves, "K = 256 W");
+    // one array per ring position, picked at compile time, so the compiler tells a read of one position from the
+    // loads still landing in the others
+    // (a position: two code loads of 1 KB; the gate positions 0 and 2 then hold 96 dwords: the scales of rows 0..31
+    // of the unit (gate rows, then up rows), 32 unused, the mins of rows 0..31)
+    constexpr int PU4 = 2 * kWave + 24;
+    __shared__ __attribute__((aligned(16))) uint4 rg0[W][PU4], rg1[W][2 * kWave], rg2[W][PU4], rg3[W][2 * kWave];
+    __shared__ float4v red[2][W][2][kWave];
+    __shared__ int32_t tb[kDecMaxTilesL];
+    __shared__ int32_t tslot[gul::kGuMaxBlockTiles][16];
+    int bid = (int)blockIdx.x, nblk = (int)gridDim.x;
+    if constexpr (SH == 1) {
+        if (bid < sh.blocks) {  // the shared expert's gate_up finish: h = bf16(silu(sum g) * sum u), a thread each
+            const int64_t i = (int64_t)bid * blockDim.x + threadIdx.x;
+            if (i < sh.units) sh.out[i] = f32_to_bf16(parts_sum<true>(sh.pin, sh.parts, sh.a.M, sh.a.N, i));
+            return;
+        }
+        bid -= sh.blocks, nblk -= sh.blocks;
+    }
+    const int tid = threadIdx.x, lane = tid % kWave, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int g = lane / 16, j = lane % 16;
+    const int nthr = (W + 1) * kWave;
+    auto ring = [&](auto P) -> uint4 * {
+        constexpr int p = decltype(P)::value;
+        if constexpr (p == 0) return rg0[wave];
+        else if constexpr (p == 1) return rg1[wave];
+        else if constexpr (p == 2) return rg2[wave];
+        else return rg3[wave];
+    };
+    const int64_t n_tiles = a.ws[0] < a.tiles_bound ? a.ws[0] : a.tiles_bound;
+    const int64_t rec0 = route::t16_rec_at(a.S, a.E);
+    const int32_t upt = (int32_t)(a.N / 32);
+    int64_t u0, u1;
+    if (!dec_range(n_tiles * upt, bid, nblk, u0, u1)) return;  // uniform per block, before any barrier
+    const __amdgpu_buffer_rsrc_t rq = rsrc(a.q, a.q_bytes), rs = rsrc(a.scale, a.s_bytes),
+                                 rm = rsrc(a.minv, a.s_bytes), rx = rsrc(a.x, a.x_bytes), ry = rsrc(a.y, a.y_bytes);
+    constexpr uint32_t rowb = 128 * W;  // code bytes a row
+    const uint32_t ldh = (uint32_t)(a.N / 2);
+    // this lane's code load pieces: load i covers rows 8 i .. 8 i + 7, lane l row 8 i + l / 8, chunk
+    // (l % 8) ^ (row % 8) ^ (row / 8) of the wave's 128 bytes
+    uint32_t loff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = 8 * i + lane / 8;
+        loff[i] = (uint32_t)r * rowb + 128u * (uint32_t)wave + (uint32_t)((((lane % 8) ^ (r % 8) ^ (r / 8))) * 16);
+    }
+    const int32_t U0 = (int32_t)u0, U1 = (int32_t)u1;
+    const int32_t T0 = U0 / upt;  // the block's first tile (the launcher checks that its tiles fit tslot)
+
+    // this wave's activations: groups 2 w, 2 w + 1 of all M <= 16 tokens (rows past M read zeros)
+    uint4 xr[2][4];
+    {
+        const uint32_t xo = j < a.M ? ((uint32_t)j * (uint32_t)a.K + 32u * g) * 2 : a.x_bytes;
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) xr[k][v] = bld16(rx, xo, (uint32_t)((2 * wave + k) * dec::kSpan + 8 * v) * 2);
+    }
+    for (int64_t t = tid; t < n_tiles; t += nthr) tb[t] = a.ws[rec0 + route::kRec16 * t];
+    const int32_t nbt = (U1 - 1) / upt - T0 + 1;  // tiles the block's units touch
+    for (int i = tid; i < nbt * 16; i += nthr) tslot[i / 16][i % 16] = a.ws[rec0 + route::kRec16 * (T0 + i / 16) + 4 + i % 16];
+    __syncthreads();  // the buckets and slots (and the activations)
+    const int32_t nq = (U1 - U0) * 2;                // stages of the block
+    const int32_t nq_pad = (nq + NS - 1) / NS * NS;  // in whole ring trips: the stages past nq load nothing
+
+    const uint32_t A32 = (uint32_t)a.A;
+    if (wave == W) {  // the finisher: after each unit's end (one barrier, as the streaming waves meet there), its h
+        for (int32_t u = U0; u < U0 + nq_pad / 2; ++u) {
+            lds_barrier();
+            if (u >= U1) continue;
+            const int par = (u - U0) & 1;
+            const int32_t t = u / upt, c = u % upt;
+            const int32_t bucket = tb[t];
+            const bool nan = bucket < 0 || bucket >= a.E;
+            // lane (rs, j): tile rows 4 pass + rs, column j (a row with slot -1, past the record's rows, is skipped)
+            for (int k0 = 0; k0 < 16; k0 += 4) {
+                const int32_t sl = tslot[t - T0][k0 + g];
+                if (__builtin_amdgcn_readfirstlane(tslot[t - T0][k0]) < 0) break;
+                if (sl < 0) continue;
+                const uint32_t tok = (uint32_t)sl / A32, i = tok % 4;
+                const int src = (int)(tok / 4) * 16 + j;
+                float gv = 0.f, uv = 0.f;
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    gv += reinterpret_cast<const float *>(&red[par][w][0][src])[i];
+                    uv += reinterpret_cast<const float *>(&red[par][w][1][src])[i];
+                }
+                const float v = nan ? qnan() : silu(gv) * uv;
+                __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), ry, ((uint32_t)sl * ldh + 16u * (uint32_t)c + j) * 2,
+                                                      0, 0);
+            }
+        }
+        return;
+    }
+
+    // stage q = unit u0 + q / 2, its gate tile (even q) or up tile (odd q), at ring position P = q mod NS: two code
+    // loads and, for a gate tile, the unit's scale and min dwords (groups 2 w, 2 w + 1 of its 32 rows), all to LDS;
+    // past u1: offsets past the ends
+    auto issue = [&](int32_t q, auto P) __attribute__((always_inline)) {
+        uint4 *R = ring(P);
+        constexpr int half = decltype(P)::value % 2;
+        const int32_t u = U0 + q / 2;
+        const bool valid = u < U1;
+        const int32_t t = valid ? u / upt : 0, c = valid ? u % upt : 0;
+        const int32_t bucket = tb[t];
+        const uint32_t expert = bucket < 0 || bucket >= a.E ? 0u : (uint32_t)bucket;
+        const uint32_t row0 = expert * (uint32_t)a.N + (half ? ldh : 0u) + 16u * (uint32_t)c;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) lds_load16(rq, R + i * kWave, valid ? row0 * rowb + loff[i] : a.q_bytes, 0);
+        if constexpr (half == 0) {
+            // unit row r = l % 32 of lane l; the scale load's lanes 32..63 and the min load's lanes 0..31 read past
+            // the end and write zeros, both into dwords 32..63 (the min load lands 32 dwords on): no branch, so each
+            // load keeps its own (uniform) resource
+            const int r = lane % 32;
+            const uint32_t so = ((row0 + (r >= 16 ? ldh : 0u) + (uint32_t)(r % 16)) * G + 2u * (uint32_t)wave) * 2;
+            uint32_t *dst = reinterpret_cast<uint32_t *>(R + 2 * kWave);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 4,
+                                                     valid && lane < 32 ? so : a.s_bytes, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (__attribute__((address_space(3))) void *)(dst + 32), 4,
+                                                     valid && lane >= 32 ? so : a.s_bytes, 0, 0, 0);
+        }
+    };
+    issue(0, std::integral_constant<int, 0>{});
+    issue(1, std::integral_constant<int, 1>{});
+    issue(2, std::integral_constant<int, 2>{});
+
+    // the fragments in the paired order, and per group the token sums (lane (g, j): tokens 4 g + i) from an MFMA
+    // against ones
+    Frag xf[2][4];
+    float xs[2][4];
+    {
+        const Frag ones{{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}};
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            float4v d = {0, 0, 0, 0};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                xf[k][v] = bf16_natural_to_paired(xr[k][v]);
+                d = mfma_bf16(Frag{{xr[k][v].x, xr[k][v].y, xr[k][v].z, xr[k][v].w}}, ones, d);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xs[k][i] = d[i];
+        }
+    }
+
+    float4v acc[2] = {float4v{0, 0, 0, 0}, float4v{0, 0, 0, 0}};
+    uint32_t smd[4] = {0, 0, 0, 0};  // the current unit's scale / min dwords of row j: gate s, gate m, up s, up m
+    // stage q at ring position P: wait for this wave's loads of it, refill the previous position (its reads returned
+    // before the previous stage's MFMAs) with stage q + NS - 1, consume stage q; a unit's end writes the wave's K part
+    // and meets the block (and the finisher)
+    auto step = [&](int32_t q, auto P) __attribute__((always_inline)) {
+        constexpr int p = decltype(P)::value, half = p % 2;
+        // loads issued after stage q's (at step q - 3): those of stages q + 1 and q + 2 (a gate stage: 4, an up: 2)
+        wait_vmcnt<6>();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (half == 0) {  // read before the up step refills this position
+            const uint32_t *sp = reinterpret_cast<const uint32_t *>(ring(P) + 2 * kWave);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) smd[i] = sp[(i % 2) * 64 + (i / 2) * 16 + j];
+        }
+        issue(q + NS - 1, std::integral_constant<int, (p + NS - 1) % NS>{});
+        const uint4 *R = ring(P);
+        float4v dd[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int c = 4 * k + g;  // lane group g's 16-byte chunk of group 2 w + k
+            // a native vector load (a uint4 struct copy would become a memcpy that loses the LDS alias scopes, and
+            // the compiler would then wait for every ring position's loads before this read)
+            const u32x4v v =
+                *reinterpret_cast<const u32x4v *>(R + (j / 8) * kWave + 8 * (j % 8) + (c ^ (j % 8) ^ (j / 8)));
+            dd[k] = float4v{0, 0, 0, 0};
+            const uint32_t qw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) dd[k] = mfma_bf16(xf[k][w], q4_paired_to_bf16(qw[w]), dd[k]);
+        }
+        const uint32_t sd = smd[2 * half], md = smd[2 * half + 1];  // this tile's
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float sc = __uint_as_float(k == 0 ? sd << 16 : sd & 0xFFFF0000u);
+            const float mn = fmaf(-128.0f, sc, __uint_as_float(k == 0 ? md << 16 : md & 0xFFFF0000u));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[half][i] = fmaf(sc, dd[k][i], fmaf(mn, xs[k][i], acc[half][i]));
+        }
+        if constexpr (half == 1) {  // unit end: this wave's K part to red[parity], meet
+            const int par = (q / 2) & 1;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) red[par][wave][t][lane] = acc[t];
+            acc[0] = acc[1] = float4v{0, 0, 0, 0};
+            lds_barrier();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int32_t q = 0; q < nq_pad; q += NS) {  // whole trips: no branch between the steps
+        step(q + 0, std::integral_constant<int, 0>{});
+        step(q + 1, std::integral_constant<int, 1>{});
+        step(q + 2, std::integral_constant<int, 2>{});
+        step(q + 3, std::integral_constant<int, 3>{});
+    }
+    wait_vmcnt<0>();  // no load still landing in LDS when the wave ends
+}
+
 // ---- down -------------------------------------------------------------------------------------------------------------
 // A unit: 32 rows (two 16-row tiles) of one expert over K = 512 (four steps). A operand: the tile's h rows (lane (g, i):
 // slot i's 8 values at k = 128 step + 32 g + 8 u), reloaded when the unit's tile changes; their per-group sums come from
@@ -485,6 +715,14 @@ inline DecodeArgs decode_args(const GemmArgs &ga, int64_t M, bool swiglu) {
     return d;
 }
 
+template <int W>
+void launch_decode_gate_up_lds(const DecodeArgs &d, SharedJob s, hipStream_t stream) {
+    s.blocks = s.units > 0 ? (int)((s.units + (W + 1) * kWave - 1) / ((W + 1) * kWave)) : 0;
+    const unsigned blocks = (unsigned)(device_cus() + s.blocks);
+    if (s.blocks > 0) decode_gate_up_lds_kernel<W, 1><<<blocks, (W + 1) * kWave, 0, stream>>>(d, s);
+    else decode_gate_up_lds_kernel<W, 0><<<blocks, (W + 1) * kWave, 0, stream>>>(d, s);
+}
+
 template <int SPW>
 void launch_decode_gate_up_spw(const DecodeArgs &d, const SharedJob &s, hipStream_t stream) {
     constexpr int W = kDecGuWaves, R = kDecGuAhead;
@@ -507,6 +745,19 @@ inline void launch_decode_gate_up(const GemmArgs &ga, int64_t M, const SharedJob
     const DecodeArgs d = decode_args(ga, M, true);
     SharedJob s = sh ? *sh : SharedJob{};
     s.blocks = sh ? (int)((s.units + kDecGuWaves * kWave - 1) / (kDecGuWaves * kWave)) : 0;
+    // the LDS-ring kernel: W = K / 256 waves; a block's unit range (at most ceil(units / CUs) units) must touch at most
+    // kGuMaxBlockTiles tiles
+    const int64_t upt = ga.N / 32, most_units = (d.tiles_bound * upt + device_cus() - 1) / device_cus();
+    if (ga.K % 256 == 0 && (ga.K / 256 == 8 || ga.K / 256 == 12) &&
+        (most_units + upt - 1) / upt + 1 <= gul::kGuMaxBlockTiles && !getenv("STRIX_OLD_GU")) {
+        SharedJob t = s;
+        t.units = sh ? s.units : 0;
+        switch (ga.K / 256) {
+            case 8: return launch_decode_gate_up_lds<8>(d, t, stream);
+            case 12: return launch_decode_gate_up_lds<12>(d, t, stream);
+            default: break;
+        }
+    }
     switch (ga.K / dec::kSpan / kDecGuWaves) {
         case 2: launch_decode_gate_up_spw<2>(d, s, stream); break;
         case 3: launch_decode_gate_up_spw<3>(d, s, stream); break;
