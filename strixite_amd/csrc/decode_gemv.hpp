@@ -685,6 +685,169 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     }
 }
 
+// ---- down through per-wave LDS rings ---------------------------------------------------------------------------------
+// K = 512 (Q4 g128: 256 bytes a row, four groups). A unit is 16 consecutive weight rows of one expert (4 KB,
+// contiguous) against one 16-slot tile; the tile's h rows are the MFMA's A operand for all of its units, held in
+// registers. Waves are dealt to tiles, not to a flat unit range: every tile gets floor or ceil(waves / tiles) waves,
+// each a contiguous range of the tile's N / 16 row blocks, so a wave loads its tile's h rows once, before its loop,
+// and streams one contiguous region of the expert's rows. A unit's codes reach LDS by four direct loads of 4 rows x
+// 256 bytes (1 KB contiguous each), with its rows' scale and min dwords, into the wave's own ring of kDnStages
+// positions; no barrier, no K split. The FP32 partials are stored as each unit ends: the waits count loads only (a
+// store may complete before older loads, so counting it could release a wait early; not counting it only makes a wait
+// stricter).
+// LDS layout of a position (uint4): codes [4 loads][lane], lane l holding row 4 load + l / 16's 16-byte chunk
+// (l % 16) ^ row at position l % 16 (the MFMA-layout reads of one chunk of the 16 rows hit 16 bank groups); then
+// 32 dwords of scales (row r: dword 2 r + group / 2) and 32 of mins.
+namespace gdn {
+constexpr int kDnStages = 4, kDnWaves = 4;  // per-wave ring; waves a block (two blocks a CU)
+constexpr int kPosU4 = 4 * kWave + 16;      // codes + 64 dwords of scales and mins
+}  // namespace gdn
+
+template <int SH>
+__global__ void __launch_bounds__(gdn::kDnWaves * kWave) decode_down_lds_kernel(DecodeArgs a, SharedJob sh) {
+    constexpr int NS = gdn::kDnStages, WB = gdn::kDnWaves, KS = kDecDownSteps;  // KS: groups a row (K = 512)
+    int bid = (int)blockIdx.x, nblk = (int)gridDim.x;
+    if constexpr (SH == 2) {
+        if (bid < sh.blocks) {  // the shared expert's down, split-K parts
+            const int64_t w = (int64_t)bid * (blockDim.x / kWave) + threadIdx.x / kWave;
+            if (w < sh.units) dense_part_unit<8>(sh.a, sh.spp, sh.parts, sh.pout, w);
+            return;
+        }
+        bid -= sh.blocks, nblk -= sh.blocks;
+    }
+    __shared__ __attribute__((aligned(16))) uint4 rp0[WB][gdn::kPosU4], rp1[WB][gdn::kPosU4], rp2[WB][gdn::kPosU4],
+        rp3[WB][gdn::kPosU4];
+    const int lane = threadIdx.x % kWave, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int g = lane / 16, j = lane % 16;
+    auto ring = [&](auto P) -> uint4 * {
+        constexpr int p = decltype(P)::value;
+        if constexpr (p == 0) return rp0[wave];
+        else if constexpr (p == 1) return rp1[wave];
+        else if constexpr (p == 2) return rp2[wave];
+        else return rp3[wave];
+    };
+    const int64_t n_tiles = a.ws[0] < a.tiles_bound ? a.ws[0] : a.tiles_bound;
+    if (n_tiles <= 0) return;
+    // this wave's tile and row-block range: tiles 0 .. extra - 1 get base + 1 waves, the rest base
+    const int32_t nw = nblk * WB, gw = bid * WB + wave, nt = (int32_t)n_tiles;
+    const int32_t base = nw / nt, extra = nw % nt;
+    if (base == 0) return;  // more tiles than waves: the launcher does not allow it
+    int32_t t, r, k;
+    if (gw < extra * (base + 1)) t = gw / (base + 1), r = gw % (base + 1), k = base + 1;
+    else t = extra + (gw - extra * (base + 1)) / base, r = (gw - extra * (base + 1)) % base, k = base;
+    const int32_t rbs = (int32_t)(a.N / 16);  // row blocks of an expert
+    const int32_t rb0 = r * rbs / k, rb1 = (r + 1) * rbs / k;
+    if (rb1 <= rb0) return;
+    const __amdgpu_buffer_rsrc_t rq = rsrc(a.q, a.q_bytes), rs = rsrc(a.scale, a.s_bytes),
+                                 rm = rsrc(a.minv, a.s_bytes), rx = rsrc(a.x, a.x_bytes), ry = rsrc(a.y, a.y_bytes);
+    const int64_t rec0 = route::t16_rec_at(a.S, a.E);
+    const int32_t bucket = __builtin_amdgcn_readfirstlane(a.ws[rec0 + route::kRec16 * t]);
+    const bool nan = bucket < 0 || bucket >= a.E;
+    const uint32_t expert = nan ? 0u : (uint32_t)bucket;
+    const int32_t slot_l = a.ws[rec0 + route::kRec16 * t + 4 + j];  // lane j: the tile's slot j (-1 past its rows)
+    // the tile's h rows (lane (g, i): slot i's 8 values at k = 128 s + 32 g + 8 v), loaded before the ring
+    uint4 hr[KS][4];
+    {
+        const uint32_t xo = slot_l >= 0 ? ((uint32_t)slot_l * (uint32_t)a.K + 32u * g) * 2 : a.x_bytes;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) hr[s][v] = bld16(rx, xo, (uint32_t)(s * dec::kSpan + 8 * v) * 2);
+    }
+    // this lane's code load pieces: load i covers rows 4 i .. 4 i + 3: lane l row 4 i + l / 16, chunk (l % 16) ^ row
+    uint32_t loff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int rr = 4 * i + lane / 16;
+        loff[i] = (uint32_t)rr * 256u + (uint32_t)(((lane % 16) ^ rr) * 16);
+    }
+    const uint32_t row_e = expert * (uint32_t)a.N;  // the expert's first row
+    // unit rb0 + q into position P: four code loads and (lanes 0..31) the 16 rows' scale and min dwords; past rb1:
+    // offsets past the ends
+    auto issue = [&](int32_t q, auto P) __attribute__((always_inline)) {
+        uint4 *R = ring(P);
+        const int32_t rb = rb0 + q;
+        const bool valid = rb < rb1;
+        const uint32_t row0 = row_e + 16u * (uint32_t)rb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds_load16(rq, R + i * kWave, valid ? row0 * 256u + loff[i] : a.q_bytes, 0);
+        if (lane < 32) {  // dword l of the rows' scales (16 rows x 4 bf16 = 32 dwords), then of the mins
+            const uint32_t so = valid ? row0 * (uint32_t)(KS * 2) + 4u * (uint32_t)lane : a.s_bytes;
+            uint32_t *dst = reinterpret_cast<uint32_t *>(R + 4 * kWave);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 4, so, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (__attribute__((address_space(3))) void *)(dst + 32), 4, so, 0,
+                                                     0, 0);
+        }
+    };
+    const int32_t nq = rb1 - rb0, nq_pad = (nq + NS - 1) / NS * NS;
+    issue(0, std::integral_constant<int, 0>{});
+    issue(1, std::integral_constant<int, 1>{});
+    issue(2, std::integral_constant<int, 2>{});
+    // A fragments and the per-group sums of the tile rows (lane (g, j): slots 4 g + i) from an MFMA against ones
+    Frag hf[KS][4];
+    float hs[KS][4];
+    {
+        const Frag ones{{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            float4v d = {0, 0, 0, 0};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                hf[s][v] = Frag{{hr[s][v].x, hr[s][v].y, hr[s][v].z, hr[s][v].w}};
+                d = mfma_bf16(hf[s][v], ones, d);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hs[s][i] = d[i];
+        }
+    }
+    // output rows of this lane's D values: slots 4 g + i (byte offsets of partial[slot][0], or past the end)
+    uint32_t orow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int32_t sl = __shfl(slot_l, 4 * g + i, kWave);
+        orow[i] = sl >= 0 ? (uint32_t)sl * (uint32_t)a.N * 4u : a.y_bytes;
+    }
+    auto step = [&](int32_t q, auto P) __attribute__((always_inline)) {
+        constexpr int p = decltype(P)::value;
+        wait_vmcnt<6 * (NS - 2)>();  // loads issued after unit q's: units q + 1 .. q + NS - 2, six each
+        __builtin_amdgcn_sched_barrier(0);
+        issue(q + NS - 1, std::integral_constant<int, (p + NS - 1) % NS>{});
+        const uint4 *R = ring(P);
+        const uint32_t *scl = reinterpret_cast<const uint32_t *>(R + 4 * kWave);
+        float4v acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const int c = 4 * s + g;  // lane group g's 16-byte chunk of group s
+            // a native vector load (a uint4 struct copy would become a memcpy that loses the LDS alias scopes)
+            const u32x4v v = *reinterpret_cast<const u32x4v *>(R + (j / 4) * kWave + 16 * (j % 4) + (c ^ j));
+            const uint32_t sw = scl[2 * j + s / 2], mw = scl[32 + 2 * j + s / 2];
+            const float sc = __uint_as_float(s % 2 == 0 ? sw << 16 : sw & 0xFFFF0000u);
+            const float mn = fmaf(-128.0f, sc, __uint_as_float(s % 2 == 0 ? mw << 16 : mw & 0xFFFF0000u));
+            float4v d = {0, 0, 0, 0};
+            const uint32_t qw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) d = mfma_bf16(hf[s][w], q4_codes_to_bf16(qw[w]), d);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = fmaf(sc, d[i], fmaf(mn, hs[s][i], acc[i]));
+        }
+        // partial[slot 4 g + i][16 rb + j] (a unit past rb1 or a slot -1: past the end, nothing written)
+        const int32_t rb = rb0 + q;
+        const uint32_t col = (16u * (uint32_t)rb + (uint32_t)j) * 4u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(nan ? qnan() : acc[i]), ry,
+                                                  rb < rb1 && orow[i] != a.y_bytes ? orow[i] + col : a.y_bytes, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int32_t q = 0; q < nq_pad; q += NS) {  // whole trips: no branch between the steps
+        step(q + 0, std::integral_constant<int, 0>{});
+        step(q + 1, std::integral_constant<int, 1>{});
+        step(q + 2, std::integral_constant<int, 2>{});
+        step(q + 3, std::integral_constant<int, 3>{});
+    }
+    wait_vmcnt<0>();  // no load still landing in LDS when the wave ends
+}
+
 // ---- launchers ----------------------------------------------------------------------------------------------------------
 constexpr int kDecGuWaves = 8, kDecGuAhead = 2;  // waves a block; units of loads in flight ahead of the math
 constexpr int kDecMaxTiles = 1024;               // M <= 16 tokens x A <= 64 slots
@@ -770,6 +933,13 @@ inline void launch_decode_down(const GemmArgs &ga, int64_t M, const SharedJob *s
     const DecodeArgs d = decode_args(ga, M, false);
     const SharedJob s = sh ? *sh : SharedJob{};
     const int blocks = 2 * device_cus() + s.blocks;  // two waves a SIMD
+    // the LDS-ring kernel deals its waves to tiles: every tile needs a wave
+    if (ga.K == dec::kSpan * kDecDownSteps && ga.N % 16 == 0 && d.tiles_bound <= 2 * device_cus() * gdn::kDnWaves &&
+        !getenv("STRIX_OLD_DN")) {
+        if (sh) decode_down_lds_kernel<2><<<(unsigned)blocks, gdn::kDnWaves * kWave, 0, stream>>>(d, s);
+        else decode_down_lds_kernel<0><<<(unsigned)blocks, gdn::kDnWaves * kWave, 0, stream>>>(d, s);
+        return;
+    }
     if (sh) decode_down_kernel<2><<<(unsigned)blocks, kThreads, 0, stream>>>(d, s);
     else decode_down_kernel<0><<<(unsigned)blocks, kThreads, 0, stream>>>(d, s);
 }
