@@ -59,7 +59,7 @@ __global__ void __launch_bounds__(kRangeChunks * kWave) route_hist_kernel(const 
 }
 
 __global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, Layout L, int32_t *ws, uint32_t *err) {
-    __shared__ int wsum[48];
+    __shared__ int wsum[99];
     __shared__ int bad_lds;
     const int E = (int)L.E, t = threadIdx.x;
     const int64_t R = L.nrange();

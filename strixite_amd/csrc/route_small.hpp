@@ -98,33 +98,44 @@ __device__ inline void chunk_place(const int32_t *ids, int64_t s0, int64_t s1, i
     }
 }
 
-// Exclusive scan of three ints over the 1024 threads of a block; totals returned through tot[3].
-__device__ inline void block_scan3(int (&v)[3], int *wsum /* [16][3] LDS */, int (&tot)[3]) {
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    int inc[3] = {v[0], v[1], v[2]};
+// Inclusive sum over the wave's lanes in lane order: Kogge-Stone inside each 16-lane row (DPP row shifts), then the
+// rows' totals carried across by the row broadcasts.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1 and 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// Exclusive scan of three ints over the threads of a block (at most 16 waves); totals returned through tot[3]. Each
+// wave scans in registers; wave 0 scans the waves' totals; two barriers.
+__device__ inline void block_scan3(int (&v)[3], int *wsum /* [2][16][3] LDS */, int (&tot)[3]) {
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, nw = (int)(blockDim.x / kWave);
+    int inc[3];
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int o = __shfl_up(inc[j], off, kWave);
-            if (lane >= off) inc[j] += o;
-        }
+    for (int j = 0; j < 3; ++j) inc[j] = wave_incl_scan(v[j]);
     if (lane == kWave - 1)
 #pragma unroll
         for (int j = 0; j < 3; ++j) wsum[wave * 3 + j] = inc[j];
     __syncthreads();
-    int before[3] = {0, 0, 0};
-    for (int w = 0; w < (int)(blockDim.x / kWave); ++w)
+    if (wave == 0) {  // lanes 0..nw-1: the waves' totals, scanned; exclusive prefixes and the totals to wsum[16..]
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
-            const int t = wsum[w * 3 + j];
-            if (w < wave) before[j] += t;
-            if (w == 0) tot[j] = 0;
-            tot[j] += t;
+            const int t = lane < nw ? wsum[lane * 3 + j] : 0;
+            const int p = wave_incl_scan(t);
+            if (lane < nw) wsum[48 + lane * 3 + j] = p - t;
+            if (lane == kWave - 1) wsum[96 + j] = p;
         }
-#pragma unroll
-    for (int j = 0; j < 3; ++j) v[j] = before[j] + inc[j] - v[j];
+    }
     __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        v[j] = wsum[48 + wave * 3 + j] + inc[j] - v[j];
+        tot[j] = wsum[96 + j];
+    }
 }
 
 __device__ inline void write_header(int32_t *ws, const Layout &L, const int (&tot)[3]) {
@@ -170,8 +181,8 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
     int *bcount = btile + nb;                 // [E + 1]
     int *b64 = bcount + nb;                   // [E + 1] bucket's first 64-slot tile
     int *tile_b = b64 + nb;                   // [T16] bucket of a tile
-    int *wsum = tile_b + L.T16;               // [48]
-    int *bad = wsum + 48;                     // [1]
+    int *wsum = tile_b + L.T16;               // [99]
+    int *bad = wsum + 99;                     // [1]
     // only the waves that hold slots (chunks of 64) count: their counters are the only ones cleared and summed
     const int nw = (S + kWave - 1) / kWave;
     for (int i = t; i < nw * nb; i += nthr) cnt[i] = 0;
@@ -181,12 +192,10 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
         for (int m = wave; m < M; m += kSmallWaves) {
             int id;
             float cf;
+            // the shared gate logit is loaded with the row (one memory round trip), checked after the top-k
+            const float gl = shared_slot ? logits[(int64_t)m * ld + Etop] : 0.f;
             int rb = topk::wave_topk<float, NV>(logits + (int64_t)m * ld, Etop, k, id, cf);
-            float sl = 0.f;
-            if (shared_slot) {
-                sl = logits[(int64_t)m * ld + Etop];
-                if (!isfinite(sl) && Etop < rb) rb = Etop;
-            }
+            if (shared_slot && !isfinite(gl) && Etop < rb) rb = Etop;
             if (rb != INT_MAX) {
                 if (lane == 0 && atomicCAS(&err_router[0], 0u, 1u) == 0u) {
                     err_router[1] = (uint32_t)m;
@@ -197,7 +206,7 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
             if (lane < k) sids[m * A + lane] = id, scoef[m * A + lane] = cf;
             if (shared_slot && lane == k)
                 sids[m * A + k] = rb != INT_MAX ? -1 : Etop,
-                scoef[m * A + k] = rb != INT_MAX ? dev::qnan() : 1.0f / (1.0f + expf(-sl));
+                scoef[m * A + k] = rb != INT_MAX ? dev::qnan() : 1.0f / (1.0f + expf(-gl));
         }
     } else {
         for (int i = t; i < S; i += nthr) sids[i] = ids_in[i];
@@ -265,7 +274,7 @@ __device__ inline void topk_route_small_body(const float *logits, int64_t ld, in
 
 // LDS bytes pack_small_body needs
 inline size_t topk_route_small_lds(const Layout &L) {
-    return ((size_t)3 * kFusedSlots + (size_t)kSmallWaves * (L.E + 1) + 4 * (size_t)(L.E + 1) + (size_t)L.T16 + 48 + 1) * 4;
+    return ((size_t)3 * kFusedSlots + (size_t)kSmallWaves * (L.E + 1) + 4 * (size_t)(L.E + 1) + (size_t)L.T16 + 99 + 1) * 4;
 }
 // ballot bits a bucket index 0..E takes
 inline int bucket_bits(int64_t E) {

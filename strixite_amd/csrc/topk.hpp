@@ -32,18 +32,18 @@ __device__ __forceinline__ float key_value(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? k & 0x7fffffffu : ~k);
 }
 
-// every lane gets the wave's largest unsigned value: row-local DPP max steps, then the four row results
+// every lane gets the wave's largest (MIN: smallest) unsigned value: four DPP steps leave each 16-lane row's result in
+// all of its lanes, two row broadcasts carry it to lane 63 (rows 1 and 3 take lane 15 of the row before, then rows 2
+// and 3 take lane 31), one readlane
 template <bool MIN> __device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v) {
-    auto step = [&](uint32_t o) __attribute__((always_inline)) { v = MIN ? (o < v ? o : v) : (o > v ? o : v); };
-    step((uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm [1, 0, 3, 2]
-    step((uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm [2, 3, 0, 1]
-    step((uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
-    step((uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
-    const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
-    const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
-    const uint32_t a = MIN ? (r0 < r1 ? r0 : r1) : (r0 > r1 ? r0 : r1);
-    const uint32_t b = MIN ? (r2 < r3 ? r2 : r3) : (r2 > r3 ? r2 : r3);
-    return MIN ? (a < b ? a : b) : (a > b ? a : b);
+    auto op = [](uint32_t a, uint32_t b) __attribute__((always_inline)) { return MIN ? (a < b ? a : b) : (a > b ? a : b); };
+    v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));   // quad_perm [1, 0, 3, 2]
+    v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));   // quad_perm [2, 3, 0, 1]
+    v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, true));  // row_half_mirror
+    v = op(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, true));  // row_mirror
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));  // row_bcast:15
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));  // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // Top-k of row[0, E) (E <= 64 NV). Returns the smallest index of a non-finite logit, or INT_MAX; when none, lanes
