@@ -259,7 +259,7 @@ def main():
     gu_gbs = gu_bytes / (gu_ms / 1e3) / 1e9
     log(f"decode gate_up kernel: {gu_ms * 1e3:.1f} us/launch, {gu_bytes / 1e6:.1f} MB -> {gu_gbs:,.0f} GB/s "
         f"({gu_gbs / PEAK_HBM_GBS:.1%} of HBM peak)")
-    line["roofline"] = {"bound": "hbm", "kernel": "decode_gate_up_kernel (grouped Q4 gate_up + SwiGLU, <= 16 tokens)",
+    line["roofline"] = {"bound": "hbm", "kernel": "decode_gate_up_lds_kernel (grouped Q4 gate_up + SwiGLU, <= 16 tokens)",
                         "achieved": round(gu_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                         "frac": round(gu_gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic(),
                         "algorithmic_bytes_per_launch": int(gu_bytes), "us_per_launch": round(gu_ms * 1e3, 3)}
