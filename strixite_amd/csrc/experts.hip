@@ -14,6 +14,7 @@
 // served layout: q4g128, q8g64).
 #include "common.hpp"
 #include "route_small.hpp"
+#include "router_small.hpp"
 
 #include <algorithm>
 #include <array>
@@ -771,6 +772,64 @@ __global__ void __launch_bounds__(1024)
         dense_part_unit<8>(sa, spp, parts, part, w);  // no barrier in this kernel
 }
 
+// The router projection, top-k and packing of a small batch in one launch, with the shared expert's gate_up parts in
+// the grid's last blocks. Blocks 0 .. nrb - 1 compute the logits (router_small.hpp: one wave per 4 tokens x 1 row, the
+// canonical order, so the bits equal the separate projection's), then take a ticket; the block that arrives last runs
+// the top-k + packing (route_small.hpp) over the logits the others stored. The ticket is a 64-bit word of the
+// workspace: high half the launch's epoch (a host counter, never 0), low half the arrivals. An arrival that finds
+// another epoch there (whatever an earlier call or the allocator left) replaces it with this epoch and a count of 1,
+// so the workspace needs no clearing; the last block writes 0 back, so a captured graph that replays the same epoch
+// starts over.
+constexpr int kRouteFusedWaves = 16;  // router items (4 tokens x 1 row) a block
+
+// Arrival count on an epoch-tagged ticket word (one thread): a fetch-add once this launch's epoch is in the word (a CAS
+// per arrival serialises the arrivals' round trips); the first arrivals install it with a CAS (the losers then find it
+// there). Returns this arrival's count, 1-based.
+__device__ inline unsigned arrive(unsigned long long *word, uint32_t epoch) {
+    const unsigned long long tag = (unsigned long long)epoch << 32;
+    unsigned long long seen = *reinterpret_cast<volatile unsigned long long *>(word);
+    for (;;) {
+        if ((seen >> 32) == epoch) return (unsigned)(atomicAdd(word, 1ull) & 0xffffffffull) + 1;
+        const unsigned long long old = atomicCAS(word, seen, tag + 1);
+        if (old == seen) return 1;
+        seen = old;
+    }
+}
+template <int NV, int NCH>
+__global__ void __launch_bounds__(1024)
+    route_fused_kernel(const uint16_t *x, const uint16_t *wr, const float *bias, float *logits, int64_t ld, int M,
+                       int E, int64_t H, int k, int32_t *ids, float *coef, route::Layout L, int nbits, int32_t *ws,
+                       uint32_t *err_router, uint32_t *err_route, unsigned long long *ticket, uint32_t epoch, int nrb,
+                       int ipb, GemmArgs sa, int spp, int parts, float *part, int64_t units) {
+    extern __shared__ int lds[];
+    __shared__ int last;
+    if ((int)blockIdx.x >= nrb) {
+        const int64_t w = (int64_t)(blockIdx.x - nrb) * kSharedUnitsPerBlock + threadIdx.x / kWave;
+        if (threadIdx.x / kWave < kSharedUnitsPerBlock && w < units)
+            dense_part_unit<8>(sa, spp, parts, part, w);  // no barrier on this side
+        return;
+    }
+    const int mg = (M + 3) / 4;  // token groups
+    const int64_t item = (int64_t)blockIdx.x * ipb + threadIdx.x / kWave;
+    if ((int)threadIdx.x / kWave < ipb && item < ld * mg)  // items in row-major order: the waves of a block share weight rows through L1
+        rsmall::router_small_wave<float, 4, 1, NCH, true>(x, wr, logits, M, ld, H, item / mg, item % mg * 4, bias, E);
+    // the block's logits before its ticket: the logits are stored device-coherent (write-through the XCD's L2), every
+    // wave waits for its stores' acknowledgements (vmcnt 0), then the barrier; no L2 write-back (a device-scope
+    // release fence a block measured +8 us at 129 blocks, +55 us at 1026: the write-backs serialise)
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const bool is_last = (int)arrive(ticket, epoch) == nrb;
+        if (is_last) *reinterpret_cast<volatile unsigned long long *>(ticket) = 0;  // every block has arrived
+        last = is_last;
+    }
+    __syncthreads();
+    if (!last) return;
+    // the other blocks' logits after their tickets: the L2 invalidated (no stale line of them read back)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    route::topk_route_small_body<NV>(logits, ld, M, E, k, ids, coef, L, nbits, ws, err_router, err_route, lds);
+}
+
 // y[m, n] = sum_a coef[m, a] * partial[m * A + a, n] in slot order (fmaf), rounded once; NaN for a token with an
 // invalid id. SH: y = stored(sum) + sigmoid(gl) * s (strixite kernels/moe_grouped.hip:948-985). RES: x_out = stored(x + y).
 // INJ (instead of RES): the hyper-connection injection of the stored y into the residual streams, in place,
@@ -1091,6 +1150,58 @@ void launch_topk_route_shared(const float *logits, int64_t ld, int64_t M, int64_
         default: go(std::integral_constant<int, 16>{}); break;
     }
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " E=", E, " k=", k);
+}
+
+// Whether the fused router + top-k + packing launch takes this projection: 16-byte rows of K = 512 * {4, 6, 8}.
+bool route_fused_fits(const void *x, const void *wr, int64_t H) {
+    return H % 512 == 0 && (H / 512 == 4 || H / 512 == 6 || H / 512 == 8) &&
+           reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(wr) % 16 == 0;
+}
+
+// The router projection (+ bias), top-k and packing of a small batch in one launch (route_fused_kernel), with the
+// shared expert's gate_up parts in the grid's last blocks. ticket: 8 bytes of the caller's workspace, any contents.
+void launch_route_fused(const uint16_t *x, const uint16_t *wr, const float *bias, float *logits, int64_t ld, int64_t M,
+                        int64_t E, int64_t H, int64_t k, int32_t *ids, float *coef, void *ws, size_t ws_bytes,
+                        uint32_t *err_router, uint32_t *err_route, unsigned long long *ticket, const GemmArgs &sa,
+                        int spp, int parts, float *part, hipStream_t stream) {
+    const char *fn = "moe_layer_forward (router + top-k + packing)";
+    STRIX_CHECK(M >= 1 && k >= 1 && k <= 64 && k <= E && E <= kMoeMaxExperts && M * k <= route::kFusedSlots &&
+                    (ld == E || ld == E + 1) && route_fused_fits(x, wr, H),
+                fn, ": M = ", M, ", E = ", E, ", k = ", k, ", H = ", H);
+    STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, k, E) && reinterpret_cast<uintptr_t>(ws) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(ticket) % 8 == 0,
+                fn, ": workspace of ", ws_bytes, " bytes, needs ", moe_route_workspace_bytes(M, k, E),
+                ", 16-byte aligned (ticket 8-byte aligned)");
+    static std::atomic<uint32_t> epochs{0};
+    uint32_t epoch = 0;
+    while (epoch == 0) epoch = ++epochs;
+    const route::Layout L = route::layout(M, k, E);
+    const int nbits = route::bucket_bits(E);
+    const size_t lds = route::topk_route_small_lds(L);
+    const int64_t items = ld * ((M + 3) / 4);
+    const int ipb = kRouteFusedWaves;
+    const int nrb = (int)((items + ipb - 1) / ipb);
+    const int64_t units = sa.N / 16 * parts;
+    const unsigned blocks = (unsigned)nrb + (unsigned)((units + kSharedUnitsPerBlock - 1) / kSharedUnitsPerBlock);
+    const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
+    auto go = [&](auto nvc, auto nchc) {
+        route_fused_kernel<decltype(nvc)::value, decltype(nchc)::value><<<blocks, 1024, lds, stream>>>(
+            x, wr, bias, logits, ld, (int)M, (int)E, H, (int)k, ids, coef, L, nbits, static_cast<int32_t *>(ws),
+            err_router, err_route, ticket, epoch, nrb, ipb, sa, spp, parts, part, units);
+    };
+    auto by_nch = [&](auto nvc) {
+        if (H / 512 == 4) go(nvc, std::integral_constant<int, 4>{});
+        else if (H / 512 == 6) go(nvc, std::integral_constant<int, 6>{});
+        else go(nvc, std::integral_constant<int, 8>{});
+    };
+    switch (nv) {
+        case 1: by_nch(std::integral_constant<int, 1>{}); break;
+        case 2: by_nch(std::integral_constant<int, 2>{}); break;
+        case 4: by_nch(std::integral_constant<int, 4>{}); break;
+        case 8: by_nch(std::integral_constant<int, 8>{}); break;
+        default: by_nch(std::integral_constant<int, 16>{}); break;
+    }
+    STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " E=", E, " k=", k, " H=", H);
 }
 
 void check_grouped(const char *fn, const void *x, const QV &w, int64_t E, const void *ws, size_t ws_bytes, int64_t M,
@@ -1426,7 +1537,7 @@ namespace strix {
 
 namespace {
 struct LayerWs {
-    int64_t logits, norms, ids, coef, route, x16, h, partial, sh_h, sh_s, sh_part, total;
+    int64_t logits, norms, ids, coef, route, x16, h, partial, sh_h, sh_s, sh_part, ticket, total;
     size_t route_bytes;
 };
 int64_t al(int64_t b) { return (b + 255) / 256 * 256; }
@@ -1450,6 +1561,7 @@ LayerWs layer_ws(const MoeLayerWeights &w, int64_t M) {
     L.sh_s = o, o += al(w.has_shared ? M * H * 2 : 0);
     // the split-K parts of the shared expert's projections at M <= 16 (gate_up, then down, in the same space)
     L.sh_part = o, o += al(w.has_shared && M <= 16 ? kernels::kSharedParts * M * std::max(2 * I, H) * 4 : 0);
+    L.ticket = o, o += al(8);  // the fused routing launch's arrival ticket (any contents)
     L.total = o;
     return L;
 }
@@ -1620,12 +1732,26 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     // router projection (+ harness bias) and top-k
     const float *lg = logits_in;
     bool routed = false;  // ids and coef already written (the prefill router selects as it projects)
+    bool fused = false;   // and the routes packed (the decode routing launch)
     if (!lg) {
         lg = logits;
         // prefill sizes: bf16 MFMA projection + exact recomputation of the candidates (the same routing bits)
         routed = M >= 256 && moe_router_prefill(x, w.router, w.router_bias, M, H, E, k, w.has_shared || stacked, logits,
                                                 reinterpret_cast<float *>(base + L.norms), ids, coef, err_router,
                                                 stream, stacked);
+        // decode sizes: router projection, top-k and packing in one launch, when asked for (STRIX_FUSED_ROUTE=1).
+        // Off by default: measured on MI355X at 16 tokens, H 3072, 513 router rows, it takes 24.9 us against 6.0 +
+        // 11.9 us for the two launches (the top-k cannot start before the last router block, and the router's waves
+        // in 1024-thread blocks take ~8 us of work against ~4 in its own launch)
+        const char *fr = getenv("STRIX_FUSED_ROUTE");
+        const bool fused_route = fr != nullptr && atoi(fr) != 0;
+        if (!routed && fused_route && fold && M * A <= 1024 && kernels::route_fused_fits(x, w.router, H)) {
+            launch_route_fused(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(w.router),
+                               w.router_bias, logits, ld, M, E, H, k, ids, coef, route, L.route_bytes, err_router,
+                               err_expert, reinterpret_cast<unsigned long long *>(base + L.ticket), sh_gu, sh_gu_spp,
+                               sh_gu_parts, sh_part, stream);
+            routed = fused = true;
+        }
         if (!routed) {
             linear_bf16w(x, w.router, logits, M, ld, H, Act::BF16, Act::F32, stream);
             if (w.router_bias) {
@@ -1636,7 +1762,9 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
             }
         }
     }
-    if (routed) {
+    if (fused) {
+        // ids, coef and the packed routes written
+    } else if (routed) {
         moe_group_routes(ids, M, A, Es, route, L.route_bytes, err_expert, stream);
     } else if (M * A <= 1024) {  // one launch: top-k and packing with the ids kept in LDS
         if (fold)

@@ -486,6 +486,59 @@ def test_layer_fused_topk_packing_matches_router(M, E, k):
     assert np.all(np.isfinite(to_np(out["y"]).view(np.uint16)[ok] != 0x7fc0))
 
 
+@pytest.mark.parametrize("M,H,biased", [(16, 3072, False), (5, 2048, True), (1, 4096, False)])
+def test_layer_fused_router_launch(M, H, biased, monkeypatch):
+    """Decode sizes with a shared expert can run the router projection, top-k and packing as one launch
+    (STRIX_FUSED_ROUTE=1; the last router block to arrive routes): ids and coefficients equal linear_bf16w (+ bias) + moe_router bit for bit, y equals the
+    same layer fed those logits (the separate top-k launch) bit for bit, on a workspace full of random bytes (the
+    arrival ticket needs no clearing), on two calls in a row on it, and on three replays of a captured graph with
+    other work between them (one epoch replayed: the last block's reset of the ticket)."""
+    say("fused router launch", M, H, biased)
+    E, k = 512, 10
+    rng = np.random.default_rng(M + H)
+    bias = torch.from_numpy((0.3 * rng.standard_normal(E)).astype(np.float32)).to(DEV) if biased else None
+    layer = moe.MoeLayer.synth(H, E, k, 256, seed=9, router_bias=bias)
+    x = moe.synth_bf16_normal(9, "x", M, (M, H), 1.0)
+    lg = moe.linear_bf16w(x, layer.router)
+    if biased:
+        lg[:, :E] += bias
+    rids, rcoef, _ = moe.moe_router(lg, E, k, ld=E + 1)
+    want = layer.forward(x, logits_in=lg)
+    torch.cuda.synchronize()
+    monkeypatch.setenv("STRIX_FUSED_ROUTE", "1")
+
+    def check(out, what):
+        assert np.array_equal(to_np(out["ids"]), to_np(rids)), what
+        assert np.array_equal(to_np(out["coef"]).view(np.uint32), to_np(rcoef).view(np.uint32)), what
+        assert np.array_equal(to_np(out["y"]).view(np.uint16), to_np(want["y"]).view(np.uint16)), what
+        assert to_np(out["err"])[0] == 0 and to_np(out["err"])[3] == 0, what
+
+    ws = torch.from_numpy(rng.integers(0, 256, layer.workspace_bytes(M), dtype=np.uint8)).to(DEV)
+    for call in range(2):
+        out = layer.forward(x, ws=ws)
+        torch.cuda.synchronize()
+        check(out, ("call", call))
+    # graph replays: the same launch arguments (epoch included) every replay
+    out = {n: torch.zeros_like(t) for n, t in want.items()}
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        layer.forward(x, ws=ws, out=out)  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer.forward(x, ws=ws, out=out)
+    for rep in range(3):
+        for t in out.values():
+            t.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        check(out, ("replay", rep))
+        layer.forward(x, ws=ws)  # eager work on the same workspace between replays
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("biased", [False, True])
 def test_layer_prefill_router_exact_routing(biased):
     """Prefill-size layers route through the bf16 MFMA projection + exact recomputation of the candidates: ids and
