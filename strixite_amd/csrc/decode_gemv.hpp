@@ -23,7 +23,15 @@
 // over one quantization group, acc += s * D + (m - 128 s) * sum(x over the group) on the FP32 accumulator.
 #pragma once
 
-constexpr int kDecMaxTilesL = 1024;  // tile records a decode launch holds in LDS (M <= 16 tokens x A <= 64 slots)
+constexpr int kDecMaxTilesL = 1024;
+
+// f(integral_constant<I>) .. f(integral_constant<N - 1>) in order: the ring positions of a trip, as constants
+template <int I, int N, typename F> __device__ __forceinline__ void ring_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        ring_for<I + 1, N>(f);
+    }
+}  // tile records a decode launch holds in LDS (M <= 16 tokens x A <= 64 slots)
 namespace dec {
 constexpr int kSpan = 128;         // Q4 codes of a row per K step: 4 lane groups x 32 (one quantization group)
 constexpr int kMaxTokens = 16;     // the MFMA's A rows
@@ -594,12 +602,8 @@ __global__ void __launch_bounds__((W + 1) * kWave) decode_gate_up_lds_kernel(Dec
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    for (int32_t q = 0; q < nq_pad; q += NS) {  // whole trips: no branch between the steps
-        step(q + 0, std::integral_constant<int, 0>{});
-        step(q + 1, std::integral_constant<int, 1>{});
-        step(q + 2, std::integral_constant<int, 2>{});
-        step(q + 3, std::integral_constant<int, 3>{});
-    }
+    for (int32_t q = 0; q < nq_pad; q += NS)  // whole trips: no branch between the steps
+        ring_for<0, NS>([&](auto Q) { step(q + decltype(Q)::value, Q); });
     wait_vmcnt<0>();  // no load still landing in LDS when the wave ends
 }
 
@@ -699,13 +703,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 // (l % 16) ^ row at position l % 16 (the MFMA-layout reads of one chunk of the 16 rows hit 16 bank groups); then
 // 32 dwords of scales (row r: dword 2 r + group / 2) and 32 of mins.
 namespace gdn {
-constexpr int kDnStages = 4, kDnWaves = 4;  // per-wave ring; waves a block (two blocks a CU)
+constexpr int kDnStages = 3, kDnWaves = 4;  // per-wave ring; waves a block (three blocks a CU)
 constexpr int kPosU4 = 4 * kWave + 16;      // codes + 64 dwords of scales and mins
 }  // namespace gdn
 
-template <int SH>
-__global__ void __launch_bounds__(gdn::kDnWaves * kWave) decode_down_lds_kernel(DecodeArgs a, SharedJob sh) {
-    constexpr int NS = gdn::kDnStages, WB = gdn::kDnWaves, KS = kDecDownSteps;  // KS: groups a row (K = 512)
+template <int SH, int WB = gdn::kDnWaves, int NS = gdn::kDnStages>
+__global__ void __launch_bounds__(WB * kWave) decode_down_lds_kernel(DecodeArgs a, SharedJob sh) {
+    static_assert(NS >= 3 && NS <= 8, "ring positions: separate LDS arrays, at most 8");
+    constexpr int KS = kDecDownSteps;  // KS: groups a row (K = 512)
     int bid = (int)blockIdx.x, nblk = (int)gridDim.x;
     if constexpr (SH == 2) {
         if (bid < sh.blocks) {  // the shared expert's down, split-K parts
@@ -715,8 +720,11 @@ __global__ void __launch_bounds__(gdn::kDnWaves * kWave) decode_down_lds_kernel(
         }
         bid -= sh.blocks, nblk -= sh.blocks;
     }
-    __shared__ __attribute__((aligned(16))) uint4 rp0[WB][gdn::kPosU4], rp1[WB][gdn::kPosU4], rp2[WB][gdn::kPosU4],
-        rp3[WB][gdn::kPosU4];
+    // one array a ring position (the compiler tracks the direct-to-LDS loads' aliasing per array); unused ones 1 x 1
+    constexpr int P = gdn::kPosU4;
+    __shared__ __attribute__((aligned(16))) uint4 rp0[WB][P], rp1[WB][P], rp2[WB][P], rp3[NS > 3 ? WB : 1][NS > 3 ? P : 1],
+        rp4[NS > 4 ? WB : 1][NS > 4 ? P : 1], rp5[NS > 5 ? WB : 1][NS > 5 ? P : 1], rp6[NS > 6 ? WB : 1][NS > 6 ? P : 1],
+        rp7[NS > 7 ? WB : 1][NS > 7 ? P : 1];
     const int lane = threadIdx.x % kWave, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int g = lane / 16, j = lane % 16;
     auto ring = [&](auto P) -> uint4 * {
@@ -724,7 +732,11 @@ __global__ void __launch_bounds__(gdn::kDnWaves * kWave) decode_down_lds_kernel(
         if constexpr (p == 0) return rp0[wave];
         else if constexpr (p == 1) return rp1[wave];
         else if constexpr (p == 2) return rp2[wave];
-        else return rp3[wave];
+        else if constexpr (p == 3) return rp3[wave];
+        else if constexpr (p == 4) return rp4[wave];
+        else if constexpr (p == 5) return rp5[wave];
+        else if constexpr (p == 6) return rp6[wave];
+        else return rp7[wave];
     };
     const int64_t n_tiles = a.ws[0] < a.tiles_bound ? a.ws[0] : a.tiles_bound;
     if (n_tiles <= 0) return;
@@ -780,9 +792,7 @@ __global__ void __launch_bounds__(gdn::kDnWaves * kWave) decode_down_lds_kernel(
         }
     };
     const int32_t nq = rb1 - rb0, nq_pad = (nq + NS - 1) / NS * NS;
-    issue(0, std::integral_constant<int, 0>{});
-    issue(1, std::integral_constant<int, 1>{});
-    issue(2, std::integral_constant<int, 2>{});
+    ring_for<0, NS - 1>([&](auto Q) { issue(decltype(Q)::value, Q); });
     // A fragments and the per-group sums of the tile rows (lane (g, j): slots 4 g + i) from an MFMA against ones
     Frag hf[KS][4];
     float hs[KS][4];
@@ -793,7 +803,7 @@ __global__ void __launch_bounds__(gdn::kDnWaves * kWave) decode_down_lds_kernel(
             float4v d = {0, 0, 0, 0};
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                hf[s][v] = Frag{{hr[s][v].x, hr[s][v].y, hr[s][v].z, hr[s][v].w}};
+                hf[s][v] = bf16_natural_to_paired(hr[s][v]);  // the codes' paired k order (below)
                 d = mfma_bf16(hf[s][v], ones, d);
             }
 #pragma unroll
@@ -826,7 +836,7 @@ __global__ void __launch_bounds__(gdn::kDnWaves * kWave) decode_down_lds_kernel(
             float4v d = {0, 0, 0, 0};
             const uint32_t qw[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int w = 0; w < 4; ++w) d = mfma_bf16(hf[s][w], q4_codes_to_bf16(qw[w]), d);
+            for (int w = 0; w < 4; ++w) d = mfma_bf16(hf[s][w], q4_paired_to_bf16(qw[w]), d);
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] = fmaf(sc, d[i], fmaf(mn, hs[s][i], acc[i]));
         }
@@ -839,12 +849,8 @@ __global__ void __launch_bounds__(gdn::kDnWaves * kWave) decode_down_lds_kernel(
                                                   rb < rb1 && orow[i] != a.y_bytes ? orow[i] + col : a.y_bytes, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
     };
-    for (int32_t q = 0; q < nq_pad; q += NS) {  // whole trips: no branch between the steps
-        step(q + 0, std::integral_constant<int, 0>{});
-        step(q + 1, std::integral_constant<int, 1>{});
-        step(q + 2, std::integral_constant<int, 2>{});
-        step(q + 3, std::integral_constant<int, 3>{});
-    }
+    for (int32_t q = 0; q < nq_pad; q += NS)  // whole trips: no branch between the steps
+        ring_for<0, NS>([&](auto Q) { step(q + decltype(Q)::value, Q); });
     wait_vmcnt<0>();  // no load still landing in LDS when the wave ends
 }
 
@@ -934,10 +940,23 @@ inline void launch_decode_down(const GemmArgs &ga, int64_t M, const SharedJob *s
     const SharedJob s = sh ? *sh : SharedJob{};
     const int blocks = 2 * device_cus() + s.blocks;  // two waves a SIMD
     // the LDS-ring kernel deals its waves to tiles: every tile needs a wave
-    if (ga.K == dec::kSpan * kDecDownSteps && ga.N % 16 == 0 && d.tiles_bound <= 2 * device_cus() * gdn::kDnWaves &&
+    constexpr int kDnBlocksPerCu = 163840 / (gdn::kDnWaves * gdn::kDnStages * gdn::kPosU4 * 16);
+    if (ga.K == dec::kSpan * kDecDownSteps && ga.N % 16 == 0 &&
+        d.tiles_bound <= (int64_t)kDnBlocksPerCu * device_cus() * gdn::kDnWaves &&
         !getenv("STRIX_OLD_DN")) {
-        if (sh) decode_down_lds_kernel<2><<<(unsigned)blocks, gdn::kDnWaves * kWave, 0, stream>>>(d, s);
-        else decode_down_lds_kernel<0><<<(unsigned)blocks, gdn::kDnWaves * kWave, 0, stream>>>(d, s);
+        // 4 waves x 3 ring positions a block, three blocks a CU (12 waves): measured on MI355X at 16 tokens, H 3072,
+        // I 512, 512 experts top-10 (layer us): 4 x 4 two blocks 104.2, 4 x 3 102.7, 3 x 4 104.1, 3 x 6 109.9,
+        // 2 x 8 109.3, 1 x 8 110.4 - more waves beat more units in flight (the LDS reads and the dequantisation
+        // of a unit are hidden by other waves, not by a wave's own ring)
+        auto go = [&](auto wbc, auto nsc) {
+            constexpr int WB = decltype(wbc)::value, NS = decltype(nsc)::value;
+            constexpr int lds = WB * NS * gdn::kPosU4 * 16;
+            const int bpc = 163840 / lds;  // blocks a CU by LDS
+            const int nb = bpc * device_cus() + s.blocks;
+            if (sh) decode_down_lds_kernel<2, WB, NS><<<(unsigned)nb, WB * kWave, 0, stream>>>(d, s);
+            else decode_down_lds_kernel<0, WB, NS><<<(unsigned)nb, WB * kWave, 0, stream>>>(d, s);
+        };
+        go(std::integral_constant<int, gdn::kDnWaves>{}, std::integral_constant<int, gdn::kDnStages>{});
         return;
     }
     if (sh) decode_down_kernel<2><<<(unsigned)blocks, kThreads, 0, stream>>>(d, s);
