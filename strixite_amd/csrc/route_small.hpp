@@ -183,6 +183,8 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
     int *tile_b = b64 + nb;                   // [T16] bucket of a tile
     int *wsum = tile_b + L.T16;               // [99]
     int *bad = wsum + 99;                     // [1]
+    // [16][kCandScratch] the waves' top-k candidates (8-byte aligned)
+    uint2 *cand = reinterpret_cast<uint2 *>(lds + ((3 * kFusedSlots + kSmallWaves * nb + 4 * nb + L.T16 + 100 + 1) & ~1));
     // only the waves that hold slots (chunks of 64) count: their counters are the only ones cleared and summed
     const int nw = (S + kWave - 1) / kWave;
     for (int i = t; i < nw * nb; i += nthr) cnt[i] = 0;
@@ -194,7 +196,8 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
             float cf;
             // the shared gate logit is loaded with the row (one memory round trip), checked after the top-k
             const float gl = shared_slot ? logits[(int64_t)m * ld + Etop] : 0.f;
-            int rb = topk::wave_topk<float, NV>(logits + (int64_t)m * ld, Etop, k, id, cf);
+            int rb = topk::wave_topk<float, NV>(logits + (int64_t)m * ld, Etop, k, id, cf,
+                                                cand + wave * topk::kCandScratch);
             if (shared_slot && !isfinite(gl) && Etop < rb) rb = Etop;
             if (rb != INT_MAX) {
                 if (lane == 0 && atomicCAS(&err_router[0], 0u, 1u) == 0u) {
@@ -274,7 +277,9 @@ __device__ inline void topk_route_small_body(const float *logits, int64_t ld, in
 
 // LDS bytes pack_small_body needs
 inline size_t topk_route_small_lds(const Layout &L) {
-    return ((size_t)3 * kFusedSlots + (size_t)kSmallWaves * (L.E + 1) + 4 * (size_t)(L.E + 1) + (size_t)L.T16 + 99 + 1) * 4;
+    const size_t ints = ((size_t)3 * kFusedSlots + (size_t)kSmallWaves * (L.E + 1) + 4 * (size_t)(L.E + 1) +
+                         (size_t)L.T16 + 100 + 1) & ~(size_t)1;
+    return ints * 4 + (size_t)kSmallWaves * topk::kCandScratch * 8;  // + the top-k candidates
 }
 // ballot bits a bucket index 0..E takes
 inline int bucket_bits(int64_t E) {

@@ -233,9 +233,10 @@ __global__ void __launch_bounds__(kThreads)
         sl = topk::load_logit(shared, m * shared_ld);
         if (!isfinite(sl)) bad = E;
     }
+    __shared__ uint2 cand[kThreads / kWave][topk::kCandScratch];
     int id;
     float cf;
-    const int rb = topk::wave_topk<T, NV>(logits + m * ld, E, k, id, cf);
+    const int rb = topk::wave_topk<T, NV>(logits + m * ld, E, k, id, cf, cand[threadIdx.x / kWave]);
     bad = rb < bad ? rb : bad;
     if (bad != INT_MAX) {
         if (lane == 0 && atomicCAS(&err[0], 0u, 1u) == 0u) {

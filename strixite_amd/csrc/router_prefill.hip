@@ -327,9 +327,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     uint32_t my_k, top;
     rounds<NV>(key, k, id, my_k, top);
     const float e0 = lane < k ? expf(topk::key_value(my_k) - topk::key_value(top)) : 0.f;
-    float sum = e0;
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, kWave);
+    const float sum = topk::wave_butterfly_sum(e0);  // the standalone top-k's order: the same coefficient bits
     if (lane < k) id_row[lane] = id, coef_row[lane] = e0 / sum;
     if (shared_slot && lane == 0) id_row[k] = E, coef_row[k] = 1.0f / (1.0f + expf(-sd));
 }
