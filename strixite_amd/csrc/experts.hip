@@ -842,6 +842,10 @@ __global__ void __launch_bounds__(1024)
 // the FP32 partials and the shared expert's parts are read as float4
 constexpr int kCombineVec = 4;
 static_assert(kCombineVec % 4 == 0, "float4 loads of FP32 partials");
+// outputs a thread: 8 over BF16 partials (16-byte loads, held as raw dwords until their FMAs; measured on MI355X at
+// the 4096-token prefill, 252 MB of partials: 88 us with 4 outputs unpacked at load, 61 us so), else kCombineVec;
+// N must be a multiple
+__host__ __device__ constexpr int combine_vec(bool pb) { return pb ? 8 : kCombineVec; }
 struct InjectArgs {
     uint16_t *xs;        // [M, streams N] BF16, updated in place
     const float *w_in;   // [M, streams]
@@ -855,7 +859,7 @@ __global__ void __launch_bounds__(kThreads)
                           int64_t N, uint16_t *y, const uint16_t *s, const float *gate_logit, int64_t gate_ld,
                           uint32_t gate_index, uint32_t *err, const uint16_t *resid, uint16_t *out,
                           const float *s_part, int s_parts, InjectArgs inj = {}) {
-    constexpr int VEC = kCombineVec, W = VEC / 2;  // W: dwords of VEC bf16
+    constexpr int VEC = combine_vec(PB), W = VEC / 2;  // W: dwords of VEC bf16
     const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * VEC;
     if (i >= M * N) return;
     const int64_t m = UNI ? (int64_t)__builtin_amdgcn_readfirstlane((int)(i / N)) : i / N, n = i % N;
@@ -900,7 +904,8 @@ __global__ void __launch_bounds__(kThreads)
     float v[VEC] = {};
     constexpr int B = 16;  // slots whose loads are in flight together
     for (int64_t a0 = 0; a0 < A; a0 += B) {
-        float p[B][VEC];
+        // raw loaded words: VEC dwords of FP32, or W dwords of BF16 pairs
+        uint32_t p[B][PB ? W : VEC];
         float c[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) {
@@ -908,13 +913,11 @@ __global__ void __launch_bounds__(kThreads)
             if (a < A) {
                 const int64_t e = (m * A + a) * N + n;
                 if constexpr (PB) {
-                    uint32_t w[W];
-                    ld_bf16(static_cast<const uint16_t *>(partial) + e, w);
-#pragma unroll
-                    for (int k = 0; k < W; ++k) p[b][2 * k] = lo(w[k]), p[b][2 * k + 1] = hi(w[k]);
+                    ld_bf16(static_cast<const uint16_t *>(partial) + e, p[b]);
                 } else {
                     const float4 q = *reinterpret_cast<const float4 *>(static_cast<const float *>(partial) + e);
-                    p[b][0] = q.x, p[b][1] = q.y, p[b][2] = q.z, p[b][3] = q.w;
+                    p[b][0] = __float_as_uint(q.x), p[b][1] = __float_as_uint(q.y), p[b][2] = __float_as_uint(q.z),
+                    p[b][3] = __float_as_uint(q.w);
                 }
                 c[b] = coef[m * A + a];
                 const int32_t id = ids[m * A + a];
@@ -925,7 +928,10 @@ __global__ void __launch_bounds__(kThreads)
         for (int b = 0; b < B; ++b) {
             if (a0 + b >= A) break;
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) v[k] = fmaf(c[b], p[b][k], v[k]);
+            for (int k = 0; k < VEC; ++k) {
+                const float pv = PB ? (k % 2 ? hi(p[b][k / 2]) : lo(p[b][k / 2])) : __uint_as_float(p[b][k]);
+                v[k] = fmaf(c[b], pv, v[k]);
+            }
         }
     }
     if (!ok)
@@ -1266,14 +1272,16 @@ void combine_reduce(const void *partial, const int32_t *ids, const float *coef, 
                     int64_t N, uint16_t *y, const MoeSharedAdd *sh, const uint16_t *resid, uint16_t *out,
                     hipStream_t stream, const float *s_part = nullptr, int s_parts = 0, bool partial_bf16 = false,
                     const InjectArgs *inj = nullptr) {
-    const unsigned blocks = (unsigned)((M * N / kCombineVec + kThreads - 1) / kThreads);
+    const int vec = combine_vec(partial_bf16);
+    STRIX_CHECK(N % vec == 0, "combine: N = ", N, " must be a multiple of ", vec);
+    const unsigned blocks = (unsigned)((M * N / vec + kThreads - 1) / kThreads);
     const uint16_t *s = sh ? static_cast<const uint16_t *>(sh->s) : nullptr;
     const float *gl = sh ? sh->gate_logit : nullptr;
     const int64_t gld = sh ? sh->gate_ld : 0;
     const uint32_t gi = sh ? sh->gate_index : 0;
     uint32_t *err = sh ? sh->err : nullptr;
     // (M N < 2^31 elements: the uniform token index fits an int)
-    const bool uni = N % (kWave * kCombineVec) == 0 && M * N < (1ll << 31);
+    const bool uni = N % (kWave * vec) == 0 && M * N < (1ll << 31);
     if (inj != nullptr) {  // the injection replaces the residual write
         auto gi_ = [&](auto shc, auto pbc) {
             if (uni)
