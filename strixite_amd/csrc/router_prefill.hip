@@ -158,42 +158,6 @@ __device__ __forceinline__ float lane_chain(const uint4 (&xr)[NCH], const uint4 
     return acc;
 }
 
-// k rounds over this lane's keys (0 = not eligible): lane r < k ends with the r-th pick's id and key
-template <int NV>
-__device__ __forceinline__ void rounds(uint32_t (&key)[NV], int k, int &id, uint32_t &my_k, uint32_t &top) {
-    const int lane = threadIdx.x % kWave;
-    uint32_t lk = 0;
-    int lj = 0;
-    auto lane_best = [&]() __attribute__((always_inline)) {
-        lk = 0, lj = 0;
-#pragma unroll
-        for (int j = 0; j < NV; ++j)
-            if (key[j] > lk) lk = key[j], lj = j;
-    };
-    lane_best();
-    id = -1, my_k = 0, top = 0;
-    for (int r = 0; r < k; ++r) {
-        const uint32_t best = topk::wave_reduce_u32<false>(lk);
-        const uint64_t holders = __ballot(lk == best);
-        int win;
-        if ((holders & (holders - 1)) == 0) {
-            win = __builtin_ctzll(holders);
-        } else {
-            const uint32_t mine = lk == best ? (uint32_t)(lane + lj * kWave) : 0xffffffffu;
-            win = (int)(topk::wave_reduce_u32<true>(mine) % kWave);
-        }
-        const int wj = __builtin_amdgcn_readlane(lj, win);
-        if (r == 0) top = best;
-        if (lane == r) my_k = best, id = win + wj * kWave;
-        if (lane == win) {
-#pragma unroll
-            for (int j = 0; j < NV; ++j)
-                if (j == wj) key[j] = 0u;
-            lane_best();
-        }
-    }
-}
-
 // One wave per token. parts: the approx pass's K parts [kParts][M][ld] (part 0 is the layer's logits buffer: the
 // exact values are written there); nx2 / nw2: the parts' squared norms.
 template <int NV, int NCH>
@@ -202,6 +166,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
                          int64_t M, int E, int k, bool shared, bool shared_slot, const float *nx2, const float *nw2,
                          int32_t *ids, float *coef, uint32_t *err) {
     __shared__ int cand_lds[kThreads / kWave][1040];  // a wave's candidate list (at most E + 1 <= 1025)
+    __shared__ uint2 pick_lds[kThreads / kWave][topk::kCandScratch];  // the picks' scratch (topk::wave_picks)
     const int lane = threadIdx.x % kWave;
     const int64_t m = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
     if (m >= M) return;  // whole wave; no barrier in this kernel
@@ -237,12 +202,12 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     uint32_t key[NV];
     bool cand[NV];
     if (!exact_all) {
-        // tau: the k-th largest lower bound (the key lane k - 1 ends with after k rounds)
+        // tau: the k-th largest lower bound (the key of pick k - 1, held by lane k - 1)
 #pragma unroll
         for (int j = 0; j < NV; ++j) key[j] = lane + j * kWave < E ? topk::order_key(va[j] - dl[j]) : 0u;
         int id_unused;
         uint32_t kth, top_unused;
-        rounds<NV>(key, k, id_unused, kth, top_unused);
+        topk::wave_picks<NV>(key, k, pick_lds[threadIdx.x / kWave], id_unused, kth, top_unused);
         const uint32_t tau = __builtin_amdgcn_readlane(kth, k - 1);
 #pragma unroll
         for (int j = 0; j < NV; ++j) cand[j] = lane + j * kWave < E && topk::order_key(va[j] + dl[j]) >= tau;
@@ -325,7 +290,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     for (int j = 0; j < NV; ++j) key[j] = cand[j] ? topk::order_key(ex[j]) : 0u;
     int id;
     uint32_t my_k, top;
-    rounds<NV>(key, k, id, my_k, top);
+    topk::wave_picks<NV>(key, k, pick_lds[threadIdx.x / kWave], id, my_k, top);
     const float e0 = lane < k ? expf(topk::key_value(my_k) - topk::key_value(top)) : 0.f;
     const float sum = topk::wave_butterfly_sum(e0);  // the standalone top-k's order: the same coefficient bits
     if (lane < k) id_row[lane] = id, coef_row[lane] = e0 / sum;

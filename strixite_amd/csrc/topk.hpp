@@ -79,37 +79,20 @@ __device__ __forceinline__ float wave_butterfly_sum(float v) {
 // LDS a wave's candidate top-k needs (uint2 entries): the candidates, then the k picks
 constexpr int kCandScratch = kWave + kWave;
 
-// Top-k of row[0, E) (E <= 64 NV). Returns the smallest index of a non-finite logit, or INT_MAX; when none, lanes
-// a < k hold the a-th pick (id) and its softmax weight over the k picks (coef).
-// Order: larger logit first, on an exact tie the lower expert index.
-// With scratch (kCandScratch uint2 of LDS for this wave): the candidates are the keys >= T, T the k-th largest of the
-// 64 lanes' maxima (the k lanes holding those maxima hold k keys >= T, so no key below T is among the top k); a
-// 32-step bitwise search with ballot counts finds T, the candidates (usually k to k + a few) are packed into LDS by a wave prefix sum
-// and ranked exactly (key, then index), and pick r goes to lane r. More than 64 candidates (many equal logits): the
-// rounds below. Without scratch, or then, the rounds: the wave max of the lanes' best keys; the lanes holding it (a
-// ballot) - one, or on an exact tie the one whose best index is lowest; that lane marks its pick taken and rescans its
-// NV keys (ascending, strict: the lowest index among its equal keys). Both give the same picks, so the same bits.
-template <typename T, int NV>
-__device__ __forceinline__ int wave_topk(const T *row, int E, int k, int &id, float &coef, uint2 *scratch = nullptr) {
+// The k largest of the wave's keys (key[j] of lane l is expert l + 64 j; 0 = not eligible), larger key first, on an
+// exact tie the lower expert index: lane r < k ends with the r-th pick's expert (id) and key (my_k), every lane with
+// the first pick's key (top). key is clobbered. With scratch (kCandScratch uint2 of LDS for this wave): the
+// candidates are the keys >= T, T the k-th largest of the 64 lanes' maxima (the k lanes holding those maxima hold k
+// keys >= T, so no key below T is among the top k); a 32-step bitwise search with ballot counts finds T, the
+// candidates (usually k to k + a few) are packed into LDS by a wave prefix sum and ranked exactly across lanes, and
+// pick r goes to lane r. More than 64 candidates (many equal keys), or no scratch: k rounds, each the wave max of the
+// lanes' best keys, its holder (the lowest index on an exact tie) marking it taken and rescanning its NV keys. Both
+// give the same picks.
+template <int NV>
+__device__ __forceinline__ void wave_picks(uint32_t (&key)[NV], int k, uint2 *scratch, int &id, uint32_t &my_k,
+                                           uint32_t &top) {
     const int lane = threadIdx.x % kWave;
-    uint32_t key[NV];
-    bool fin = true;
-    int bad = INT_MAX;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int e = lane + j * kWave;
-        const float xv = e < E ? load_logit(row, e) : 0.0f;
-        const bool f = isfinite(xv);
-        if (e < E && !f && e < bad) bad = e;
-        fin = fin && f;
-        key[j] = e < E && f ? order_key(xv) : 0u;
-    }
-    if (__ballot(!fin) != 0) {  // rare: the smallest bad index
-#pragma unroll
-        for (int off = kWave / 2; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off, kWave));
-        return bad;
-    }
-    uint32_t my_k = 0, top = 0;
+    my_k = 0, top = 0;
     id = -1;
     bool done = false;
     if (scratch != nullptr) {
@@ -128,7 +111,7 @@ __device__ __forceinline__ int wave_topk(const T *row, int E, int k, int &id, fl
         for (int j = 0; j < NV; ++j) cnt += key[j] >= thr && key[j] != 0u;
         const int incl = wave_incl_sum(cnt);
         const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
-        if (total <= kWave) {
+        if (total <= kWave && total >= k) {
             int pos = incl - cnt;
 #pragma unroll
             for (int j = 0; j < NV; ++j)
@@ -188,6 +171,33 @@ __device__ __forceinline__ int wave_topk(const T *row, int E, int k, int &id, fl
             }
         }
     }
+}
+
+// Top-k of row[0, E) (E <= 64 NV). Returns the smallest index of a non-finite logit, or INT_MAX; when none, lanes
+// a < k hold the a-th pick (id) and its softmax weight over the k picks (coef). Order: larger logit first, on an exact
+// tie the lower expert index (wave_picks; scratch as there).
+template <typename T, int NV>
+__device__ __forceinline__ int wave_topk(const T *row, int E, int k, int &id, float &coef, uint2 *scratch = nullptr) {
+    const int lane = threadIdx.x % kWave;
+    uint32_t key[NV];
+    bool fin = true;
+    int bad = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int e = lane + j * kWave;
+        const float xv = e < E ? load_logit(row, e) : 0.0f;
+        const bool f = isfinite(xv);
+        if (e < E && !f && e < bad) bad = e;
+        fin = fin && f;
+        key[j] = e < E && f ? order_key(xv) : 0u;
+    }
+    if (__ballot(!fin) != 0) {  // rare: the smallest bad index
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) bad = min(bad, __shfl_xor(bad, off, kWave));
+        return bad;
+    }
+    uint32_t my_k, top;
+    wave_picks<NV>(key, k, scratch, id, my_k, top);
     const float ex = lane < k ? expf(key_value(my_k) - key_value(top)) : 0.f;
     coef = ex / wave_butterfly_sum(ex);
     return INT_MAX;
