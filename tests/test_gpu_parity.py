@@ -78,6 +78,14 @@ def test_moe_router_matches_oracle(E, k):
     lg[8, 1::2] = -0.0  # -0 and +0 compare equal: the lower index wins
     lg[9, :] = -1.0
     lg[9, E - 1] = lg[9, E // 2] = 3.0  # a tie between far-apart experts
+    # equal values straddling the k-th place (the candidate picks rank them by index): a few above, then 40 equal
+    # (at most 64 candidates), then 80 equal (more than 64: the rounds)
+    for r, n_eq in ((10, 40), (11, 80)):
+        lg[r, :] = -2.0
+        top = min(k - 1, 3)
+        lg[r, E - top:E] = 5.0
+        eq = rng.permutation(E - top)[:min(n_eq, E - top)]
+        lg[r, eq] = 1.0
     ids, coef, err = moe.moe_router(torch.from_numpy(lg).to(DEV), E, k, ld=E + 3)
     rids, rcoef, rerr = orc.topk(lg, E, k)
     assert np.array_equal(to_np(ids), rids)
