@@ -748,8 +748,10 @@ __global__ void __launch_bounds__(WB * kWave) decode_down_lds_kernel(DecodeArgs 
     if (gw < extra * (base + 1)) t = gw / (base + 1), r = gw % (base + 1), k = base + 1;
     else t = extra + (gw - extra * (base + 1)) / base, r = (gw - extra * (base + 1)) % base, k = base;
     const int32_t rbs = (int32_t)(a.N / 16);  // row blocks of an expert
-    const int32_t rb0 = r * rbs / k, rb1 = (r + 1) * rbs / k;
-    if (rb1 <= rb0) return;
+    // the tile's k waves interleave its row blocks (wave r: r, r + k, ...), so at any time they read one contiguous
+    // stretch of the expert's rows (measured on MI355X at cfg2: 29.0 us, a contiguous range a wave 29.4)
+    if (r >= rbs) return;
+    const int32_t nq = (rbs - r + k - 1) / k;
     const __amdgpu_buffer_rsrc_t rq = rsrc(a.q, a.q_bytes), rs = rsrc(a.scale, a.s_bytes),
                                  rm = rsrc(a.minv, a.s_bytes), rx = rsrc(a.x, a.x_bytes), ry = rsrc(a.y, a.y_bytes);
     const int64_t rec0 = route::t16_rec_at(a.S, a.E);
@@ -774,12 +776,13 @@ __global__ void __launch_bounds__(WB * kWave) decode_down_lds_kernel(DecodeArgs 
         loff[i] = (uint32_t)rr * 256u + (uint32_t)(((lane % 16) ^ rr) * 16);
     }
     const uint32_t row_e = expert * (uint32_t)a.N;  // the expert's first row
-    // unit rb0 + q into position P: four code loads and (lanes 0..31) the 16 rows' scale and min dwords; past rb1:
+    // unit q (row block r + q k) into position P: four code loads and (lanes 0..31) the 16 rows' scale and min dwords;
+    // past the expert's rows:
     // offsets past the ends
     auto issue = [&](int32_t q, auto P) __attribute__((always_inline)) {
         uint4 *R = ring(P);
-        const int32_t rb = rb0 + q;
-        const bool valid = rb < rb1;
+        const int32_t rb = r + q * k;
+        const bool valid = rb < rbs;
         const uint32_t row0 = row_e + 16u * (uint32_t)rb;
 #pragma unroll
         for (int i = 0; i < 4; ++i) lds_load16(rq, R + i * kWave, valid ? row0 * 256u + loff[i] : a.q_bytes, 0);
@@ -791,7 +794,7 @@ __global__ void __launch_bounds__(WB * kWave) decode_down_lds_kernel(DecodeArgs 
                                                      0, 0);
         }
     };
-    const int32_t nq = rb1 - rb0, nq_pad = (nq + NS - 1) / NS * NS;
+    const int32_t nq_pad = (nq + NS - 1) / NS * NS;
     ring_for<0, NS - 1>([&](auto Q) { issue(decltype(Q)::value, Q); });
     // A fragments and the per-group sums of the tile rows (lane (g, j): slots 4 g + i) from an MFMA against ones
     Frag hf[KS][4];
@@ -840,13 +843,13 @@ __global__ void __launch_bounds__(WB * kWave) decode_down_lds_kernel(DecodeArgs 
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] = fmaf(sc, d[i], fmaf(mn, hs[s][i], acc[i]));
         }
-        // partial[slot 4 g + i][16 rb + j] (a unit past rb1 or a slot -1: past the end, nothing written)
-        const int32_t rb = rb0 + q;
+        // partial[slot 4 g + i][16 rb + j] (a unit past the rows or a slot -1: past the end, nothing written)
+        const int32_t rb = r + q * k;
         const uint32_t col = (16u * (uint32_t)rb + (uint32_t)j) * 4u;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(nan ? qnan() : acc[i]), ry,
-                                                  rb < rb1 && orow[i] != a.y_bytes ? orow[i] + col : a.y_bytes, 0, 0);
+                                                  rb < rbs && orow[i] != a.y_bytes ? orow[i] + col : a.y_bytes, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
     };
     for (int32_t q = 0; q < nq_pad; q += NS)  // whole trips: no branch between the steps
