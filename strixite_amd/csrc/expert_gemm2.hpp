@@ -21,7 +21,8 @@
 // The k order of an MFMA operand: lane half h takes k 32 h .. 32 h + 31 of a chunk and K step ks the 8 at
 // 32 h + 8 ks, whose 8 halves hold k = 0, 4, 1, 5, 2, 6, 3, 7 of that block (the paired order), for the activations
 // and the weights alike (an MFMA sums over k in any order both operands share). In that order a dword of 8 Q4 codes
-// (code i at bits 4 i) gives each F16 pair in one and-or: pair j = bits 4 j and 16 + 4 j.
+// (code i at bits 4 i) gives each F16 pair in one and-or: pair j = bits 4 j and 16 + 4 j (pairs 2 and 3 after one
+// shift by 8).
 #pragma once
 
 namespace g2 {
@@ -53,16 +54,22 @@ __device__ __forceinline__ uint32_t pk_f16_rtz(float a, float b) {
 // position of k (0..7) of an 8-element block in the paired order
 __host__ __device__ constexpr int paired_pos(int k) { return (k % 4) * 2 + k / 4; }
 
-// 8 Q4 codes -> F16 code * s + m (one F16 FMA each) in the paired order. A code n under the F16 exponent of 1024
-// (bias = 0x64006400: 0x6400 | n = 1024 + n exactly) loses 1024 exactly, then the FMA rounds once.
-__device__ __forceinline__ Frag q4_dequant_f16(uint32_t w, f16x2v s, f16x2v m, uint32_t bias) {
-    const f16x2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+// 8 Q4 codes -> F16 code * s + m (one F16 FMA each) in the paired order. Pair j's codes sit at bits 4 j and 16 + 4 j
+// of the dword. Under an F16 exponent whose mantissa step is 1 the code is exact above the exponent's value: a code n
+// in mantissa bits 0..3 under 0x6400 (1024, step 1) reads 1024 + n, and in bits 4..7 under 0x5400 (64, step 1/16)
+// reads 64 + n, so pairs 0 and 1 come from w and pairs 2 and 3 from w >> 8 without further shifts. Subtracting
+// 1024 or 64 is exact; the FMA rounds once. b64 / b54: 0x64006400 / 0x54005400, in VGPRs (the and-or then takes
+// its mask as its one scalar operand).
+__device__ __forceinline__ Frag q4_dequant_f16(uint32_t w, f16x2v s, f16x2v m, uint32_t b64, uint32_t b54) {
+    const f16x2v k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
+    const uint32_t w8 = w >> 8;
+    const uint32_t c[4] = {(w & 0x000F000Fu) | b64, (w & 0x00F000F0u) | b54, (w8 & 0x000F000Fu) | b64,
+                           (w8 & 0x00F000F0u) | b54};
     Frag f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t c = ((w >> (4 * j)) & 0x000F000Fu) | bias;
-        f.d[j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2v, c) - k1024, s, m));
-    }
+    for (int j = 0; j < 4; ++j)
+        f.d[j] = __builtin_bit_cast(
+            uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2v, c[j]) - (j % 2 ? k64 : k1024), s, m));
     return f;
 }
 
@@ -154,8 +161,9 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     int aofs[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) aofs[ks] = l32 * 8 + ((4 * h + ks) ^ (l32 & 7));
-    uint32_t bias;  // in a VGPR, so the and-or takes the mask as its one scalar operand
-    asm("v_mov_b32 %0, 0x64006400" : "=v"(bias));
+    uint32_t b64, b54;  // in VGPRs, so the and-or takes the mask as its one scalar operand
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(b64));
+    asm("v_mov_b32 %0, 0x54005400" : "=v"(b54));
 
     // Loads past the last chunk read in-bounds or zero data that is never used. X16: every chunk issues the same
     // loads in the same order (scales at a group's first chunk, then codes and activations two chunks ahead), so the
@@ -254,7 +262,8 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                     if (ks + 1 < 4) read_a(ks + 1, af[(ks + 1) & 1]);
                     const uint32_t cw0 = ks == 0 ? q[0].x : ks == 1 ? q[0].y : ks == 2 ? q[0].z : q[0].w;
                     const uint32_t cw1 = ks == 0 ? q[1].x : ks == 1 ? q[1].y : ks == 2 ? q[1].z : q[1].w;
-                    const Frag b0 = q4_dequant_f16(cw0, sc[0], mn[0], bias), b1 = q4_dequant_f16(cw1, sc[1], mn[1], bias);
+                    const Frag b0 = q4_dequant_f16(cw0, sc[0], mn[0], b64, b54),
+                               b1 = q4_dequant_f16(cw1, sc[1], mn[1], b64, b54);
 #pragma unroll
                     for (int i = 0; i < NT; ++i) {
                         acc[i][0] = mfma32_f16(af[ks & 1][i], b0, acc[i][0]);
