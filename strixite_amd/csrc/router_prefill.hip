@@ -5,8 +5,8 @@
 // order (lane l of a wave64 takes the 8-element chunks l, l + 64, ... with fmaf, then a butterfly over the 64 lanes;
 // oracle: orc_router_logits). That order does not map onto MFMA, and at 4096 tokens x 513 rows x 3072 the VALU form
 // costs ~0.3 ms. So the projection runs in two passes:
-//   1. approx: logits a = x . w^T with bf16 MFMA (FP32 accumulation, any internal order), and the 2-norms |x_m|,
-//      |w_e|. For ANY order of summing the K exact bf16 x bf16 products in FP32 - rounded to nearest or toward zero,
+//   1. approx: logits a = x . w^T with bf16 MFMA (FP32 accumulation, any internal order), and the 2-norms |w_e|
+//      (|x_m| comes from pass 2, which loads the token's row). For ANY order of summing the K exact bf16 x bf16 products in FP32 - rounded to nearest or toward zero,
 //      FP32 denormals kept or flushed - the result differs from the exact sum by at most (2K u) S + K 2^-125 with
 //      u = 2^-24 and S = sum_k |x_k w_k| <= |x| |w| (Cauchy-Schwarz). Both the canonical and the MFMA sums obey it, so
 //      |a - c| <= delta = (4K + 64) u |x| |w| + K 2^-124 (norms rounded up).
@@ -31,8 +31,9 @@ using namespace strix::dev;
 constexpr int kWave = 64, kThreads = 256;
 
 
-// ---- pass 1: approximate logits + norms -----------------------------------------------------------------------------
-// Only the E routed rows (the shared gate row is computed exactly by pass 2). Block tile 128 tokens x 128 rows, K in
+// ---- pass 1: approximate logits + router row norms ------------------------------------------------------------------
+// Only the E routed rows (the shared gate row is computed exactly by pass 2). kNormRows extra rows of blocks (grid y)
+// only sum the squares of the router rows, so the GEMM blocks carry no norm work. Block tile 128 tokens x 128 rows, K in
 // steps of 64 through LDS (rows padded to 144 bytes: the 16 lanes of a fragment read hit 16 distinct 16-byte bank
 // groups); wave w computes tokens 64 (w / 2) .. + 63 x rows 64 (w % 2) .. + 63 as 4 x 4 v_mfma_f32_16x16x32_bf16
 // tiles whose A and B fragments are both 16-byte row segments (x rows for tokens, w rows for experts). The next K
@@ -41,7 +42,7 @@ constexpr int kWave = 64, kThreads = 256;
 // which the large tiles keep to 4 reads of x and 32 of w at E 512, M 4096).
 // (parts: 1, 2, 4 measured 139, 122, 124 us for both passes at 4096 x 512 x 3072 on MI355X - more parts shorten this
 // pass but their partial logits push the router rows out of L2 before pass 2 re-reads them)
-constexpr int kBM = 128, kBN = 128, kBK = 64, kLd = kBK + 8, kParts = 2;
+constexpr int kBM = 128, kBN = 128, kBK = 64, kLd = kBK + 8, kParts = 2, kNormRows = kBN / 16;
 
 __device__ __forceinline__ float sumsq8(const uint4 &v) {
     const uint32_t d[4] = {v.x, v.y, v.z, v.w};
@@ -57,18 +58,37 @@ __device__ __forceinline__ float sumsq8(const uint4 &v) {
 
 __global__ void __launch_bounds__(kThreads)
     router_approx_kernel(const uint16_t *x, const uint16_t *w, float *a_out, int64_t ld, int64_t M, int64_t N,
-                         int64_t K, float *nx, float *nw) {
+                         int64_t K, float *nw) {
     __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLd], Bs[kBN * kLd];
     // K part blockIdx.z of gridDim.z: its sums go to part z of the outputs ([parts][M][ld], [parts][M], [parts][N])
     const int64_t kp = K / gridDim.z, kbeg = kp * blockIdx.z, kend = kbeg + kp;
-    a_out += (int64_t)blockIdx.z * M * ld, nx += (int64_t)blockIdx.z * M, nw += (int64_t)blockIdx.z * N;
+    a_out += (int64_t)blockIdx.z * M * ld, nw += (int64_t)blockIdx.z * N;
     const int t = threadIdx.x, lane = t % kWave, wave = t / kWave, g = lane / 16, j = lane % 16;
     const int wm = 64 * (wave / 2), wn = 64 * (wave % 2);
     const int64_t n0 = (int64_t)blockIdx.x * kBN, m0 = (int64_t)blockIdx.y * kBM;
     // staging: chunk u covers row (t >> 3) + 32 u, 16 bytes at column 8 (t & 7), of A and of B
     const int sr = t >> 3, sc = (t & 7) * 8;
+    const int64_t gemm_rows = (int64_t)gridDim.y - kNormRows;
+    if ((int64_t)blockIdx.y >= gemm_rows) {
+        // the last kNormRows rows of blocks: the squared norms of the router rows over this K part, 16 rows a block
+        // (16 threads a row, each summing every 16th 16-byte piece; the tokens' norms come from the select pass,
+        // which loads each token's whole row anyway)
+        const int64_t c = n0 + 16 * (blockIdx.y - gemm_rows) + t / 16;
+        float q = 0.f;
+        if (c < N) {
+            const uint4 *wr = reinterpret_cast<const uint4 *>(w + c * K + kbeg);
+            const int n16 = (int)(kp / 8);
+#pragma unroll 12
+            for (int i = t % 16; i < n16; i += 16) q += sumsq8(wr[i]);
+        }
+        q += __shfl_xor(q, 1, kWave);
+        q += __shfl_xor(q, 2, kWave);
+        q += __shfl_xor(q, 4, kWave);
+        q += __shfl_xor(q, 8, kWave);
+        if (t % 16 == 0 && c < N) nw[c] = q;
+        return;
+    }
     uint4 ra[4], rb[4];
-    float qa[4] = {0, 0, 0, 0}, qb[4] = {0, 0, 0, 0};
     auto load = [&](int64_t k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -88,8 +108,6 @@ __global__ void __launch_bounds__(kThreads)
         for (int u = 0; u < 4; ++u) {
             *reinterpret_cast<uint4 *>(&As[(sr + 32 * u) * kLd + sc]) = ra[u];
             *reinterpret_cast<uint4 *>(&Bs[(sr + 32 * u) * kLd + sc]) = rb[u];
-            qa[u] += sumsq8(ra[u]);
-            qb[u] += sumsq8(rb[u]);
         }
         __syncthreads();
         if (k0 + kBK < kend) load(k0 + kBK);
@@ -123,20 +141,6 @@ __global__ void __launch_bounds__(kThreads)
                 const int64_t m = m0 + wm + 16 * a + 4 * g + r, n = n0 + wn + 16 * b + j;
                 if (m < M && n < N) a_out[m * ld + n] = acc[a][b][r];
             }
-    // squared norms of this K part: the 8 threads staging a row meet
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        float q = qa[u], p = qb[u];
-        q += __shfl_xor(q, 1, kWave);
-        q += __shfl_xor(q, 2, kWave);
-        q += __shfl_xor(q, 4, kWave);
-        p += __shfl_xor(p, 1, kWave);
-        p += __shfl_xor(p, 2, kWave);
-        p += __shfl_xor(p, 4, kWave);
-        const int64_t r = m0 + sr + 32 * u, c = n0 + sr + 32 * u;
-        if (blockIdx.x == 0 && (t & 7) == 0 && r < M) nx[r] = q;
-        if (blockIdx.y == 0 && (t & 7) == 0 && c < N) nw[c] = p;
-    }
 }
 
 // ---- pass 2: select -------------------------------------------------------------------------------------------------
@@ -159,11 +163,11 @@ __device__ __forceinline__ float lane_chain(const uint4 (&xr)[NCH], const uint4 
 }
 
 // One wave per token. parts: the approx pass's K parts [kParts][M][ld] (part 0 is the layer's logits buffer: the
-// exact values are written there); nx2 / nw2: the parts' squared norms.
+// exact values are written there); nw2: the parts' squared norms of the router rows.
 template <int NV, int NCH>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     router_select_kernel(const uint16_t *x, const uint16_t *w, const float *bias, float *logits, int64_t ld,
-                         int64_t M, int E, int k, bool shared, bool shared_slot, const float *nx2, const float *nw2,
+                         int64_t M, int E, int k, bool shared, bool shared_slot, const float *nw2,
                          int32_t *ids, float *coef, uint32_t *err) {
     __shared__ int cand_lds[kThreads / kWave][1040];  // a wave's candidate list (at most E + 1 <= 1025)
     __shared__ uint2 pick_lds[kThreads / kWave][topk::kCandScratch];  // the picks' scratch (topk::wave_picks)
@@ -177,9 +181,12 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     uint4 xr[NCH];
 #pragma unroll
     for (int i = 0; i < NCH; ++i) xr[i] = *reinterpret_cast<const uint4 *>(xm + (lane + i * kWave) * 8);
+    // the token's squared norm from the row just loaded (any FP32 order is within the bound's allowance)
     float q = 0.f;
 #pragma unroll
-    for (int p = 0; p < kParts; ++p) q += nx2[p * M + m];
+    for (int i = 0; i < NCH; ++i) q += sumsq8(xr[i]);
+#pragma unroll
+    for (int s = 1; s < kWave; s *= 2) q += __shfl_xor(q, s, kWave);
     constexpr float up = 1.0f + 1.0f / 256;  // the FP32 sums of squares are within 2^-10 of the exact ones
     const float nxm = sqrtf(q) * up;
     float va[NV], dl[NV];
@@ -306,16 +313,16 @@ bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int
     if (H % 512 != 0 || nch < 1 || nch > 8 || E > 1024 || k > 32 || k > E || (H / kParts) % kBK != 0 ||
         reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
         return false;
-    float *nx = norms, *nw = norms + (int64_t)kParts * M;
-    dim3 g1((unsigned)((E + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM), (unsigned)kParts);
+    float *nw = norms + (int64_t)kParts * M;  // (the first kParts * M floats: unused)
+    // kNormRows more rows of blocks for the router rows' norms
+    dim3 g1((unsigned)((E + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM + kNormRows), (unsigned)kParts);
     STRIX_CHECK(g1.y <= 65535, "moe_router_prefill: M = ", M, " too large");
-    router_approx_kernel<<<g1, kThreads, 0, stream>>>(static_cast<const uint16_t *>(x), w, logits, ld, M, E, H, nx,
-                                                       nw);
+    router_approx_kernel<<<g1, kThreads, 0, stream>>>(static_cast<const uint16_t *>(x), w, logits, ld, M, E, H, nw);
     const unsigned g2 = (unsigned)((M + 3) / 4);
     const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
     auto go = [&](auto nvc, auto nchc) {
         router_select_kernel<decltype(nvc)::value, decltype(nchc)::value><<<g2, kThreads, 0, stream>>>(
-            static_cast<const uint16_t *>(x), w, bias, logits, ld, M, (int)E, (int)k, shared, shared && shared_slot, nx, nw,
+            static_cast<const uint16_t *>(x), w, bias, logits, ld, M, (int)E, (int)k, shared, shared && shared_slot, nw,
             ids, coef, err);
     };
     auto by_nch = [&](auto nvc) {
