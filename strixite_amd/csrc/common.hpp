@@ -25,10 +25,12 @@ void moe_topk_group_routes_small(const float *logits, int64_t ld, int64_t M, int
 // optional FP32 bias) and top-k with the canonical order's exact routing via bf16 MFMA plus exact recomputation of the
 // candidates. logits: [4][M][E (+1)] floats (the layer's logits are part 0); norms: 4 (M + E (+1)) floats of
 // scratch. shared_slot (with shared): the shared expert routed as slot k of every token (id E, coefficient
-// sigmoid(its gate logit)): ids / coef [M, k + 1]. Returns false (nothing launched) for shapes it does not take.
+// sigmoid(its gate logit)): ids / coef [M, k + 1]. x16 (optional): x [M, H] also written as F16 (toward zero) in the
+// paired k order of every 8 elements, the prefill expert GEMM's input. Returns false (nothing launched) for shapes it
+// does not take.
 bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
                         int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
-                        hipStream_t stream, bool shared_slot = false);
+                        hipStream_t stream, bool shared_slot = false, void *x16 = nullptr);
 }  // namespace kernels
 
 // ---- host-side checks -----------------------------------------------------------------------------------------

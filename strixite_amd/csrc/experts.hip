@@ -1737,16 +1737,30 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         if (ctx != nullptr) STRIX_HIP_CHECK(hipEventRecord(ctx->join, ctx->s), fn, ": join");
     }
 
+    const bool q8 = w.gate_up_bits == 8;
+    // Q4 experts at prefill sizes run the reference's F16 math (MoeMath::WmmaF16): x converted to F16 once, h kept
+    // in F16 (the F16 form of its BF16 rounding), both in the GEMM's paired k order, and the down's partials stored in
+    // BF16 (strixite kernels/moe_grouped.hpp:84)
+    GemmArgs gu2 = make_args(qv(w.gate_up), Es, base + L.x16, h, I);
+    gu2.A = A, gu2.ws = static_cast<const int32_t *>(route), gu2.S = M * A;
+    GemmArgs dn2 = make_args(qv(w.down), Es, h, partial, H);
+    dn2.A = A, dn2.ws = static_cast<const int32_t *>(route), dn2.S = M * A;
+    const bool f16p = !q8 && !fold && use_expert_gemm(M * A, Es, H, w.gate_up.G) &&
+                      use_expert_gemm(M * A, Es, I, w.down.G) && expert_gemm2_fits<EPI_SWIGLU>(gu2) &&
+                      expert_gemm2_fits<EPI_BF16>(dn2) && H % 8 == 0 && I % 8 == 0;
     // router projection (+ harness bias) and top-k
     const float *lg = logits_in;
+    bool x16_done = false;  // x in the F16 GEMM's input form already written (by the prefill router)
     bool routed = false;  // ids and coef already written (the prefill router selects as it projects)
     bool fused = false;   // and the routes packed (the decode routing launch)
     if (!lg) {
         lg = logits;
         // prefill sizes: bf16 MFMA projection + exact recomputation of the candidates (the same routing bits)
+        // (with the F16-math experts it also writes x in their F16 input form, which saves the conversion launch)
         routed = M >= 256 && moe_router_prefill(x, w.router, w.router_bias, M, H, E, k, w.has_shared || stacked, logits,
                                                 reinterpret_cast<float *>(base + L.norms), ids, coef, err_router,
-                                                stream, stacked);
+                                                stream, stacked, f16p ? base + L.x16 : nullptr);
+        x16_done = routed && f16p;
         // decode sizes: router projection, top-k and packing in one launch, when asked for (STRIX_FUSED_ROUTE=1).
         // Off by default: measured on MI355X at 16 tokens, H 3072, 513 router rows, it takes 24.9 us against 6.0 +
         // 11.9 us for the two launches (the top-k cannot start before the last router block, and the router's waves
@@ -1786,23 +1800,12 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         moe_group_routes(ids, M, A, Es, route, L.route_bytes, err_expert, stream);
     }
     // routed experts: gate_up + SwiGLU -> h, down -> partial
-    const bool q8 = w.gate_up_bits == 8;
     const Q8DeviceView gu8{w.gate_up.q, w.gate_up.scale, w.gate_up.minv, w.gate_up.N, w.gate_up.K, w.gate_up.G};
     const Q8DeviceView dn8{w.down.q, w.down.scale, w.down.minv, w.down.N, w.down.K, w.down.G};
-    // Q4 experts at prefill sizes run the reference's F16 math (MoeMath::WmmaF16): x converted to F16 once, h kept
-    // in F16 (the F16 form of its BF16 rounding), both in the GEMM's paired k order, and the down's partials stored in
-    // BF16 (strixite kernels/moe_grouped.hpp:84)
-    GemmArgs gu2 = make_args(qv(w.gate_up), Es, base + L.x16, h, I);
-    gu2.A = A, gu2.ws = static_cast<const int32_t *>(route), gu2.S = M * A;
-    GemmArgs dn2 = make_args(qv(w.down), Es, h, partial, H);
-    dn2.A = A, dn2.ws = static_cast<const int32_t *>(route), dn2.S = M * A;
-    const bool f16p = !q8 && !fold && use_expert_gemm(M * A, Es, H, w.gate_up.G) &&
-                      use_expert_gemm(M * A, Es, I, w.down.G) && expert_gemm2_fits<EPI_SWIGLU>(gu2) &&
-                      expert_gemm2_fits<EPI_BF16>(dn2) && H % 8 == 0 && I % 8 == 0;
     // otherwise h in bf16: the oracle's rounding of silu(g) * u, with bf16's range
     if (f16p) {
         check_grouped(fn, x, qv(w.gate_up), Es, route, L.route_bytes, M, A, h, Act::BF16, M * A * I * 2, M);
-        bf16_to_f16_paired(x, base + L.x16, M, H, stream);
+        if (!x16_done) bf16_to_f16_paired(x, base + L.x16, M, H, stream);
         STRIX_CHECK((launch_expert_gemm2<EPI_SWIGLU, true, g2::H_F16P, true>(gu2, stream)), fn, ": F16 gate_up");
     } else if (fold) {
         const QV gv = q8 ? qv(gu8) : qv(w.gate_up);

@@ -168,7 +168,7 @@ template <int NV, int NCH>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     router_select_kernel(const uint16_t *x, const uint16_t *w, const float *bias, float *logits, int64_t ld,
                          int64_t M, int E, int k, bool shared, bool shared_slot, const float *nw2,
-                         int32_t *ids, float *coef, uint32_t *err) {
+                         int32_t *ids, float *coef, uint32_t *err, uint4 *x16) {
     __shared__ int cand_lds[kThreads / kWave][1040];  // a wave's candidate list (at most E + 1 <= 1025)
     __shared__ uint2 pick_lds[kThreads / kWave][topk::kCandScratch];  // the picks' scratch (topk::wave_picks)
     const int lane = threadIdx.x % kWave;
@@ -181,6 +181,17 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     uint4 xr[NCH];
 #pragma unroll
     for (int i = 0; i < NCH; ++i) xr[i] = *reinterpret_cast<const uint4 *>(xm + (lane + i * kWave) * 8);
+    if (x16 != nullptr) {  // the row as F16 toward zero, each 8-element block in the paired order k0 k4 k1 k5 ..
+        auto lo = [](uint32_t d) { return __uint_as_float(d << 16); };
+        auto hi = [](uint32_t d) { return __uint_as_float(d & 0xFFFF0000u); };
+        auto pk = [](float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); };
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const uint4 v = xr[i];
+            x16[m * (K / 8) + lane + i * kWave] =
+                make_uint4(pk(lo(v.x), lo(v.z)), pk(hi(v.x), hi(v.z)), pk(lo(v.y), lo(v.w)), pk(hi(v.y), hi(v.w)));
+        }
+    }
     // the token's squared norm from the row just loaded (any FP32 order is within the bound's allowance)
     float q = 0.f;
 #pragma unroll
@@ -308,7 +319,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 
 bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
                         int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
-                        hipStream_t stream, bool shared_slot) {
+                        hipStream_t stream, bool shared_slot, void *x16) {
     const int64_t nch = H / 512, ld = E + (shared ? 1 : 0);
     if (H % 512 != 0 || nch < 1 || nch > 8 || E > 1024 || k > 32 || k > E || (H / kParts) % kBK != 0 ||
         reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
@@ -323,7 +334,7 @@ bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int
     auto go = [&](auto nvc, auto nchc) {
         router_select_kernel<decltype(nvc)::value, decltype(nchc)::value><<<g2, kThreads, 0, stream>>>(
             static_cast<const uint16_t *>(x), w, bias, logits, ld, M, (int)E, (int)k, shared, shared && shared_slot, nw,
-            ids, coef, err);
+            ids, coef, err, static_cast<uint4 *>(x16));
     };
     auto by_nch = [&](auto nvc) {
         switch (nch) {
