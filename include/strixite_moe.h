@@ -146,6 +146,13 @@ int strix_moe_layer_forward(const strix_moe_layer_weights *w, const void *x, int
 /* strixite kernels/hc.hpp:51-55 hc_inject: x[t, s d + j] = stored(fma(w_in[t, s], y[t, j], x[...])) in place */
 int strix_hc_inject(void *x, const float *w_in, const void *y, int64_t T, int64_t H, int64_t d, int act,
                     void *stream);
+/* strixite kernels/hc.hpp:31-36 hc_mix_down (bits 4 or 8: the Q4 / Q8 overload; w row-major, folded): inv [T, H],
+ * h [T, r] = silu(a / H), w_in [T, H] = 2 sigmoid(a / H) when inject (w_in null iff !inject) */
+int strix_hc_mix_down(const void *x, const strix_qview *w, int bits, int64_t T, int64_t H, int64_t d, int64_t r,
+                      int inject, float eps, float *h, float *w_in, float *inv, int act, void *stream);
+/* strixite kernels/hc.hpp:38-50 hc_mix_up (bits 4 or 8; w_up chunk-major [H d, r]): u [T, d] */
+int strix_hc_mix_up(const float *h, const strix_qview *w_up, int bits, const void *x, const float *norm_w,
+                    const float *inv, int64_t T, int64_t H, int64_t d, void *u, int act, void *stream);
 
 /* No counterpart in the reference: strix_moe_layer_forward for callers that cannot allocate (graph capture, serving
  * loops, harnesses that forbid hipMalloc). Its scratch is a fixed 16 MiB device array per device, held until the

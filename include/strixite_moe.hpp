@@ -45,9 +45,24 @@ void moe_shared_add_inject(void *y, const void *s, const float *gate_logit, int6
 
 // ---- residual injection: strixite kernels/hc.hpp:51-55 -----------------------------------------------------------
 // In place: x[t, s d + j] = stored(fma(w_in[t, s], y[t, j], x[t, s d + j])), one rounding per element; y must not
-// overlap x. (The rest of kernels/hc.hpp, the hc_mix projections, is not part of this library.)
+// overlap x.
 void hc_inject(void *x, const float *w_in, const void *y, int64_t T, int64_t H, int64_t d, Act act,
                hipStream_t stream);
+
+// ---- hyper-connection mix, the step that produces the sublayer's input: strixite kernels/hc.hpp:31-50 -----------
+// X [T, H d] (H = 4 streams) -> inv [T, H] = 1 / sqrt(mean(X_s^2) + eps), a = sum_s inv_s (W_s . X_s) for the rows of
+// the folded w [r (+ H), H d], h [T, r] = silu(a / H), w_in [T, H] = 2 sigmoid(a / H) for the H injection rows (when
+// inject; w_in null iff !inject). FP32 inside; d % 32 == 0; x 16-byte aligned.
+void hc_mix_down(const void *x, const Q4DeviceView &w, int64_t T, int64_t H, int64_t d, int64_t r, bool inject,
+                 float eps, float *h, float *w_in, float *inv, Act act, hipStream_t stream);
+void hc_mix_down(const void *x, const Q8DeviceView &w, int64_t T, int64_t H, int64_t d, int64_t r, bool inject,
+                 float eps, float *h, float *w_in, float *inv, Act act, hipStream_t stream);
+// u[t, j] = (1/H) sum_s sigmoid(W_up[s d + j] . h[t]) * (X[t, s d + j] * inv[t, s] * (1 + norm_w[s d + j])), W_up
+// [H d, r] chunk-major, r % 32 == 0, r <= 1024; u [T, d] in the activation dtype, rounded once.
+void hc_mix_up(const float *h, const Q4ChunkMajorView &w_up, const void *x, const float *norm_w, const float *inv,
+               int64_t T, int64_t H, int64_t d, void *u, Act act, hipStream_t stream);
+void hc_mix_up(const float *h, const Q8ChunkMajorView &w_up, const void *x, const float *norm_w, const float *inv,
+               int64_t T, int64_t H, int64_t d, void *u, Act act, hipStream_t stream);
 
 // ---- grouping: strixite kernels/moe_grouped.hpp:46-54 ----------------------------------------------------------
 // ws (int32): [n_tiles, S, E, n_wide_tiles], offsets [E + 2] at ws + 4 (bucket b's slots at slots[offsets[b] ..

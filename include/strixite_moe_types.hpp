@@ -37,6 +37,21 @@ struct Q8DeviceView {
     const uint16_t *minv = nullptr;
     int64_t N = 0, K = 0, G = 0;
 };
+// strixite runtime/q4_device.hpp:37-43, runtime/q8_device.hpp:36-42: the same codes, scales and mins laid out
+// chunk-major (formats/q4.hpp:43-55): 32-code chunk c of row n at q[(c N + n) * 16] (Q4) or [(c N + n) * 32] (Q8),
+// group g's scale / min at [g N + n].
+struct Q4ChunkMajorView {
+    const uint8_t *q = nullptr;
+    const uint16_t *scale = nullptr;
+    const uint16_t *minv = nullptr;
+    int64_t N = 0, K = 0, G = 0;
+};
+struct Q8ChunkMajorView {
+    const uint8_t *q = nullptr;
+    const uint16_t *scale = nullptr;
+    const uint16_t *minv = nullptr;
+    int64_t N = 0, K = 0, G = 0;
+};
 
 namespace kernels {
 

@@ -89,6 +89,8 @@ _SIGS = {
     "strix_moe_layer_forward": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _sz, _p, _p, _p,
                                        C.POINTER(InjectArgs)]),
     "strix_hc_inject": (_int, [_p, _p, _p, _i64, _i64, _i64, _int, _p]),
+    "strix_hc_mix_down": (_int, [_p, _p, _int, _i64, _i64, _i64, _i64, _int, C.c_float, _p, _p, _p, _int, _p]),
+    "strix_hc_mix_up": (_int, [_p, _p, _int, _p, _p, _p, _i64, _i64, _i64, _p, _int, _p]),
     "strix_strixw_hash64": (_u64, [_p, _sz]),
     "strix_strixw_open": (_int, [C.c_char_p, C.POINTER(_p)]),
     "strix_strixw_close": (_int, [_p]),

@@ -262,6 +262,30 @@ int strix_hc_inject(void *x, const float *w_in, const void *y, int64_t T, int64_
     return guard([&] { strix::kernels::hc_inject(x, w_in, y, T, H, d, act_of(act), st(stream)); });
 }
 
+int strix_hc_mix_down(const void *x, const strix_qview *w, int bits, int64_t T, int64_t H, int64_t d, int64_t r,
+                      int inject, float eps, float *h, float *w_in, float *inv, int act, void *stream) {
+    return guard([&] {
+        STRIX_CHECK(w != nullptr && (bits == 4 || bits == 8), "strix_hc_mix_down: null view or bits = ", bits);
+        if (bits == 4)
+            strix::kernels::hc_mix_down(x, q4(w), T, H, d, r, inject != 0, eps, h, w_in, inv, act_of(act), st(stream));
+        else
+            strix::kernels::hc_mix_down(x, q8(w), T, H, d, r, inject != 0, eps, h, w_in, inv, act_of(act), st(stream));
+    });
+}
+int strix_hc_mix_up(const float *h, const strix_qview *w_up, int bits, const void *x, const float *norm_w,
+                    const float *inv, int64_t T, int64_t H, int64_t d, void *u, int act, void *stream) {
+    return guard([&] {
+        STRIX_CHECK(w_up != nullptr && (bits == 4 || bits == 8), "strix_hc_mix_up: null view or bits = ", bits);
+        if (bits == 4) {
+            const strix::Q4ChunkMajorView v{w_up->q, w_up->scale, w_up->minv, w_up->N, w_up->K, w_up->G};
+            strix::kernels::hc_mix_up(h, v, x, norm_w, inv, T, H, d, u, act_of(act), st(stream));
+        } else {
+            const strix::Q8ChunkMajorView v{w_up->q, w_up->scale, w_up->minv, w_up->N, w_up->K, w_up->G};
+            strix::kernels::hc_mix_up(h, v, x, norm_w, inv, T, H, d, u, act_of(act), st(stream));
+        }
+    });
+}
+
 int64_t strix_moe_layer_noalloc_max_bytes(void) { return (int64_t)strix::moe_layer_noalloc_max_bytes(); }
 int strix_moe_layer_forward_noalloc(const strix_moe_layer_weights *w, const void *x, int64_t M,
                                     const float *logits_in, void *y, void *x_out, int32_t *ids, float *coef,

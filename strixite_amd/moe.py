@@ -419,3 +419,30 @@ class MoeLayer:
                                                 _p(out["err"]), _stream(), ctx.handle if ctx is not None else None,
                                                 C.byref(inj) if inj is not None else None))
         return out
+
+
+# ---- hyper-connection mix: strixite kernels/hc.hpp:31-50 ----------------------------------------------------------
+def hc_mix_down(x: torch.Tensor, w: QWeight, r: int, inject: bool, eps: float):
+    """strixite kernels/hc.hpp:31-36: x [T, 4 d] (F32 or BF16) with the folded w [r (+ 4), 4 d] (row-major Q4 / Q8)
+    -> (h [T, r], w_in [T, 4] or None, inv [T, 4]), FP32."""
+    T, Hd = x.shape
+    H = 4
+    h = torch.empty((T, r), dtype=torch.float32, device=x.device)
+    w_in = torch.empty((T, H), dtype=torch.float32, device=x.device) if inject else None
+    inv = torch.empty((T, H), dtype=torch.float32, device=x.device)
+    v = w.view()
+    L.check(L.lib().strix_hc_mix_down(_p(x), C.byref(v), w.bits, T, H, Hd // H, r, int(inject), eps, _p(h), _p(w_in),
+                                      _p(inv), _act(x), _stream()))
+    return h, w_in, inv
+
+
+def hc_mix_up(h: torch.Tensor, w_up: QWeight, x: torch.Tensor, norm_w: torch.Tensor, inv: torch.Tensor) -> torch.Tensor:
+    """strixite kernels/hc.hpp:38-50: w_up [4 d, r] in the chunk-major layout (the QWeight's arrays hold it) -> u
+    [T, d] in x's dtype."""
+    T, Hd = x.shape
+    H = 4
+    u = torch.empty((T, Hd // H), dtype=x.dtype, device=x.device)
+    v = w_up.view()
+    L.check(L.lib().strix_hc_mix_up(_p(h), C.byref(v), w_up.bits, _p(x), _p(norm_w), _p(inv), T, H, Hd // H, _p(u),
+                                    _act(x), _stream()))
+    return u

@@ -92,7 +92,7 @@ def test_host_error_words_report_like_the_reference():
 
 REF = "/root/reference"
 REF_HEADERS = ["kernels/moe_router.hpp", "kernels/moe_grouped.hpp", "kernels/linear_q4.hpp", "kernels/swiglu.hpp",
-               "kernels/linear_q8.hpp", "kernels/linear.hpp"]
+               "kernels/linear_q8.hpp", "kernels/linear.hpp", "kernels/hc.hpp"]
 # reference declarations in those headers this library does not define (the Q5 expert format, optional in the
 # reference's interface and absent from its served layout)
 NOT_BUILT = {"linear_q5_experts_gather", "linear_q5_experts_combine", "linear_q5_experts_gather_swiglu",
@@ -103,7 +103,8 @@ _TYPES = {"int64_t": "long", "int32_t": "int", "uint32_t": "unsigned int", "uint
           "uint8_t": "unsigned char", "size_t": "unsigned long", "hipStream_t": "ihipStream_t*",
           "Act": "strix::kernels::Act", "MoeMath": "strix::kernels::MoeMath",
           "MoeSharedAdd": "strix::kernels::MoeSharedAdd", "Q4DeviceView": "strix::Q4DeviceView",
-          "Q5DeviceView": "strix::Q5DeviceView", "Q8DeviceView": "strix::Q8DeviceView"}
+          "Q5DeviceView": "strix::Q5DeviceView", "Q8DeviceView": "strix::Q8DeviceView",
+          "Q4ChunkMajorView": "strix::Q4ChunkMajorView", "Q8ChunkMajorView": "strix::Q8ChunkMajorView"}
 
 
 def _demangled_param(p: str) -> str:
@@ -136,7 +137,7 @@ def reference_declarations():
 @pytest.mark.skipif(not os.path.isdir(REF), reason="the reference tree is only in the build container")
 def test_exports_match_reference_declarations():
     """Every launcher the reference's kernel headers declare (kernels/moe_router, moe_grouped, linear_q4, swiglu,
-    linear_q8, linear .hpp) is exported with the same demangled C++ signature, so strixite's call sites link against
+    linear_q8, linear, hc .hpp) is exported with the same demangled C++ signature, so strixite's call sites link against
     this library with their own headers; and the library exports no act_name (strixite's kernels/norm.hip defines
     it)."""
     import subprocess
