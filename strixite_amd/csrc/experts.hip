@@ -473,7 +473,7 @@ __device__ __forceinline__ void stage_load(const Stream<RT> &st, const GemmArgs 
     for (int k = 0; k < kStageMax; ++k) {
         const int d = tid + (k >> 1) * nthr;       // even k: scales, odd k: mins
         const int rt = d / (8 * groups), w = d % (8 * groups);
-        const uint32_t rows = SWI ? (uint32_t)(rt % 2) * 16u + (uint32_t)(rt / 2) * (uint32_t)(a.N / 2) : 16u * rt;
+        const uint32_t rows = SWI ? (uint32_t)(rt % (RT / 2)) * 16u + (uint32_t)(rt / (RT / 2)) * (uint32_t)(a.N / 2) : 16u * rt;
         const uint32_t off = d < per ? (rows * (uint32_t)groups + 2u * (uint32_t)w) * 2 : st.s_bytes;
         sg.v[k] = bld4(k % 2 ? st.rm : st.rs, off, base);
     }
@@ -540,8 +540,9 @@ struct SharedJob {
     int blocks;         // leading blocks of the grid that take the units
 };
 
-// SH: the shared expert's projection riding along (0 none, 1 the Q8 gate_up + SwiGLU, 2 the Q8 down)
-template <int BITS, int SP, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH>
+// SH: the shared expert's projection riding along (0 none, 1 the Q8 gate_up + SwiGLU, 2 the Q8 down). RTH: items of
+// half the weight tiles (more items for the CUs when a projection has few rows, as Q8 experts of one token)
+template <int BITS, int SP, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH, int RTH = 0>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_simd<EPI == EPI_SWIGLU>())))
     expert_stream_kernel(GemmArgs a, int64_t tiles_bound, int64_t col_blocks, int ks, uint32_t q_bytes,
                          uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes, SharedJob sh) {
@@ -561,7 +562,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
         bid -= sh.blocks, nblk -= sh.blocks;
     }
     constexpr bool SWI = EPI == EPI_SWIGLU;
-    constexpr int RT = wave_tiles<SWI>();
+    constexpr int RT = RTH ? wave_tiles<SWI>() / 2 : wave_tiles<SWI>();
     constexpr int KS = SWI ? kWaves : 1;  // most waves of a block sharing an item (SwiGLU: the block's ks waves)
     constexpr int D = ring_depth<SWI>();
     // partial sums of waves 1..ks-1
@@ -592,7 +593,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(w
     st.q_bytes = q_bytes, st.s_bytes = s_bytes, st.x_bytes = x_bytes;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const uint32_t rows = SWI ? 16u * (rt % 2) + (uint32_t)(rt / 2) * (uint32_t)(a.N / 2) : 16u * rt;
+        // SwiGLU: gate tiles 0 .. RT / 2 - 1, then the matching up tiles
+        const uint32_t rows = SWI ? 16u * (rt % (RT / 2)) + (uint32_t)(rt / (RT / 2)) * (uint32_t)(a.N / 2) : 16u * rt;
         st.dq[rt] = rows * (uint32_t)(a.K * BITS / 8);
         st.dsm[rt] = rows * (uint32_t)(a.K / a.G) * 2;
     }
@@ -1043,10 +1045,10 @@ int swiglu_ks(int64_t spans, int D) {
 
 #include "decode_gemv.hpp"
 
-template <int BITS, int SP, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH>
+template <int BITS, int SP, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH, int RTH = 0>
 void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, const SharedJob &sh, hipStream_t stream) {
     constexpr bool SWI = EPI == EPI_SWIGLU;
-    constexpr int RT = wave_tiles<SWI>();
+    constexpr int RT = RTH ? wave_tiles<SWI>() / 2 : wave_tiles<SWI>();
     const int64_t spans = a.K / SP;
     const int ks = SWI ? swiglu_ks(spans, ring_depth<SWI>()) : 1;  // otherwise one wave per item over all of K
     // SwiGLU: two stage buffers for the block; otherwise one a wave
@@ -1054,7 +1056,7 @@ void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, const SharedJob &sh, 
     const int threads = SWI ? ks * kWave : kThreads;
     const int64_t col_blocks = SWI ? (a.N / 2 + 16 * RT / 2 - 1) / (16 * RT / 2) : (a.N + 16 * RT - 1) / (16 * RT);
     const int64_t items = tiles_bound * col_blocks, per_block = SWI ? 1 : kWaves;
-    auto kernel = expert_stream_kernel<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, SST, SH>;
+    auto kernel = expert_stream_kernel<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, SST, SH, RTH>;
     // resident blocks a CU, cached for the last (block size, LDS) this instantiation was launched with
     static thread_local int occ_threads = -1, occ = 1;
     static thread_local size_t occ_lds = 0;
@@ -1095,6 +1097,15 @@ void launch_gemm_s(const GemmArgs &a, int64_t tiles_bound, hipStream_t stream, c
         }
     }
     STRIX_CHECK(sh == nullptr, "expert kernels: a shared projection rides along only with a grouped gate_up or down");
+    if constexpr (BITS == 8 && MODE == GROUPED && !XF16 && (EPI == EPI_SWIGLU || EPI == EPI_F32)) {
+        // grouped Q8 projections whose items (weight tiles x token tiles) would leave CUs idle: half-size items
+        const int64_t rows = SWI ? 16 * wave_tiles<SWI>() / 2 : 16 * wave_tiles<SWI>();
+        const int64_t items = tiles_bound * (((SWI ? a.N / 2 : a.N) + rows - 1) / rows);
+        if ((SWI ? items : (items + kWaves - 1) / kWaves) < device_cus()) {
+            if (sst) return launch_gemm_v<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, true, 0, 1>(a, tiles_bound, none, stream);
+            return launch_gemm_v<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, false, 0, 1>(a, tiles_bound, none, stream);
+        }
+    }
     if (sst) return launch_gemm_v<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, true, 0>(a, tiles_bound, none, stream);
     launch_gemm_v<BITS, SP, MODE, EPI, XF16, XROW_DIV, HF16, false, 0>(a, tiles_bound, none, stream);
 }
