@@ -99,7 +99,6 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                         uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
     using namespace g2;
     constexpr bool SWI = EPI == EPI_SWIGLU;
-    constexpr int NB = X16 ? 3 : 2;  // LDS activation buffers
     // the activation buffers [row * 8 + (col ^ (row & 7))], separate arrays picked at compile time: the compiler
     // then tells a read of one from the loads still landing in another and waits for those loads no longer than it
     // must
