@@ -23,7 +23,8 @@ namespace kernels {
 // ---- router: strixite kernels/linear.hpp:20-26 ----------------------------------------------------------------
 // y[M, N] = x[M, K] * W^T, W [N, K] BF16 bits. FP32 accumulation in one fixed order at every M: lane l of a wave64
 // accumulates the 8-element chunks l, l + 64, ... with fmaf (elements in order), then a butterfly over the lanes
-// (offsets 32 .. 1). out_act F32 stores the sum unrounded (the router logits). x BF16 only.
+// (offsets 32 .. 1). out_act F32 stores the sum unrounded (the router logits). x BF16, or F32 (each
+// product fmaf(x, w) in FP32 in the same order: F32 x holding BF16 values gives the BF16 bits).
 void linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, Act act,
                   hipStream_t stream);
 void linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t N, int64_t K, Act act, Act out_act,

@@ -179,6 +179,34 @@ __global__ void __launch_bounds__(kThreads)
     rsmall::router_small_wave<TY, TT, TE, NCH>(x, w, y, M, N, K, n0, m0);
 }
 
+// Act::F32 activations (the reference's FP32-activation form of linear_bf16w): one wave per (token, row) in the same
+// canonical order - lane l takes the 8-element chunks l, l + 64, ... with fmaf in element order, then the butterfly
+// over offsets 32 .. 1 - so an FP32 x holding BF16 values gives the BF16 path's bits. A compatibility path: every
+// wave reads its token's and its row's whole K from L2.
+template <typename TY>
+__global__ void __launch_bounds__(kThreads)
+    router_f32x_kernel(const float *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t item = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+    if (item >= M * N) return;  // whole wave; no barrier in this kernel
+    const int64_t m = item / N, n = item % N;
+    const float *xr = x + m * K;
+    const uint16_t *wr = w + n * K;
+    float a = 0.f;
+    for (int64_t c = lane; c * 8 < K; c += kWave)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int64_t i = c * 8 + k;
+            if (i < K) a = fmaf(xr[i], bf16_to_f32(wr[i]), a);
+        }
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, kWave);
+    if (lane == 0) {
+        if constexpr (std::is_same_v<TY, float>) y[item] = a;
+        else y[item] = f32_to_bf16(a);
+    }
+}
+
 template <typename TY>
 void launch_router_rows(const uint16_t *x, const uint16_t *w, TY *y, int64_t M, int64_t N, int64_t K,
                         hipStream_t stream) {
@@ -321,11 +349,20 @@ void linear_bf16w(const void *x, const uint16_t *w, void *y, int64_t M, int64_t 
                 (const void *)w, ", y=", y, ")");
     STRIX_CHECK(M >= 1 && N >= 1 && K >= 1 && K <= (1 << 24) && N <= 0x7fffffff, "linear_bf16w: M = ", M, ", N = ",
                 N, ", K = ", K, " out of range");
-    STRIX_CHECK(act == Act::BF16, "linear_bf16w: activations must be BF16 on this path, got ", act_str(act));
+    STRIX_CHECK(act == Act::F32 || act == Act::BF16, "linear_bf16w: unsupported activation dtype ", (int)act);
     STRIX_CHECK(out_act == Act::F32 || out_act == Act::BF16, "linear_bf16w: output dtype ", (int)out_act);
-    const int64_t oes = out_act == Act::F32 ? 4 : 2;
-    STRIX_CHECK(disjoint(y, M * N * oes, x, M * K * 2), "linear_bf16w: output y overlaps input x");
-    if (out_act == Act::F32)
+    const int64_t oes = out_act == Act::F32 ? 4 : 2, xes = act == Act::F32 ? 4 : 2;
+    STRIX_CHECK(disjoint(y, M * N * oes, x, M * K * xes), "linear_bf16w: output y overlaps input x");
+    if (act == Act::F32) {
+        const int64_t blocks = (M * N + kThreads / kWave - 1) / (kThreads / kWave);
+        STRIX_CHECK(blocks < (1ll << 31), "linear_bf16w: M * N = ", M * N, " too large for the FP32-activation path");
+        if (out_act == Act::F32)
+            router_f32x_kernel<float><<<(unsigned)blocks, kThreads, 0, stream>>>(static_cast<const float *>(x), w,
+                                                                                 static_cast<float *>(y), M, N, K);
+        else
+            router_f32x_kernel<uint16_t><<<(unsigned)blocks, kThreads, 0, stream>>>(
+                static_cast<const float *>(x), w, static_cast<uint16_t *>(y), M, N, K);
+    } else if (out_act == Act::F32)
         launch_router_rows(static_cast<const uint16_t *>(x), w, static_cast<float *>(y), M, N, K, stream);
     else
         launch_router_rows(static_cast<const uint16_t *>(x), w, static_cast<uint16_t *>(y), M, N, K, stream);

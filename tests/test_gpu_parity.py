@@ -63,6 +63,17 @@ def test_linear_bf16w_bit_exact(M, N, K):
     assert np.array_equal(to_np(y).view(np.uint32), ref.view(np.uint32))
     yb = moe.linear_bf16w(bf16(x), bf16(w), out_dtype=torch.bfloat16)
     assert np.array_equal(to_np(yb), orc.f32_to_bf16(ref))
+    # Act::F32 activations: an FP32 x holding the same BF16 values gives the same bits (same products, same order)
+    xf = torch.from_numpy(orc.bf16_to_f32(x)).to(DEV)
+    yf = moe.linear_bf16w(xf, bf16(w))
+    assert np.array_equal(to_np(yf).view(np.uint32), ref.view(np.uint32))
+    # and general FP32 x against the float64 sum, within the FP32 summation bound (2 K u |x| |w| per dot)
+    xg = torch.from_numpy(np.random.default_rng(M).standard_normal((M, K)).astype(np.float32)).to(DEV)
+    yg = to_np(moe.linear_bf16w(xg, bf16(w))).astype(np.float64)
+    w64 = orc.bf16_to_f32(w).astype(np.float64)
+    x64 = xg.cpu().numpy().astype(np.float64)
+    bound = 2 * K * 2.0 ** -24 * np.abs(x64) @ np.abs(w64).T + 1e-30
+    assert np.all(np.abs(yg - x64 @ w64.T) <= bound)
 
 
 @pytest.mark.parametrize("E,k", [(64, 8), (512, 10), (1024, 32), (100, 32), (7, 7)])
