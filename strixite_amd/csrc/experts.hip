@@ -1044,6 +1044,48 @@ int swiglu_ks(int64_t spans, int D) {
 }
 
 #include "decode_gemv.hpp"
+#include "f32act.hpp"
+
+// ---- FP32 activations (f32act.hpp) -----------------------------------------------------------------------------------
+f32a::Args f32_args(const QV &w, int64_t E, const void *x, void *y, int64_t ncol) {
+    f32a::Args a{};
+    a.x = static_cast<const float *>(x), a.q = w.q, a.scale = w.scale, a.minv = w.minv;
+    a.N = w.N / E, a.K = w.K, a.G = w.G, a.E = E, a.y = y, a.ldy = ncol, a.ncol = ncol;
+    return a;
+}
+
+void check_f32(const char *fn, const void *x, const QV &w, int64_t E, int64_t M, int64_t A, const void *y,
+               int64_t y_elems, int64_t x_rows) {
+    STRIX_CHECK(x != nullptr && y != nullptr, fn, ": null pointer (x=", x, ", y=", y, ")");
+    check_view(fn, w, E);
+    STRIX_CHECK(E <= kMoeMaxExperts, fn, ": E = ", E, " > ", kMoeMaxExperts);
+    STRIX_CHECK(M >= 1 && A >= 1 && A <= 64 && M * A <= kMoeMaxSlots, fn, ": M = ", M, ", A = ", A, " out of range");
+    STRIX_CHECK(w.K % 32 == 0, fn, ": K = ", w.K, " must be a multiple of 32 with FP32 activations");
+    STRIX_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0, fn, ": input must be 16-byte aligned");
+    STRIX_CHECK(disjoint(y, y_elems * 4, x, x_rows * w.K * 4), fn, ": output overlaps the input");
+}
+
+// gather (+ SwiGLU) with FP32 x and y: grouped through the workspace (ws), or per slot through ids
+void f32_gather(const char *fn, const void *x, const QV &w, int64_t E, const void *ws, size_t ws_bytes,
+                const int32_t *ids, uint32_t *err, int64_t M, int64_t A, void *y, bool swi, hipStream_t stream) {
+    const int64_t ncol = swi ? w.N / E / 2 : w.N / E;
+    check_f32(fn, x, w, E, M, A, y, M * A * ncol, M);
+    f32a::Args a = f32_args(w, E, x, y, ncol);
+    a.A = A, a.S = M * A;
+    if (ws != nullptr) {
+        STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, A, E), fn, ": workspace of ", ws_bytes, " bytes, needs ",
+                    moe_route_workspace_bytes(M, A, E));
+        a.ws = static_cast<const int32_t *>(ws);
+        if (swi) f32a::launch_bits<f32a::GROUPED_POS, true, float>(w.bits, a, stream);
+        else f32a::launch_bits<f32a::GROUPED_POS, false, float>(w.bits, a, stream);
+    } else {
+        STRIX_CHECK(ids != nullptr && err != nullptr, fn, ": null ids or err");
+        a.ids = ids, a.err = err;
+        if (swi) f32a::launch_bits<f32a::PERSLOT_IDS, true, float>(w.bits, a, stream);
+        else f32a::launch_bits<f32a::PERSLOT_IDS, false, float>(w.bits, a, stream);
+    }
+    STRIX_HIP_CHECK_LAUNCH(fn, " F32 M=", M, " A=", A, " E=", E);
+}
 
 template <int BITS, int SP, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH, int RTH = 0>
 void launch_gemm_v(const GemmArgs &a, int64_t tiles_bound, const SharedJob &sh, hipStream_t stream) {
@@ -1254,6 +1296,11 @@ template <typename V>
 void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E, const void *ws, size_t ws_bytes,
                            int64_t M, int64_t A, void *h, Act act, bool h_f16, bool f16, hipStream_t stream) {
     const QV w = qv(wv);
+    if (act == Act::F32) {
+        STRIX_CHECK(!h_f16, fn, ": the F16 h form goes with BF16 activations");
+        STRIX_CHECK(ws != nullptr, fn, ": null workspace");
+        return f32_gather(fn, x, w, E, ws, ws_bytes, nullptr, nullptr, M, A, h, true, stream);
+    }
     const int64_t N = w.N / E, I = N / 2;
     check_grouped(fn, x, w, E, ws, ws_bytes, M, A, h, act, M * A * I * 2, M);
     STRIX_CHECK(I % 16 == 0, fn, ": gate_up has ", N, " rows an expert; I = N / 2 must be a multiple of 16");
@@ -1331,6 +1378,25 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
                      const MoeSharedAdd *shared, bool h_f16, bool f16, hipStream_t stream) {
     const QV w = qv(wv);
     const int64_t N = w.N / E;
+    if (act == Act::F32) {  // FP32 per-slot partials, their ordered sum, the shared add (moe_shared_add, FP32)
+        STRIX_CHECK(!h_f16, fn, ": the F16 h form goes with BF16 activations");
+        STRIX_CHECK(ws != nullptr && ids != nullptr && coef != nullptr && partial != nullptr, fn, ": null pointer");
+        STRIX_CHECK(disjoint(partial, M * A * N * 4, y, M * N * 4) && disjoint(partial, M * A * N * 4, h, M * A * w.K * 4),
+                    fn, ": partial overlaps y or h");
+        check_f32(fn, h, w, E, M, A, partial, M * A * N, M * A);
+        STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, A, E), fn, ": workspace of ", ws_bytes, " bytes, needs ",
+                    moe_route_workspace_bytes(M, A, E));
+        f32a::Args a = f32_args(w, E, h, partial, N);
+        a.A = 1, a.S = M * A, a.ws = static_cast<const int32_t *>(ws);  // h and partial rows are slots
+        f32a::launch_bits<f32a::GROUPED_POS, false, float>(w.bits, a, stream);
+        const unsigned blocks = (unsigned)((M * N + 255) / 256);
+        f32a::f32_combine_kernel<<<blocks, 256, 0, stream>>>(partial, ids, coef, M, A, E, N, static_cast<float *>(y));
+        STRIX_HIP_CHECK_LAUNCH(fn, " F32 combine M=", M, " N=", N);
+        if (shared != nullptr)
+            moe_shared_add(y, shared->s, shared->gate_logit, shared->gate_ld, M, N, shared->gate_index, Act::F32,
+                           shared->err, stream);
+        return;
+    }
     check_grouped(fn, h, w, E, ws, ws_bytes, M, A, y, act, M * N * 2, M * A);
     STRIX_CHECK(ids != nullptr && coef != nullptr && partial != nullptr, fn, ": null pointer (ids=", (const void *)ids,
                 ", coef=", (const void *)coef, ", partial=", (const void *)partial, ")");
@@ -1383,6 +1449,10 @@ void linear_q4_experts_gather_grouped(const void *x, const Q4DeviceView &w, int6
     const char *fn = "linear_q4_experts_gather_grouped";
     const QV v = qv(w);
     const int64_t N = v.N / E;
+    if (act == Act::F32) {
+        STRIX_CHECK(ws != nullptr, fn, ": null workspace");
+        return f32_gather(fn, x, v, E, ws, ws_bytes, nullptr, nullptr, M, A, y, false, stream);
+    }
     check_grouped(fn, x, v, E, ws, ws_bytes, M, A, y, act, M * A * N * 2, M);
     STRIX_CHECK(reinterpret_cast<uintptr_t>(y) % 8 == 0, fn, ": y must be 8-byte aligned");
     GemmArgs a = make_args(v, E, x, y, N);
@@ -1426,6 +1496,7 @@ void linear_q4_experts_gather(const void *x, const Q4DeviceView &w, int64_t E, c
                               int64_t A, void *y, Act act, uint32_t *err, hipStream_t stream) {
     const char *fn = "linear_q4_experts_gather";
     const QV v = qv(w);
+    if (act == Act::F32) return f32_gather(fn, x, v, E, nullptr, 0, ids, err, M, A, y, false, stream);
     check_perslot(fn, x, v, E, ids, M, A, y, act, err);
     const int64_t N = v.N / E;
     STRIX_CHECK(disjoint(y, M * A * N * 2, x, M * v.K * 2), fn, ": y overlaps x");
@@ -1439,6 +1510,7 @@ void linear_q4_experts_gather_swiglu(const void *x, const Q4DeviceView &w, int64
                                      int64_t A, void *h, Act act, uint32_t *err, hipStream_t stream) {
     const char *fn = "linear_q4_experts_gather_swiglu";
     const QV v = qv(w);
+    if (act == Act::F32) return f32_gather(fn, x, v, E, nullptr, 0, ids, err, M, A, h, true, stream);
     check_perslot(fn, x, v, E, ids, M, A, h, act, err);
     const int64_t I = v.N / E / 2;
     STRIX_CHECK(I % 16 == 0, fn, ": I = ", I, " must be a multiple of 16");
@@ -1454,6 +1526,18 @@ void linear_q4_experts_combine(const void *h, const Q4DeviceView &w, int64_t E, 
                                hipStream_t stream) {
     const char *fn = "linear_q4_experts_combine";
     const QV v = qv(w);
+    if (act == Act::F32) {
+        const int64_t N = v.N / E;
+        check_f32(fn, h, v, E, M, A, y, M * N, M * A);
+        STRIX_CHECK(ids != nullptr && err != nullptr && coef != nullptr, fn, ": null ids, err or coef");
+        f32a::Args a = f32_args(v, E, h, y, N);
+        a.A = A, a.S = M, a.ids = ids, a.err = err;
+        const int64_t blocks = (M * N + 3) / 4;
+        STRIX_CHECK(blocks < (1ll << 31), fn, ": M * N too large");
+        f32a::f32_perslot_combine_kernel<4><<<(unsigned)blocks, 256, 0, stream>>>(a, coef, M);
+        STRIX_HIP_CHECK_LAUNCH(fn, " F32 M=", M, " A=", A, " E=", E);
+        return;
+    }
     check_perslot(fn, h, v, E, ids, M, A, y, act, err);
     STRIX_CHECK(coef != nullptr, fn, ": null coef");
     const int64_t N = v.N / E;
@@ -1505,9 +1589,20 @@ namespace {
 void dense_projection(const char *fn, const QV &v, const void *x, void *y, int64_t M, Act act, Act out_act,
                       hipStream_t stream) {
     STRIX_CHECK(x != nullptr && y != nullptr, fn, ": null pointer (x=", x, ", y=", y, ")");
-    STRIX_CHECK(act == Act::BF16, fn, ": activations must be BF16 on this path, got ", act_str(act));
+    STRIX_CHECK(act == Act::BF16 || act == Act::F32, fn, ": unsupported activation dtype ", (int)act);
     STRIX_CHECK(out_act == Act::BF16 || out_act == Act::F32, fn, ": output dtype ", (int)out_act);
     check_view(fn, v, 1);
+    if (act == Act::F32) {  // FP32 activations: f32act.hpp
+        STRIX_CHECK(M >= 1 && v.K % 32 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0, fn, ": M = ", M, ", K = ", v.K,
+                    " (a multiple of 32) and x 16-byte aligned with FP32 activations");
+        STRIX_CHECK(disjoint(y, M * v.N * (out_act == Act::F32 ? 4 : 2), x, M * v.K * 4), fn, ": y overlaps x");
+        f32a::Args a = f32_args(v, 1, x, y, v.N);
+        a.A = 1, a.S = M;
+        if (out_act == Act::F32) f32a::launch_bits<f32a::DENSE_ROWS, false, float>(v.bits, a, stream);
+        else f32a::launch_bits<f32a::DENSE_ROWS, false, uint16_t>(v.bits, a, stream);
+        STRIX_HIP_CHECK_LAUNCH(fn, " F32 M=", M, " N=", v.N, " K=", v.K);
+        return;
+    }
     STRIX_CHECK(M >= 1 && (M + 15) / 16 <= 65535ll * 64, fn, ": M = ", M);
     STRIX_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0, fn,
                 ": x and y must be 16-byte aligned");

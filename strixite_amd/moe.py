@@ -36,6 +36,11 @@ def _stream():
     return C.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+def _act_dtype(t: torch.Tensor) -> torch.dtype:
+    """The activation dtype of the outputs that follow input t: FP32 for an FP32 input, BF16 otherwise."""
+    return torch.float32 if t.dtype == torch.float32 else torch.bfloat16
+
+
 def _act(t: torch.Tensor) -> int:
     if t.dtype == torch.float32:
         return F32
@@ -200,9 +205,9 @@ def experts_gather_grouped_swiglu(x, w: QWeight, E, ws, M, A, h_f16=False, h=Non
     """strixite kernels/moe_grouped.hpp:66-69 (Q4; Q8 through the same signature family)."""
     I = w.N // E // 2
     if h is None:
-        h = torch.empty((M * A, I), dtype=torch.float16 if h_f16 else torch.bfloat16, device=x.device)
+        h = torch.empty((M * A, I), dtype=torch.float16 if h_f16 else _act_dtype(x), device=x.device)
     v = w.view()
-    L.check(_swiglu_fn(w.bits)(_p(x), C.byref(v), E, _p(ws), ws.numel() * 4, M, A, _p(h), BF16, math, _stream(),
+    L.check(_swiglu_fn(w.bits)(_p(x), C.byref(v), E, _p(ws), ws.numel() * 4, M, A, _p(h), _act(x), math, _stream(),
                                1 if h_f16 else 0))
     return h
 
@@ -211,10 +216,10 @@ def experts_gather_grouped(x, w: QWeight, E, ws, M, A, y=None):
     """strixite kernels/moe_grouped.hpp:56-58: y [M * A, N] = x[slot / A] W[id]^T (Q4)."""
     N = w.N // E
     if y is None:
-        y = torch.empty((M * A, N), dtype=torch.bfloat16, device=x.device)
+        y = torch.empty((M * A, N), dtype=_act_dtype(x), device=x.device)
     v = w.view()
     L.check(L.lib().strix_linear_q4_experts_gather_grouped(_p(x), C.byref(v), E, _p(ws), ws.numel() * 4, M, A, _p(y),
-                                                           BF16, MOE_MATH_WMMA_F16, _stream()))
+                                                           _act(x), MOE_MATH_WMMA_F16, _stream()))
     return y
 
 
@@ -225,14 +230,14 @@ def experts_combine_grouped(h, w: QWeight, E, ids, coef, ws, M, A, partial=None,
     if partial is None:
         partial = torch.empty((M * A, N), dtype=torch.float32, device=h.device)
     if y is None:
-        y = torch.empty((M, N), dtype=torch.bfloat16, device=h.device)
+        y = torch.empty((M, N), dtype=_act_dtype(h), device=h.device)
     sh = None
     if shared is not None:
         sh = L.SharedAdd(_p(shared["s"]), _p(shared["gate_logit"]), shared["gate_ld"], shared["gate_index"],
                          _p(shared["err"]))
     v = w.view()
     L.check(_combine_fn(w.bits)(_p(h), C.byref(v), E, _p(ids), _p(coef), _p(ws), ws.numel() * 4, _p(partial), M, A,
-                                _p(y), BF16, math, _stream(), C.byref(sh) if sh is not None else None,
+                                _p(y), _act(h) if not h_f16 else BF16, math, _stream(), C.byref(sh) if sh is not None else None,
                                 1 if h_f16 else 0))
     return y
 
@@ -241,10 +246,10 @@ def experts_gather(x, w: QWeight, E, ids, err, swiglu=False):
     """strixite kernels/linear_q4.hpp:42-43 / 55-56 (per-slot)."""
     M, A = ids.shape
     N = w.N // E
-    y = torch.empty((M * A, N // 2 if swiglu else N), dtype=torch.bfloat16, device=x.device)
+    y = torch.empty((M * A, N // 2 if swiglu else N), dtype=_act_dtype(x), device=x.device)
     fn = L.lib().strix_linear_q4_experts_gather_swiglu if swiglu else L.lib().strix_linear_q4_experts_gather
     v = w.view()
-    L.check(fn(_p(x), C.byref(v), E, _p(ids), M, A, _p(y), BF16, _p(err), _stream()))
+    L.check(fn(_p(x), C.byref(v), E, _p(ids), M, A, _p(y), _act(x), _p(err), _stream()))
     return y
 
 
@@ -252,9 +257,9 @@ def experts_combine(h, w: QWeight, E, ids, coef, err):
     """strixite kernels/linear_q4.hpp:44-46 (per-slot)."""
     M, A = ids.shape
     N = w.N // E
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=h.device)
+    y = torch.empty((M, N), dtype=_act_dtype(h), device=h.device)
     v = w.view()
-    L.check(L.lib().strix_linear_q4_experts_combine(_p(h), C.byref(v), E, _p(ids), _p(coef), M, A, _p(y), BF16,
+    L.check(L.lib().strix_linear_q4_experts_combine(_p(h), C.byref(v), E, _p(ids), _p(coef), M, A, _p(y), _act(h),
                                                     _p(err), _stream()))
     return y
 
