@@ -99,6 +99,26 @@ int strix_linear_q4_experts_gather_swiglu(const void *x, const strix_qview *w, i
 int strix_linear_q4_experts_combine(const void *h, const strix_qview *w, int64_t E, const int32_t *ids,
                                     const float *coef, int64_t M, int64_t A, void *y, int act, uint32_t *err,
                                     void *stream);
+/* strixite kernels/moe_grouped.hpp:93-104, kernels/linear_q4.hpp:47-58: the same with Q5 experts (formats/q5.hpp,
+ * K % 128 == 0; the view's q holds each row's low and high planes). Either activation dtype; exact weights under
+ * every MoeMath; h_f16 refused. */
+int strix_linear_q5_experts_gather_grouped(const void *x, const strix_qview *w, int64_t E, const void *ws,
+                                           size_t ws_bytes, int64_t M, int64_t A, void *y, int act, int math,
+                                           void *stream);
+int strix_linear_q5_experts_gather_grouped_swiglu(const void *x, const strix_qview *w, int64_t E, const void *ws,
+                                                  size_t ws_bytes, int64_t M, int64_t A, void *h, int act, int math,
+                                                  void *stream, int h_f16);
+int strix_linear_q5_experts_combine_grouped(const void *h, const strix_qview *w, int64_t E, const int32_t *ids,
+                                            const float *coef, const void *ws, size_t ws_bytes, float *partial,
+                                            int64_t M, int64_t A, void *y, int act, int math, void *stream,
+                                            const strix_moe_shared_add_t *shared, int h_f16);
+int strix_linear_q5_experts_gather(const void *x, const strix_qview *w, int64_t E, const int32_t *ids, int64_t M,
+                                   int64_t A, void *y, int act, uint32_t *err, void *stream);
+int strix_linear_q5_experts_gather_swiglu(const void *x, const strix_qview *w, int64_t E, const int32_t *ids,
+                                          int64_t M, int64_t A, void *h, int act, uint32_t *err, void *stream);
+int strix_linear_q5_experts_combine(const void *h, const strix_qview *w, int64_t E, const int32_t *ids,
+                                    const float *coef, int64_t M, int64_t A, void *y, int act, uint32_t *err,
+                                    void *stream);
 int strix_check_expert_error(const uint32_t *err, const char *what);
 int strix_report_expert_error(const uint32_t *err_host, const char *what);
 

@@ -50,6 +50,27 @@ void moe_shared_add_inject(void *y, const void *s, const float *gate_logit, int6
 void hc_inject(void *x, const float *w_in, const void *y, int64_t T, int64_t H, int64_t d, Act act,
                hipStream_t stream);
 
+// ---- Q5 experts: strixite kernels/moe_grouped.hpp:93-104, kernels/linear_q4.hpp:47-58 --------------------------
+// The Q4 entry points' meaning with formats/q5.hpp weights (K % 128 == 0), either activation dtype. Every MoeMath
+// kind computes with the exact weights (FP32 accumulation); the F16 h form (h_f16) is refused.
+void linear_q5_experts_gather_grouped(const void *x, const Q5DeviceView &w, int64_t E, const void *ws,
+                                      size_t ws_bytes, int64_t M, int64_t A, void *y, Act act, MoeMath math,
+                                      hipStream_t stream);
+void linear_q5_experts_gather_grouped_swiglu(const void *x, const Q5DeviceView &w, int64_t E, const void *ws,
+                                             size_t ws_bytes, int64_t M, int64_t A, void *h, Act act, MoeMath math,
+                                             hipStream_t stream, bool h_f16 = false);
+void linear_q5_experts_combine_grouped(const void *h, const Q5DeviceView &w, int64_t E, const int32_t *ids,
+                                       const float *coef, const void *ws, size_t ws_bytes, float *partial, int64_t M,
+                                       int64_t A, void *y, Act act, MoeMath math, hipStream_t stream,
+                                       const MoeSharedAdd *shared = nullptr, bool h_f16 = false);
+void linear_q5_experts_gather(const void *x, const Q5DeviceView &w, int64_t E, const int32_t *ids, int64_t M,
+                              int64_t A, void *y, Act act, uint32_t *err, hipStream_t stream);
+void linear_q5_experts_gather_swiglu(const void *x, const Q5DeviceView &w, int64_t E, const int32_t *ids, int64_t M,
+                                     int64_t A, void *h, Act act, uint32_t *err, hipStream_t stream);
+void linear_q5_experts_combine(const void *h, const Q5DeviceView &w, int64_t E, const int32_t *ids,
+                               const float *coef, int64_t M, int64_t A, void *y, Act act, uint32_t *err,
+                               hipStream_t stream);
+
 // ---- hyper-connection mix, the step that produces the sublayer's input: strixite kernels/hc.hpp:31-50 -----------
 // X [T, H d] (H = 4 streams) -> inv [T, H] = 1 / sqrt(mean(X_s^2) + eps), a = sum_s inv_s (W_s . X_s) for the rows of
 // the folded w [r (+ H), H d], h [T, r] = silu(a / H), w_in [T, H] = 2 sigmoid(a / H) for the H injection rows (when

@@ -37,6 +37,15 @@ struct Q8DeviceView {
     const uint16_t *minv = nullptr;
     int64_t N = 0, K = 0, G = 0;
 };
+// strixite runtime/q5_device.hpp:13-18: formats/q5.hpp rows (K % 128 == 0): per row a low plane [K/2] of 4-bit
+// codes (low nibble = even k) and a high plane [K/8] of bit 4 (code k at bit k % 8 of byte k / 8), scale / min
+// [N, K/G] BF16 bits, w = q * scale + min.
+struct Q5DeviceView {
+    const uint8_t *q = nullptr;
+    const uint16_t *scale = nullptr;
+    const uint16_t *minv = nullptr;
+    int64_t N = 0, K = 0, G = 0;
+};
 // strixite runtime/q4_device.hpp:37-43, runtime/q8_device.hpp:36-42: the same codes, scales and mins laid out
 // chunk-major (formats/q4.hpp:43-55): 32-code chunk c of row n at q[(c N + n) * 16] (Q4) or [(c N + n) * 32] (Q8),
 // group g's scale / min at [g N + n].

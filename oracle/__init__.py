@@ -83,14 +83,14 @@ def lib() -> C.CDLL:
 
 
 def ref_lib():
-    """The reference's own formats/q4.cpp + q8.cpp (oracle/_ref), or None where it is not built."""
+    """The reference's own formats/q4.cpp + q8.cpp + q5.cpp (oracle/_ref), or None where it is not built."""
     if not os.path.exists(_REF):
         return None
     L = C.CDLL(_REF)
-    for n in ("ref_quantize_q4", "ref_quantize_q8"):
+    for n in ("ref_quantize_q4", "ref_quantize_q8", "ref_quantize_q5"):
         getattr(L, n).restype = C.c_int
         getattr(L, n).argtypes = [_p, _i64, _i64, _i64, _p, _p, _p]
-    for n in ("ref_dequantize_q4", "ref_dequantize_q8"):
+    for n in ("ref_dequantize_q4", "ref_dequantize_q8", "ref_dequantize_q5"):
         getattr(L, n).restype = C.c_int
         getattr(L, n).argtypes = [_p, _p, _p, _i64, _i64, _i64, _p]
     return L

@@ -74,6 +74,15 @@ _SIGS = {
     "strix_linear_q4_experts_gather": (_int, [_p, C.POINTER(QView), _i64, _p, _i64, _i64, _p, _int, _p, _p]),
     "strix_linear_q4_experts_gather_swiglu": (_int, [_p, C.POINTER(QView), _i64, _p, _i64, _i64, _p, _int, _p, _p]),
     "strix_linear_q4_experts_combine": (_int, [_p, C.POINTER(QView), _i64, _p, _p, _i64, _i64, _p, _int, _p, _p]),
+    "strix_linear_q5_experts_gather_grouped": (_int, [_p, C.POINTER(QView), _i64, _p, _sz, _i64, _i64, _p, _int,
+                                                      _int, _p]),
+    "strix_linear_q5_experts_gather_grouped_swiglu": (_int, [_p, C.POINTER(QView), _i64, _p, _sz, _i64, _i64, _p,
+                                                             _int, _int, _p, _int]),
+    "strix_linear_q5_experts_combine_grouped": (_int, [_p, C.POINTER(QView), _i64, _p, _p, _p, _sz, _p, _i64, _i64,
+                                                       _p, _int, _int, _p, C.POINTER(SharedAdd), _int]),
+    "strix_linear_q5_experts_gather": (_int, [_p, C.POINTER(QView), _i64, _p, _i64, _i64, _p, _int, _p, _p]),
+    "strix_linear_q5_experts_gather_swiglu": (_int, [_p, C.POINTER(QView), _i64, _p, _i64, _i64, _p, _int, _p, _p]),
+    "strix_linear_q5_experts_combine": (_int, [_p, C.POINTER(QView), _i64, _p, _p, _i64, _i64, _p, _int, _p, _p]),
     "strix_check_expert_error": (_int, [_p, C.c_char_p]),
     "strix_report_expert_error": (_int, [_p, C.c_char_p]),
     "strix_swiglu": (_int, [_p, _p, _i64, _i64, _int, _p]),

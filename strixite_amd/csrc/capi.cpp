@@ -54,6 +54,10 @@ strix::Q4DeviceView q4(const strix_qview *w) {
     STRIX_CHECK(w != nullptr, "null weight view");
     return {w->q, w->scale, w->minv, w->N, w->K, w->G};
 }
+strix::Q5DeviceView q5(const strix_qview *w) {
+    STRIX_CHECK(w != nullptr, "null weight view");
+    return {w->q, w->scale, w->minv, w->N, w->K, w->G};
+}
 strix::Q8DeviceView q8(const strix_qview *w) {
     STRIX_CHECK(w != nullptr, "null weight view");
     return {w->q, w->scale, w->minv, w->N, w->K, w->G};
@@ -205,6 +209,58 @@ int strix_linear_q4_experts_combine(const void *h, const strix_qview *w, int64_t
                                     void *stream) {
     return guard([&] {
         strix::kernels::linear_q4_experts_combine(h, q4(w), E, ids, coef, M, A, y, act_of(act), err, st(stream));
+    });
+}
+
+int strix_linear_q5_experts_gather_grouped(const void *x, const strix_qview *w, int64_t E, const void *ws,
+                                           size_t ws_bytes, int64_t M, int64_t A, void *y, int act, int math,
+                                           void *stream) {
+    return guard([&] {
+        strix::kernels::linear_q5_experts_gather_grouped(x, q5(w), E, ws, ws_bytes, M, A, y, act_of(act), math_of(math),
+                                                         st(stream));
+    });
+}
+
+int strix_linear_q5_experts_gather_grouped_swiglu(const void *x, const strix_qview *w, int64_t E, const void *ws,
+                                                  size_t ws_bytes, int64_t M, int64_t A, void *h, int act, int math,
+                                                  void *stream, int h_f16) {
+    return guard([&] {
+        strix::kernels::linear_q5_experts_gather_grouped_swiglu(x, q5(w), E, ws, ws_bytes, M, A, h, act_of(act),
+                                                                math_of(math), st(stream), h_f16 != 0);
+    });
+}
+
+int strix_linear_q5_experts_combine_grouped(const void *h, const strix_qview *w, int64_t E, const int32_t *ids,
+                                            const float *coef, const void *ws, size_t ws_bytes, float *partial,
+                                            int64_t M, int64_t A, void *y, int act, int math, void *stream,
+                                            const strix_moe_shared_add_t *shared, int h_f16) {
+    return guard([&] {
+        const strix::kernels::MoeSharedAdd sh = shared ? shared_of(shared) : strix::kernels::MoeSharedAdd{};
+        strix::kernels::linear_q5_experts_combine_grouped(h, q5(w), E, ids, coef, ws, ws_bytes, partial, M, A, y,
+                                                          act_of(act), math_of(math), st(stream),
+                                                          shared ? &sh : nullptr, h_f16 != 0);
+    });
+}
+
+int strix_linear_q5_experts_gather(const void *x, const strix_qview *w, int64_t E, const int32_t *ids, int64_t M,
+                                   int64_t A, void *y, int act, uint32_t *err, void *stream) {
+    return guard([&] {
+        strix::kernels::linear_q5_experts_gather(x, q5(w), E, ids, M, A, y, act_of(act), err, st(stream));
+    });
+}
+
+int strix_linear_q5_experts_gather_swiglu(const void *x, const strix_qview *w, int64_t E, const int32_t *ids,
+                                          int64_t M, int64_t A, void *h, int act, uint32_t *err, void *stream) {
+    return guard([&] {
+        strix::kernels::linear_q5_experts_gather_swiglu(x, q5(w), E, ids, M, A, h, act_of(act), err, st(stream));
+    });
+}
+
+int strix_linear_q5_experts_combine(const void *h, const strix_qview *w, int64_t E, const int32_t *ids,
+                                    const float *coef, int64_t M, int64_t A, void *y, int act, uint32_t *err,
+                                    void *stream) {
+    return guard([&] {
+        strix::kernels::linear_q5_experts_combine(h, q5(w), E, ids, coef, M, A, y, act_of(act), err, st(stream));
     });
 }
 

@@ -1007,6 +1007,7 @@ struct QV {
 };
 QV qv(const Q4DeviceView &w) { return {w.q, w.scale, w.minv, w.N, w.K, w.G, 4}; }
 QV qv(const Q8DeviceView &w) { return {w.q, w.scale, w.minv, w.N, w.K, w.G, 8}; }
+QV qv(const Q5DeviceView &w) { return {w.q, w.scale, w.minv, w.N, w.K, w.G, 5}; }
 
 void check_view(const char *fn, const QV &w, int64_t E) {
     STRIX_CHECK(w.q != nullptr && w.scale != nullptr && w.minv != nullptr, fn, ": null weight pointer (q=",
@@ -1049,42 +1050,54 @@ int swiglu_ks(int64_t spans, int D) {
 // ---- FP32 activations (f32act.hpp) -----------------------------------------------------------------------------------
 f32a::Args f32_args(const QV &w, int64_t E, const void *x, void *y, int64_t ncol) {
     f32a::Args a{};
-    a.x = static_cast<const float *>(x), a.q = w.q, a.scale = w.scale, a.minv = w.minv;
+    a.x = x, a.q = w.q, a.scale = w.scale, a.minv = w.minv;
     a.N = w.N / E, a.K = w.K, a.G = w.G, a.E = E, a.y = y, a.ldy = ncol, a.ncol = ncol;
     return a;
 }
 
 void check_f32(const char *fn, const void *x, const QV &w, int64_t E, int64_t M, int64_t A, const void *y,
-               int64_t y_elems, int64_t x_rows) {
+               int64_t y_elems, int64_t x_rows, int64_t es = 4) {
     STRIX_CHECK(x != nullptr && y != nullptr, fn, ": null pointer (x=", x, ", y=", y, ")");
     check_view(fn, w, E);
     STRIX_CHECK(E <= kMoeMaxExperts, fn, ": E = ", E, " > ", kMoeMaxExperts);
     STRIX_CHECK(M >= 1 && A >= 1 && A <= 64 && M * A <= kMoeMaxSlots, fn, ": M = ", M, ", A = ", A, " out of range");
-    STRIX_CHECK(w.K % 32 == 0, fn, ": K = ", w.K, " must be a multiple of 32 with FP32 activations");
+    STRIX_CHECK(w.bits == 5 ? w.K % 128 == 0 : w.K % 32 == 0, fn, ": K = ", w.K, " must be a multiple of ",
+                w.bits == 5 ? "128 (Q5: 16-byte aligned code planes)" : "32 with FP32 activations");
     STRIX_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0, fn, ": input must be 16-byte aligned");
-    STRIX_CHECK(disjoint(y, y_elems * 4, x, x_rows * w.K * 4), fn, ": output overlaps the input");
+    STRIX_CHECK(disjoint(y, y_elems * es, x, x_rows * w.K * es), fn, ": output overlaps the input");
 }
 
-// gather (+ SwiGLU) with FP32 x and y: grouped through the workspace (ws), or per slot through ids
+// gather (+ SwiGLU) on the compatibility path (FP32 activations, or Q5 weights), x and y in the activation dtype:
+// grouped through the workspace (ws), or per slot through ids
 void f32_gather(const char *fn, const void *x, const QV &w, int64_t E, const void *ws, size_t ws_bytes,
-                const int32_t *ids, uint32_t *err, int64_t M, int64_t A, void *y, bool swi, hipStream_t stream) {
+                const int32_t *ids, uint32_t *err, int64_t M, int64_t A, void *y, bool swi, hipStream_t stream,
+                Act act = Act::F32) {
+    STRIX_CHECK(act == Act::F32 || act == Act::BF16, fn, ": unsupported activation dtype ", (int)act);
     const int64_t ncol = swi ? w.N / E / 2 : w.N / E;
-    check_f32(fn, x, w, E, M, A, y, M * A * ncol, M);
+    check_f32(fn, x, w, E, M, A, y, M * A * ncol, M, act == Act::F32 ? 4 : 2);
     f32a::Args a = f32_args(w, E, x, y, ncol);
     a.A = A, a.S = M * A;
+    auto go = [&](auto mode, auto ty) {
+        constexpr int MD = decltype(mode)::value;
+        using T = decltype(ty);
+        if (swi) f32a::launch_bits<MD, true, T, T>(w.bits, a, stream);
+        else f32a::launch_bits<MD, false, T, T>(w.bits, a, stream);
+    };
+    auto by_act = [&](auto mode) {
+        if (act == Act::F32) go(mode, float{});
+        else go(mode, uint16_t{});
+    };
     if (ws != nullptr) {
         STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, A, E), fn, ": workspace of ", ws_bytes, " bytes, needs ",
                     moe_route_workspace_bytes(M, A, E));
         a.ws = static_cast<const int32_t *>(ws);
-        if (swi) f32a::launch_bits<f32a::GROUPED_POS, true, float>(w.bits, a, stream);
-        else f32a::launch_bits<f32a::GROUPED_POS, false, float>(w.bits, a, stream);
+        by_act(std::integral_constant<int, f32a::GROUPED_POS>{});
     } else {
         STRIX_CHECK(ids != nullptr && err != nullptr, fn, ": null ids or err");
         a.ids = ids, a.err = err;
-        if (swi) f32a::launch_bits<f32a::PERSLOT_IDS, true, float>(w.bits, a, stream);
-        else f32a::launch_bits<f32a::PERSLOT_IDS, false, float>(w.bits, a, stream);
+        by_act(std::integral_constant<int, f32a::PERSLOT_IDS>{});
     }
-    STRIX_HIP_CHECK_LAUNCH(fn, " F32 M=", M, " A=", A, " E=", E);
+    STRIX_HIP_CHECK_LAUNCH(fn, " ", act_str(act), " M=", M, " A=", A, " E=", E, " Q", w.bits);
 }
 
 template <int BITS, int SP, int MODE, int EPI, bool XF16, bool XROW_DIV, bool HF16, bool SST, int SH, int RTH = 0>
@@ -1534,7 +1547,7 @@ void linear_q4_experts_combine(const void *h, const Q4DeviceView &w, int64_t E, 
         a.A = A, a.S = M, a.ids = ids, a.err = err;
         const int64_t blocks = (M * N + 3) / 4;
         STRIX_CHECK(blocks < (1ll << 31), fn, ": M * N too large");
-        f32a::f32_perslot_combine_kernel<4><<<(unsigned)blocks, 256, 0, stream>>>(a, coef, M);
+        f32a::f32_perslot_combine_kernel<4, float, float><<<(unsigned)blocks, 256, 0, stream>>>(a, coef, M);
         STRIX_HIP_CHECK_LAUNCH(fn, " F32 M=", M, " A=", A, " E=", E);
         return;
     }
@@ -1552,6 +1565,90 @@ void linear_q4_experts_combine(const void *h, const Q4DeviceView &w, int64_t E, 
         default: perslot_combine_kernel<4, 32, false><<<grid, block, 0, stream>>>(a, coef); break;
     }
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E);
+}
+
+// ---- Q5 experts (strixite kernels/moe_grouped.hpp:93-104, linear_q4.hpp:47-58): the compatibility path --------------
+void linear_q5_experts_gather_grouped(const void *x, const Q5DeviceView &w, int64_t E, const void *ws,
+                                      size_t ws_bytes, int64_t M, int64_t A, void *y, Act act, MoeMath,
+                                      hipStream_t stream) {
+    const char *fn = "linear_q5_experts_gather_grouped";
+    STRIX_CHECK(ws != nullptr, fn, ": null workspace");
+    f32_gather(fn, x, qv(w), E, ws, ws_bytes, nullptr, nullptr, M, A, y, false, stream, act);
+}
+
+void linear_q5_experts_gather_grouped_swiglu(const void *x, const Q5DeviceView &w, int64_t E, const void *ws,
+                                             size_t ws_bytes, int64_t M, int64_t A, void *h, Act act, MoeMath,
+                                             hipStream_t stream, bool h_f16) {
+    const char *fn = "linear_q5_experts_gather_grouped_swiglu";
+    STRIX_CHECK(!h_f16, fn, ": the F16 h form is not served for Q5 experts");
+    STRIX_CHECK(ws != nullptr, fn, ": null workspace");
+    f32_gather(fn, x, qv(w), E, ws, ws_bytes, nullptr, nullptr, M, A, h, true, stream, act);
+}
+
+void linear_q5_experts_combine_grouped(const void *h, const Q5DeviceView &w, int64_t E, const int32_t *ids,
+                                       const float *coef, const void *ws, size_t ws_bytes, float *partial, int64_t M,
+                                       int64_t A, void *y, Act act, MoeMath, hipStream_t stream,
+                                       const MoeSharedAdd *shared, bool h_f16) {
+    const char *fn = "linear_q5_experts_combine_grouped";
+    STRIX_CHECK(!h_f16, fn, ": the F16 h form is not served for Q5 experts");
+    STRIX_CHECK(act == Act::F32 || act == Act::BF16, fn, ": unsupported activation dtype ", (int)act);
+    STRIX_CHECK(ws != nullptr && ids != nullptr && coef != nullptr && partial != nullptr, fn, ": null pointer");
+    const QV v = qv(w);
+    const int64_t N = v.N / E, es = act == Act::F32 ? 4 : 2;
+    check_f32(fn, h, v, E, M, A, partial, M * A * N, M * A, es);
+    STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, A, E), fn, ": workspace of ", ws_bytes, " bytes, needs ",
+                moe_route_workspace_bytes(M, A, E));
+    STRIX_CHECK(N % 8 == 0 && reinterpret_cast<uintptr_t>(partial) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0,
+                fn, ": N = ", N, " must be a multiple of 8, partial and y 16-byte aligned");
+    STRIX_CHECK(disjoint(partial, M * A * N * 4, y, M * N * es), fn, ": partial overlaps y");
+    if (shared != nullptr)
+        STRIX_CHECK(shared->s != nullptr && shared->gate_logit != nullptr && shared->err != nullptr &&
+                        shared->gate_ld >= 1 && reinterpret_cast<uintptr_t>(shared->s) % 16 == 0,
+                    fn, ": shared add with a null pointer, gate_ld < 1 or a misaligned s");
+    // FP32 per-slot partials (h and partial rows are slots), then the ordered sum in the activation dtype
+    f32a::Args a = f32_args(v, E, h, partial, N);
+    a.A = 1, a.S = M * A, a.ws = static_cast<const int32_t *>(ws);
+    if (act == Act::F32) {
+        f32a::launch_bits<f32a::GROUPED_POS, false, float, float>(5, a, stream);
+        f32a::f32_combine_kernel<<<(unsigned)((M * N + 255) / 256), 256, 0, stream>>>(partial, ids, coef, M, A, E, N,
+                                                                                      static_cast<float *>(y));
+        STRIX_HIP_CHECK_LAUNCH(fn, " F32 M=", M, " N=", N);
+        if (shared != nullptr)
+            moe_shared_add(y, shared->s, shared->gate_logit, shared->gate_ld, M, N, shared->gate_index, Act::F32,
+                           shared->err, stream);
+    } else {
+        f32a::launch_bits<f32a::GROUPED_POS, false, float, uint16_t>(5, a, stream);
+        combine_reduce(partial, ids, coef, M, A, E, N, static_cast<uint16_t *>(y), shared, nullptr, nullptr, stream);
+        STRIX_HIP_CHECK_LAUNCH(fn, " BF16 M=", M, " N=", N);
+    }
+}
+
+void linear_q5_experts_gather(const void *x, const Q5DeviceView &w, int64_t E, const int32_t *ids, int64_t M,
+                              int64_t A, void *y, Act act, uint32_t *err, hipStream_t stream) {
+    f32_gather("linear_q5_experts_gather", x, qv(w), E, nullptr, 0, ids, err, M, A, y, false, stream, act);
+}
+
+void linear_q5_experts_gather_swiglu(const void *x, const Q5DeviceView &w, int64_t E, const int32_t *ids, int64_t M,
+                                     int64_t A, void *h, Act act, uint32_t *err, hipStream_t stream) {
+    f32_gather("linear_q5_experts_gather_swiglu", x, qv(w), E, nullptr, 0, ids, err, M, A, h, true, stream, act);
+}
+
+void linear_q5_experts_combine(const void *h, const Q5DeviceView &w, int64_t E, const int32_t *ids,
+                               const float *coef, int64_t M, int64_t A, void *y, Act act, uint32_t *err,
+                               hipStream_t stream) {
+    const char *fn = "linear_q5_experts_combine";
+    STRIX_CHECK(act == Act::F32 || act == Act::BF16, fn, ": unsupported activation dtype ", (int)act);
+    const QV v = qv(w);
+    const int64_t N = v.N / E;
+    check_f32(fn, h, v, E, M, A, y, M * N, M * A, act == Act::F32 ? 4 : 2);
+    STRIX_CHECK(ids != nullptr && err != nullptr && coef != nullptr, fn, ": null ids, err or coef");
+    f32a::Args a = f32_args(v, E, h, y, N);
+    a.A = A, a.S = M, a.ids = ids, a.err = err;
+    const int64_t blocks = (M * N + 3) / 4;
+    STRIX_CHECK(blocks < (1ll << 31), fn, ": M * N too large");
+    if (act == Act::F32) f32a::f32_perslot_combine_kernel<5, float, float><<<(unsigned)blocks, 256, 0, stream>>>(a, coef, M);
+    else f32a::f32_perslot_combine_kernel<5, uint16_t, uint16_t><<<(unsigned)blocks, 256, 0, stream>>>(a, coef, M);
+    STRIX_HIP_CHECK_LAUNCH(fn, " ", act_str(act), " M=", M, " A=", A, " E=", E);
 }
 
 void check_expert_error(const uint32_t *err, const char *what) {

@@ -1,9 +1,11 @@
-// FP32 activations (Act::F32) for the expert and dense projections: the reference's FP32-activation semantics
-// (strixite kernels/linear_q4.hpp:32-41, moe_grouped.hpp:3-16: FP32 x against the Q4 / Q8 codes, per 32-code chunk
-// acc = fma(s, sum(x * code), fma(m, sum(x), acc)), FP32 accumulation) for engines that run FP32 activations.
-// Included by experts.hip (it uses QV, route::slots_at, the bf16 helpers). The BF16 path keeps its streaming and
-// matrix-core kernels; this one is a compatibility path: one wave per output element (a lane per 32-code chunk,
-// chunks l, l + 64, ..., then a butterfly), x and weight rows read through L2.
+// The compatibility path of the expert and dense projections: FP32 activations (Act::F32) with Q4 / Q8 weights, and
+// the Q5 experts (strixite formats/q5.hpp) with either activation dtype. The reference's semantics (strixite
+// kernels/linear_q4.hpp:32-41, moe_grouped.hpp:3-16: x against the exact codes, per 32-code chunk
+// acc = fma(s, sum(x * code), fma(m, sum(x), acc)), FP32 accumulation). Included by experts.hip (it uses QV,
+// route::slots_at, the bf16 helpers). The BF16 Q4 / Q8 path keeps its streaming and matrix-core kernels; this one is
+// one wave per output element (a lane per 32-code chunk, chunks l, l + 64, ..., then a butterfly), x and weight rows
+// read through L2. FMT: 4, 8 (one plane, row-major) or 5 (per row a low plane [K/2] of 4-bit codes and a high plane
+// [K/8] of bit 4, code k at bit k % 8 of byte k / 8).
 #pragma once
 
 namespace f32a {
@@ -11,7 +13,7 @@ namespace f32a {
 enum Mode { DENSE_ROWS = 0, GROUPED_POS = 1, PERSLOT_IDS = 2 };
 
 struct Args {
-    const float *x;                       // activation rows [*, K] FP32
+    const void *x;                        // activation rows [*, K] (FP32 or BF16)
     const uint8_t *q;
     const uint16_t *scale, *minv;
     int64_t N, K, G;                      // N: weight rows an expert (DENSE: all)
@@ -23,33 +25,59 @@ struct Args {
     int64_t ncol;                         // output columns (SwiGLU: I = N / 2)
 };
 
+// 8 activations of a chunk (FP32 or BF16 bits) at element offset i
+__device__ __forceinline__ void ld8x(const float *p, int64_t i, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(p + i), b = *reinterpret_cast<const float4 *>(p + i + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+__device__ __forceinline__ void ld8x(const uint16_t *p, int64_t i, float (&v)[8]) {
+    const uint4 u = *reinterpret_cast<const uint4 *>(p + i);
+    const uint32_t d[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[2 * k] = __uint_as_float(d[k] << 16), v[2 * k + 1] = __uint_as_float(d[k] & 0xffff0000u);
+}
+
+// the 32 codes of chunk c of weight row wrow: code i = (w[i / per] >> (BITS (i % per))) & mask (FMT 4, 8), or the low
+// nibble of lo[] with bit i of hi (FMT 5)
+template <int FMT> struct ChunkCodes {
+    static constexpr int W = FMT == 5 ? 4 : FMT;
+    uint32_t w[W], hi = 0;
+    __device__ __forceinline__ void load(const uint8_t *q, int64_t K, int64_t wrow, int64_t c) {
+        const uint8_t *p = FMT == 5 ? q + wrow * (K / 2 + K / 8) + c * 16 : q + (wrow * (K / 32) + c) * (4 * FMT);
+#pragma unroll
+        for (int i = 0; i < W / 4; ++i) {
+            const uint4 u = reinterpret_cast<const uint4 *>(p)[i];
+            w[4 * i] = u.x, w[4 * i + 1] = u.y, w[4 * i + 2] = u.z, w[4 * i + 3] = u.w;
+        }
+        if constexpr (FMT == 5) hi = *reinterpret_cast<const uint32_t *>(q + wrow * (K / 2 + K / 8) + K / 2 + c * 4);
+    }
+    __device__ __forceinline__ float code(int i) const {
+        if constexpr (FMT == 5) return (float)(((w[i / 8] >> (4 * (i % 8))) & 0xFu) | (((hi >> i) & 1u) << 4));
+        else {
+            constexpr int per = 32 / FMT;
+            return (float)((w[i / per] >> (FMT * (i % per))) & ((1u << FMT) - 1u));
+        }
+    }
+};
+
 // the dot of activation row xr with weight row wrow (FP32, the reference's per-chunk form), every lane holding it
-template <int BITS>
-__device__ __forceinline__ float row_dot(const Args &a, const float *xr, int64_t wrow, int lane) {
+template <int BITS, typename TX>
+__device__ __forceinline__ float row_dot(const Args &a, const TX *xr, int64_t wrow, int lane) {
     const int64_t nc = a.K / 32, gpr = a.K / a.G;
     float acc = 0.f;
     for (int64_t c = lane; c < nc; c += 64) {
-        const uint4 *qp = reinterpret_cast<const uint4 *>(a.q + (wrow * nc + c) * (32 * BITS / 8));
-        uint32_t w[BITS];
-#pragma unroll
-        for (int i = 0; i < BITS / 4; ++i) {
-            const uint4 u = qp[i];
-            w[4 * i] = u.x, w[4 * i + 1] = u.y, w[4 * i + 2] = u.z, w[4 * i + 3] = u.w;
-        }
+        ChunkCodes<BITS> cc;
+        cc.load(a.q, a.K, wrow, c);
         const int64_t gi = wrow * gpr + c * 32 / a.G;
         const float s = strix::dev::bf16_to_f32(a.scale[gi]), m = strix::dev::bf16_to_f32(a.minv[gi]);
-        const float4 *xp = reinterpret_cast<const float4 *>(xr + c * 32);
         float dot = 0.f, xs = 0.f;
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const float4 v = xp[p];
-            const float xv[4] = {v.x, v.y, v.z, v.w};
+        for (int p = 0; p < 4; ++p) {
+            float xv[8];
+            ld8x(xr, c * 32 + 8 * p, xv);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int i = 4 * p + k;
-                constexpr int per = 32 / BITS;
-                const float code = (float)((w[i / per] >> (BITS * (i % per))) & ((1u << BITS) - 1u));
-                dot = fmaf(xv[k], code, dot);
+            for (int k = 0; k < 8; ++k) {
+                dot = fmaf(xv[k], cc.code(8 * p + k), dot);
                 xs += xv[k];
             }
         }
@@ -73,7 +101,7 @@ __device__ __forceinline__ int32_t bucket_of(const int32_t *ws, int64_t E, int64
 
 // one wave per (output row r, column j): MODE picks where r's activation row and expert come from; SWI: h = silu(g) u
 // from the gate row j and up row ncol + j of the expert
-template <int BITS, int MODE, bool SWI, typename TY>
+template <int BITS, int MODE, bool SWI, typename TY, typename TX>
 __global__ void __launch_bounds__(256) f32act_kernel(Args a) {
     const int lane = threadIdx.x % 64;
     const int64_t item = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
@@ -94,14 +122,14 @@ __global__ void __launch_bounds__(256) f32act_kernel(Args a) {
             a.err[2] = (uint32_t)r0;
         }
     }
-    const float *xr = a.x + xrow * a.K;
+    const TX *xr = static_cast<const TX *>(a.x) + xrow * a.K;
     float v;
     if constexpr (SWI) {
-        const float g = row_dot<BITS>(a, xr, expert * a.N + j, lane);
-        const float u = row_dot<BITS>(a, xr, expert * a.N + a.ncol + j, lane);
+        const float g = row_dot<BITS, TX>(a, xr, expert * a.N + j, lane);
+        const float u = row_dot<BITS, TX>(a, xr, expert * a.N + a.ncol + j, lane);
         v = strix::dev::silu(g) * u;
     } else {
-        v = row_dot<BITS>(a, xr, expert * a.N + j, lane);
+        v = row_dot<BITS, TX>(a, xr, expert * a.N + j, lane);
     }
     if (nan) v = strix::dev::qnan();
     if (lane == 0) {
@@ -127,15 +155,18 @@ __global__ void __launch_bounds__(256) f32_combine_kernel(const float *partial, 
     y[i] = bad ? strix::dev::qnan() : acc;
 }
 
-template <int BITS, int MODE, bool SWI, typename TY> void launch(const Args &a, hipStream_t stream) {
+template <int BITS, int MODE, bool SWI, typename TY, typename TX> void launch(const Args &a, hipStream_t stream) {
     const int64_t blocks = (a.S * a.ncol + 3) / 4;
-    STRIX_CHECK(blocks < (1ll << 31), "FP32-activation path: ", a.S, " x ", a.ncol, " outputs, too many");
-    f32act_kernel<BITS, MODE, SWI, TY><<<(unsigned)blocks, 256, 0, stream>>>(a);
+    STRIX_CHECK(blocks < (1ll << 31), "compatibility projection path: ", a.S, " x ", a.ncol, " outputs, too many");
+    f32act_kernel<BITS, MODE, SWI, TY, TX><<<(unsigned)blocks, 256, 0, stream>>>(a);
 }
 
-template <int MODE, bool SWI, typename TY> void launch_bits(int bits, const Args &a, hipStream_t stream) {
-    if (bits == 4) launch<4, MODE, SWI, TY>(a, stream);
-    else launch<8, MODE, SWI, TY>(a, stream);
+// TX: the activations' type (float: FP32, uint16_t: BF16 bits)
+template <int MODE, bool SWI, typename TY, typename TX = float>
+void launch_bits(int bits, const Args &a, hipStream_t stream) {
+    if (bits == 4) launch<4, MODE, SWI, TY, TX>(a, stream);
+    else if (bits == 5) launch<5, MODE, SWI, TY, TX>(a, stream);
+    else launch<8, MODE, SWI, TY, TX>(a, stream);
 }
 
 }  // namespace f32a
@@ -143,7 +174,7 @@ template <int MODE, bool SWI, typename TY> void launch_bits(int bits, const Args
 namespace f32a {
 // per-slot combine: y[m, n] = sum_a coef[m, a] (h[m A + a] . W[ids[m, a] N + n]) (fmaf in slot order), FP32; an
 // invalid id: NaN and the error word
-template <int BITS>
+template <int BITS, typename TY, typename TX>
 __global__ void __launch_bounds__(256) f32_perslot_combine_kernel(Args a, const float *coef, int64_t M) {
     const int lane = threadIdx.x % 64;
     const int64_t item = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
@@ -159,9 +190,14 @@ __global__ void __launch_bounds__(256) f32_perslot_combine_kernel(Args a, const 
             a.err[2] = (uint32_t)(m * a.A + s);
         }
         bad = bad || nan;
-        const float d = row_dot<BITS>(a, a.x + (m * a.A + s) * a.K, (nan ? 0 : id) * a.N + n, lane);
+        const float d = row_dot<BITS, TX>(a, static_cast<const TX *>(a.x) + (m * a.A + s) * a.K, (nan ? 0 : id) * a.N + n,
+                                          lane);
         acc = fmaf(coef[m * a.A + s], d, acc);
     }
-    if (lane == 0) static_cast<float *>(a.y)[m * a.ldy + n] = bad ? strix::dev::qnan() : acc;
+    if (lane == 0) {
+        const float v = bad ? strix::dev::qnan() : acc;
+        if constexpr (std::is_same_v<TY, float>) static_cast<float *>(a.y)[m * a.ldy + n] = v;
+        else static_cast<TY *>(a.y)[m * a.ldy + n] = strix::dev::f32_to_bf16(v);
+    }
 }
 }  // namespace f32a

@@ -191,14 +191,17 @@ def route_tables(ws: torch.Tensor, M: int, A: int, E: int) -> dict:
 
 
 # ---- experts ---------------------------------------------------------------------------------------------------
+def _fam(bits):
+    """The C-ABI family of a weight format: q4, q5 (formats/q5.hpp) or q8."""
+    return {4: "q4", 5: "q5", 8: "q8"}[bits]
+
+
 def _swiglu_fn(bits):
-    return (L.lib().strix_linear_q4_experts_gather_grouped_swiglu if bits == 4
-            else L.lib().strix_linear_q8_experts_gather_grouped_swiglu)
+    return getattr(L.lib(), f"strix_linear_{_fam(bits)}_experts_gather_grouped_swiglu")
 
 
 def _combine_fn(bits):
-    return (L.lib().strix_linear_q4_experts_combine_grouped if bits == 4
-            else L.lib().strix_linear_q8_experts_combine_grouped)
+    return getattr(L.lib(), f"strix_linear_{_fam(bits)}_experts_combine_grouped")
 
 
 def experts_gather_grouped_swiglu(x, w: QWeight, E, ws, M, A, h_f16=False, h=None, math=MOE_MATH_WMMA_F16):
@@ -218,7 +221,8 @@ def experts_gather_grouped(x, w: QWeight, E, ws, M, A, y=None):
     if y is None:
         y = torch.empty((M * A, N), dtype=_act_dtype(x), device=x.device)
     v = w.view()
-    L.check(L.lib().strix_linear_q4_experts_gather_grouped(_p(x), C.byref(v), E, _p(ws), ws.numel() * 4, M, A, _p(y),
+    L.check(getattr(L.lib(), f"strix_linear_{_fam(w.bits)}_experts_gather_grouped")(
+        _p(x), C.byref(v), E, _p(ws), ws.numel() * 4, M, A, _p(y),
                                                            _act(x), MOE_MATH_WMMA_F16, _stream()))
     return y
 
@@ -247,7 +251,8 @@ def experts_gather(x, w: QWeight, E, ids, err, swiglu=False):
     M, A = ids.shape
     N = w.N // E
     y = torch.empty((M * A, N // 2 if swiglu else N), dtype=_act_dtype(x), device=x.device)
-    fn = L.lib().strix_linear_q4_experts_gather_swiglu if swiglu else L.lib().strix_linear_q4_experts_gather
+    fam = _fam(w.bits)
+    fn = getattr(L.lib(), f"strix_linear_{fam}_experts_gather_swiglu" if swiglu else f"strix_linear_{fam}_experts_gather")
     v = w.view()
     L.check(fn(_p(x), C.byref(v), E, _p(ids), M, A, _p(y), _act(x), _p(err), _stream()))
     return y
@@ -259,7 +264,7 @@ def experts_combine(h, w: QWeight, E, ids, coef, err):
     N = w.N // E
     y = torch.empty((M, N), dtype=_act_dtype(h), device=h.device)
     v = w.view()
-    L.check(L.lib().strix_linear_q4_experts_combine(_p(h), C.byref(v), E, _p(ids), _p(coef), M, A, _p(y), _act(h),
+    L.check(getattr(L.lib(), f"strix_linear_{_fam(w.bits)}_experts_combine")(_p(h), C.byref(v), E, _p(ids), _p(coef), M, A, _p(y), _act(h),
                                                     _p(err), _stream()))
     return y
 
