@@ -19,9 +19,10 @@
 // wave takes one row: lane l walks the row's 32-code chunks l, l + 64, ... (the 64 lanes' code loads are one
 // contiguous run of the row; a chunk lies inside one stream as d % 32 == 0), dots each with the chunk of every token
 // of the group (x rows from L2, one contiguous 4 KB run across the lanes) into per-stream sums, then a butterfly.
-// hc_mix_up: a thread owns an output column j for the group's tokens and walks the 4 streams' rows s d + j in turn;
-// consecutive threads read consecutive rows, which the chunk-major layout puts next to each other (one contiguous
-// run per 16-byte load instruction); the tokens' h live in LDS with each chunk's sum of h.
+// hc_mix_up: a block covers 64 output columns j; its thread (s, jl) owns row s d + j of W_up for the group's tokens,
+// so the 64 threads of a stream read 64 consecutive rows, which the chunk-major layout puts next to each other (one
+// contiguous run per 16-byte load instruction); a thread issues 8 chunks' loads before it uses them; the tokens' h live
+// in LDS with each chunk's sum of h, and the 4 streams' gated terms meet in LDS, summed in stream order.
 #include "common.hpp"
 
 #include <cmath>
@@ -141,12 +142,16 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
+constexpr int kUpCols = kThreads / kStreams;  // output columns a block (its threads: 4 streams x 64 columns)
+constexpr int kUpBatch = 8;                   // chunk loads a thread issues before it uses them
+
 template <typename T, int BITS, int MT>
 __global__ void __launch_bounds__(kThreads)
     hc_up_kernel(const float *h, const uint8_t *q, const uint16_t *scale, const uint16_t *minv, const T *x,
                  const float *norm_w, const float *inv, int64_t d, int64_t r, int64_t G, int64_t Tn, T *u) {
     __shared__ float hs[MT][kMaxR];
     __shared__ float hsum[MT][kMaxR / kChunk];
+    __shared__ float part[MT][kStreams][kUpCols];
     const int64_t t0 = (int64_t)blockIdx.y * MT;
     const int nt = (int)(Tn - t0 < MT ? Tn - t0 : MT);
     for (int i = threadIdx.x; i < nt * r; i += kThreads) hs[i / r][i % r] = h[(t0 + i / r) * r + i % r];
@@ -158,44 +163,56 @@ __global__ void __launch_bounds__(kThreads)
         hsum[i / nc][i % nc] = s;
     }
     __syncthreads();
-    const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x, N = kStreams * d;
-    if (j >= d) return;  // after the barriers
-    float sum[MT];
+    // thread (s, jl): row s d + j of W_up; the 64 threads of a stream read 64 consecutive rows (contiguous in the
+    // chunk-major layout)
+    const int s = threadIdx.x / kUpCols, jl = threadIdx.x % kUpCols;
+    const int64_t j = (int64_t)blockIdx.x * kUpCols + jl, N = kStreams * d;
+    const bool live = j < d;
+    const int64_t row = s * d + (live ? j : d - 1);
+    float acc[MT];
 #pragma unroll
-    for (int tt = 0; tt < MT; ++tt) sum[tt] = 0.f;
-    for (int s = 0; s < kStreams; ++s) {
-        const int64_t row = s * d + j;
-        float acc[MT];
+    for (int tt = 0; tt < MT; ++tt) acc[tt] = 0.f;
+    for (int c0 = 0; c0 < nc; c0 += kUpBatch) {
+        uint32_t w[kUpBatch][BITS];
+        float sc[kUpBatch], mn[kUpBatch];
 #pragma unroll
-        for (int tt = 0; tt < MT; ++tt) acc[tt] = 0.f;
-        for (int c = 0; c < nc; ++c) {
-            uint32_t w[BITS];
-            ld_chunk<BITS>(q + ((int64_t)c * N + row) * (kChunk * BITS / 8), w);
-            const int64_t gi = (int64_t)c * kChunk / G * N + row;
-            const float sc = bf16_to_f32(scale[gi]), mn = bf16_to_f32(minv[gi]);
+        for (int b = 0; b < kUpBatch; ++b)  // the batch's loads first (one round trip), then its math
+            if (c0 + b < nc) {
+                const int c = c0 + b;
+                ld_chunk<BITS>(q + ((int64_t)c * N + row) * (kChunk * BITS / 8), w[b]);
+                const int64_t gi = (int64_t)c * kChunk / G * N + row;
+                sc[b] = bf16_to_f32(scale[gi]), mn[b] = bf16_to_f32(minv[gi]);
+            }
+#pragma unroll
+        for (int b = 0; b < kUpBatch; ++b) {
+            const int c = c0 + b;
+            if (c >= nc) break;
 #pragma unroll
             for (int tt = 0; tt < MT; ++tt) {
                 if (tt >= nt) break;
                 float dot = 0.f;
 #pragma unroll
-                for (int k = 0; k < kChunk; ++k) dot = fmaf(hs[tt][c * kChunk + k], code_at<BITS>(w, k), dot);
-                acc[tt] = fmaf(sc, dot, fmaf(mn, hsum[tt][c], acc[tt]));
+                for (int k = 0; k < kChunk; ++k) dot = fmaf(hs[tt][c * kChunk + k], code_at<BITS>(w[b], k), dot);
+                acc[tt] = fmaf(sc[b], dot, fmaf(mn[b], hsum[tt][c], acc[tt]));
             }
         }
-        const float nw = 1.0f + norm_w[row];
-#pragma unroll
-        for (int tt = 0; tt < MT; ++tt) {
-            if (tt >= nt) break;
-            const int64_t t = t0 + tt;
-            const float g = 1.0f / (1.0f + expf(-acc[tt]));
-            sum[tt] += g * (ld_act(x, t * N + row) * inv[t * kStreams + s] * nw);
-        }
     }
+    const float nw = 1.0f + norm_w[row];
 #pragma unroll
     for (int tt = 0; tt < MT; ++tt) {
         if (tt >= nt) break;
-        st_act(u, (t0 + tt) * d + j, sum[tt] / (float)kStreams);
+        const int64_t t = t0 + tt;
+        const float g = 1.0f / (1.0f + expf(-acc[tt]));
+        part[tt][s][jl] = g * (ld_act(x, t * N + row) * inv[t * kStreams + s] * nw);
     }
+    __syncthreads();
+    if (s == 0 && live)  // the streams in order, as a running sum from 0
+        for (int tt = 0; tt < nt; ++tt) {
+            float sum = 0.f;
+#pragma unroll
+            for (int k = 0; k < kStreams; ++k) sum += part[tt][k][jl];
+            st_act(u, (t0 + tt) * d + j, sum / (float)kStreams);
+        }
 }
 
 struct QArr {
@@ -269,7 +286,7 @@ void mix_up(const float *h, const QArr &w, const void *x, const float *norm_w, c
     const int64_t es = act == Act::F32 ? 4 : 2;
     STRIX_CHECK(disjoint(u, T * d * es, x, T * H * d * es), fn, ": u overlaps the streams x");
     const int MT = tokens_per_block(T);
-    const dim3 grid((unsigned)((d + kThreads - 1) / kThreads), (unsigned)((T + MT - 1) / MT));
+    const dim3 grid((unsigned)((d + kUpCols - 1) / kUpCols), (unsigned)((T + MT - 1) / MT));
     auto go = [&](auto tc, auto mtc) {
         using TT = decltype(tc);
         hc_up_kernel<TT, BITS, decltype(mtc)::value><<<grid, kThreads, 0, stream>>>(
