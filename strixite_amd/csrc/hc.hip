@@ -71,7 +71,8 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-template <typename T, int BITS, int MT>
+// KS waves share a row (split over its chunks, sums meeting in LDS; 4 / KS rows a block)
+template <typename T, int BITS, int MT, int KS>
 __global__ void __launch_bounds__(kThreads)
     hc_down_kernel(const T *x, const uint8_t *q, const uint16_t *scale, const uint16_t *minv, int64_t R, int64_t K,
                    int64_t d, int64_t G, int64_t r, float eps, int64_t Tn, float *h, float *w_in, float *inv) {
@@ -83,6 +84,7 @@ __global__ void __launch_bounds__(kThreads)
     for (int tt = 0; tt < nt; ++tt) {
         const T *xs = x + (t0 + tt) * K + (int64_t)wave * d;
         float sq = 0.f;
+#pragma unroll 8
         for (int64_t i = 8 * lane; i < d; i += 8 * kWave) {
             float v[8];
             ld8(xs, i, v);
@@ -95,15 +97,18 @@ __global__ void __launch_bounds__(kThreads)
     __syncthreads();
     if (blockIdx.x == 0 && lane == 0)
         for (int tt = 0; tt < nt; ++tt) inv[(t0 + tt) * kStreams + wave] = invs[tt][wave];
-    const int64_t n = (int64_t)blockIdx.x * (kThreads / kWave) + wave;
-    if (n >= R) return;  // after the only barrier
+    constexpr int RPB = kThreads / kWave / KS;  // rows a block
+    const int64_t n = (int64_t)blockIdx.x * RPB + wave / KS;
+    const int kw = wave % KS;
+    if (KS == 1 && n >= R) return;  // after the only barrier (KS > 1: the grid holds whole rows)
     float acc[MT][kStreams];
 #pragma unroll
     for (int tt = 0; tt < MT; ++tt)
 #pragma unroll
         for (int s = 0; s < kStreams; ++s) acc[tt][s] = 0.f;
     const int64_t nc = K / kChunk;
-    for (int64_t c = lane; c < nc; c += kWave) {
+#pragma unroll 4
+    for (int64_t c = (int64_t)kw * kWave + lane; c < nc; c += (int64_t)kWave * KS) {
         uint32_t w[BITS];
         ld_chunk<BITS>(q + (n * nc + c) * (kChunk * BITS / 8), w);
         const int64_t gi = n * (K / G) + c * kChunk / G;
@@ -127,12 +132,32 @@ __global__ void __launch_bounds__(kThreads)
                 if (s == sg) acc[tt][s] += pv;
         }
     }
+    if constexpr (KS > 1) {  // the waves' per-stream sums meet in LDS; wave 0 adds them in wave order
+        __shared__ float red[KS][MT][kStreams];
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+            for (int s = 0; s < kStreams; ++s) {
+                const float v = wave_sum(acc[tt][s]);
+                if (lane == 0) red[kw][tt][s] = v;
+            }
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+            for (int s = 0; s < kStreams; ++s) {
+                float v = 0.f;
+                for (int k = 0; k < KS; ++k) v += red[k][tt][s];
+                acc[tt][s] = v;
+            }
+    }
 #pragma unroll
     for (int tt = 0; tt < MT; ++tt) {
         if (tt >= nt) break;
         float a = 0.f;
 #pragma unroll
-        for (int s = 0; s < kStreams; ++s) a = fmaf(invs[tt][s], wave_sum(acc[tt][s]), a);
+        for (int s = 0; s < kStreams; ++s) a = fmaf(invs[tt][s], KS > 1 ? acc[tt][s] : wave_sum(acc[tt][s]), a);
         if (lane == 0) {
             const int64_t t = t0 + tt;
             const float z = a / (float)kStreams;
@@ -253,11 +278,21 @@ void mix_down(const void *x, const QArr &w, int64_t T, int64_t H, int64_t d, int
     STRIX_CHECK(reinterpret_cast<uintptr_t>(x) % 16 == 0, fn, ": x must be 16-byte aligned");
     STRIX_CHECK(std::isfinite(eps) && eps > 0.f, fn, ": eps must be finite and > 0, got ", eps);
     const int MT = tokens_per_block(T);
-    const dim3 grid((unsigned)((R + kThreads / kWave - 1) / (kThreads / kWave)), (unsigned)((T + MT - 1) / MT));
+    // one token: a row's chunks split over the block's 4 waves (a round trip or two a lane, 4x the blocks); more
+    // tokens: 4 rows a block, each wave's code loads shared by its token group (splitting measured no faster at 5)
+    const bool split = T == 1;
+    const int64_t rpb = split ? 1 : kThreads / kWave;
+    const dim3 grid((unsigned)((R + rpb - 1) / rpb), (unsigned)((T + MT - 1) / MT));
     auto go = [&](auto tc, auto mtc) {
         using TT = decltype(tc);
-        hc_down_kernel<TT, BITS, decltype(mtc)::value><<<grid, kThreads, 0, stream>>>(
-            static_cast<const TT *>(x), w.q, w.scale, w.minv, R, w.K, d, w.G, r, eps, T, h, w_in, inv);
+        constexpr int MTV = decltype(mtc)::value;
+        if (split)
+            hc_down_kernel<TT, BITS, MTV, 4><<<grid, kThreads, 0, stream>>>(static_cast<const TT *>(x), w.q, w.scale,
+                                                                         w.minv, R, w.K, d, w.G, r, eps, T, h, w_in, inv);
+        else
+            hc_down_kernel<TT, BITS, MTV, 1><<<grid, kThreads, 0, stream>>>(static_cast<const TT *>(x), w.q, w.scale,
+                                                                           w.minv, R, w.K, d, w.G, r, eps, T, h, w_in,
+                                                                           inv);
     };
     auto by_mt = [&](auto tc) {
         switch (MT) {
