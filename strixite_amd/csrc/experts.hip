@@ -1394,8 +1394,9 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
     if (act == Act::F32) {  // FP32 per-slot partials, their ordered sum, the shared add (moe_shared_add, FP32)
         STRIX_CHECK(!h_f16, fn, ": the F16 h form goes with BF16 activations");
         STRIX_CHECK(ws != nullptr && ids != nullptr && coef != nullptr && partial != nullptr, fn, ": null pointer");
-        STRIX_CHECK(disjoint(partial, M * A * N * 4, y, M * N * 4) && disjoint(partial, M * A * N * 4, h, M * A * w.K * 4),
-                    fn, ": partial overlaps y or h");
+        STRIX_CHECK(disjoint(partial, M * A * N * 4, y, M * N * 4) && disjoint(partial, M * A * N * 4, h, M * A * w.K * 4) &&
+                        disjoint(y, M * N * 4, h, M * A * w.K * 4),
+                    fn, ": partial, y and h must not overlap");
         check_f32(fn, h, w, E, M, A, partial, M * A * N, M * A);
         STRIX_CHECK(ws_bytes >= moe_route_workspace_bytes(M, A, E), fn, ": workspace of ", ws_bytes, " bytes, needs ",
                     moe_route_workspace_bytes(M, A, E));
@@ -1600,7 +1601,8 @@ void linear_q5_experts_combine_grouped(const void *h, const Q5DeviceView &w, int
                 moe_route_workspace_bytes(M, A, E));
     STRIX_CHECK(N % 8 == 0 && reinterpret_cast<uintptr_t>(partial) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0,
                 fn, ": N = ", N, " must be a multiple of 8, partial and y 16-byte aligned");
-    STRIX_CHECK(disjoint(partial, M * A * N * 4, y, M * N * es), fn, ": partial overlaps y");
+    STRIX_CHECK(disjoint(partial, M * A * N * 4, y, M * N * es) && disjoint(y, M * N * es, h, M * A * v.K * es), fn,
+                ": partial, y and h must not overlap");
     if (shared != nullptr)
         STRIX_CHECK(shared->s != nullptr && shared->gate_logit != nullptr && shared->err != nullptr &&
                         shared->gate_ld >= 1 && reinterpret_cast<uintptr_t>(shared->s) % 16 == 0,
