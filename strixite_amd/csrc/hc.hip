@@ -71,8 +71,9 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// KS waves share a row (split over its chunks, sums meeting in LDS; 4 / KS rows a block)
-template <typename T, int BITS, int MT, int KS>
+// KS waves share a row (split over its chunks, sums meeting in LDS), or a wave takes RW consecutive rows and loads
+// each activation chunk once for them; 4 RW / KS rows a block
+template <typename T, int BITS, int MT, int KS, int RW>
 __global__ void __launch_bounds__(kThreads)
     hc_down_kernel(const T *x, const uint8_t *q, const uint16_t *scale, const uint16_t *minv, int64_t R, int64_t K,
                    int64_t d, int64_t G, int64_t r, float eps, int64_t Tn, float *h, float *w_in, float *inv) {
@@ -98,47 +99,65 @@ __global__ void __launch_bounds__(kThreads)
     if (blockIdx.x == 0 && lane == 0)
         for (int tt = 0; tt < nt; ++tt) inv[(t0 + tt) * kStreams + wave] = invs[tt][wave];
     constexpr int RPB = kThreads / kWave / KS;  // rows a block
-    const int64_t n = (int64_t)blockIdx.x * RPB + wave / KS;
+    const int64_t n0 = ((int64_t)blockIdx.x * RPB + wave / KS) * RW;  // the wave's first row
     const int kw = wave % KS;
-    if (KS == 1 && n >= R) return;  // after the only barrier (KS > 1: the grid holds whole rows)
-    float acc[MT][kStreams];
+    if (KS == 1 && n0 >= R) return;  // after the only barrier (KS > 1: the grid holds whole rows)
+    float acc[RW][MT][kStreams];
 #pragma unroll
-    for (int tt = 0; tt < MT; ++tt)
+    for (int rr = 0; rr < RW; ++rr)
 #pragma unroll
-        for (int s = 0; s < kStreams; ++s) acc[tt][s] = 0.f;
+        for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+            for (int s = 0; s < kStreams; ++s) acc[rr][tt][s] = 0.f;
     const int64_t nc = K / kChunk;
-#pragma unroll 4
+#pragma unroll 2
     for (int64_t c = (int64_t)kw * kWave + lane; c < nc; c += (int64_t)kWave * KS) {
-        uint32_t w[BITS];
-        ld_chunk<BITS>(q + (n * nc + c) * (kChunk * BITS / 8), w);
-        const int64_t gi = n * (K / G) + c * kChunk / G;
-        const float sc = bf16_to_f32(scale[gi]), mn = bf16_to_f32(minv[gi]);
+        uint32_t w[RW][BITS];
+        float sc[RW], mn[RW];
+#pragma unroll
+        for (int rr = 0; rr < RW; ++rr) {  // rows past R read the last one (not stored)
+            const int64_t n = n0 + rr < R ? n0 + rr : R - 1;
+            ld_chunk<BITS>(q + (n * nc + c) * (kChunk * BITS / 8), w[rr]);
+            const int64_t gi = n * (K / G) + c * kChunk / G;
+            sc[rr] = bf16_to_f32(scale[gi]), mn[rr] = bf16_to_f32(minv[gi]);
+        }
         const int sg = (int)(c * kChunk / d);
+        float cf[RW][kChunk];  // the codes as floats, once for the token group
+#pragma unroll
+        for (int rr = 0; rr < RW; ++rr)
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) cf[rr][k] = code_at<BITS>(w[rr], k);
 #pragma unroll
         for (int tt = 0; tt < MT; ++tt) {
             if (tt >= nt) break;
-            const T *xc = x + (t0 + tt) * K + c * kChunk;
-            float dot = 0.f, xsum = 0.f;
+            const T *xc = x + (t0 + tt) * K + c * kChunk;  // one load of the chunk for the wave's RW rows
+            float xv[kChunk], xsum = 0.f;
 #pragma unroll
             for (int p = 0; p < kChunk / 8; ++p) {
                 float v[8];
                 ld8(xc, 8 * p, v);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) dot = fmaf(v[k], code_at<BITS>(w, 8 * p + k), dot), xsum += v[k];
+                for (int k = 0; k < 8; ++k) xv[8 * p + k] = v[k], xsum += v[k];
             }
-            const float pv = fmaf(sc, dot, mn * xsum);
 #pragma unroll
-            for (int s = 0; s < kStreams; ++s)  // constant indices keep acc in registers
-                if (s == sg) acc[tt][s] += pv;
+            for (int rr = 0; rr < RW; ++rr) {
+                float dot = 0.f;
+#pragma unroll
+                for (int k = 0; k < kChunk; ++k) dot = fmaf(xv[k], cf[rr][k], dot);
+                const float pv = fmaf(sc[rr], dot, mn[rr] * xsum);
+#pragma unroll
+                for (int s = 0; s < kStreams; ++s)  // constant indices keep acc in registers
+                    if (s == sg) acc[rr][tt][s] += pv;
+            }
         }
     }
-    if constexpr (KS > 1) {  // the waves' per-stream sums meet in LDS; wave 0 adds them in wave order
+    if constexpr (KS > 1) {  // (RW 1) the waves' per-stream sums meet in LDS; wave 0 adds them in wave order
         __shared__ float red[KS][MT][kStreams];
 #pragma unroll
         for (int tt = 0; tt < MT; ++tt)
 #pragma unroll
             for (int s = 0; s < kStreams; ++s) {
-                const float v = wave_sum(acc[tt][s]);
+                const float v = wave_sum(acc[0][tt][s]);
                 if (lane == 0) red[kw][tt][s] = v;
             }
         __syncthreads();
@@ -149,20 +168,26 @@ __global__ void __launch_bounds__(kThreads)
             for (int s = 0; s < kStreams; ++s) {
                 float v = 0.f;
                 for (int k = 0; k < KS; ++k) v += red[k][tt][s];
-                acc[tt][s] = v;
+                acc[0][tt][s] = v;
             }
     }
 #pragma unroll
-    for (int tt = 0; tt < MT; ++tt) {
-        if (tt >= nt) break;
-        float a = 0.f;
+    for (int rr = 0; rr < RW; ++rr) {
+        const int64_t n = n0 + rr;
+        if (n >= R) break;
 #pragma unroll
-        for (int s = 0; s < kStreams; ++s) a = fmaf(invs[tt][s], KS > 1 ? acc[tt][s] : wave_sum(acc[tt][s]), a);
-        if (lane == 0) {
-            const int64_t t = t0 + tt;
-            const float z = a / (float)kStreams;
-            if (n < r) h[t * r + n] = z / (1.0f + expf(-z));
-            else w_in[t * kStreams + (n - r)] = 2.0f / (1.0f + expf(-z));
+        for (int tt = 0; tt < MT; ++tt) {
+            if (tt >= nt) break;
+            float a = 0.f;
+#pragma unroll
+            for (int s = 0; s < kStreams; ++s)
+                a = fmaf(invs[tt][s], KS > 1 ? acc[rr][tt][s] : wave_sum(acc[rr][tt][s]), a);
+            if (lane == 0) {
+                const int64_t t = t0 + tt;
+                const float z = a / (float)kStreams;
+                if (n < r) h[t * r + n] = z / (1.0f + expf(-z));
+                else w_in[t * kStreams + (n - r)] = 2.0f / (1.0f + expf(-z));
+            }
         }
     }
 }
@@ -281,18 +306,21 @@ void mix_down(const void *x, const QArr &w, int64_t T, int64_t H, int64_t d, int
     // one token: a row's chunks split over the block's 4 waves (a round trip or two a lane, 4x the blocks); more
     // tokens: 4 rows a block, each wave's code loads shared by its token group (splitting measured no faster at 5)
     const bool split = T == 1;
-    const int64_t rpb = split ? 1 : kThreads / kWave;
+    constexpr int kRW = 1;  // rows a wave when tokens share the waves' code loads (2: slower, measured)
+    const int64_t rpb = split ? 1 : kThreads / kWave * kRW;
     const dim3 grid((unsigned)((R + rpb - 1) / rpb), (unsigned)((T + MT - 1) / MT));
     auto go = [&](auto tc, auto mtc) {
         using TT = decltype(tc);
         constexpr int MTV = decltype(mtc)::value;
-        if (split)
-            hc_down_kernel<TT, BITS, MTV, 4><<<grid, kThreads, 0, stream>>>(static_cast<const TT *>(x), w.q, w.scale,
-                                                                         w.minv, R, w.K, d, w.G, r, eps, T, h, w_in, inv);
-        else
-            hc_down_kernel<TT, BITS, MTV, 1><<<grid, kThreads, 0, stream>>>(static_cast<const TT *>(x), w.q, w.scale,
-                                                                           w.minv, R, w.K, d, w.G, r, eps, T, h, w_in,
-                                                                           inv);
+        if constexpr (MTV == 1) {
+            if (split) {
+                hc_down_kernel<TT, BITS, 1, 4, 1><<<grid, kThreads, 0, stream>>>(
+                    static_cast<const TT *>(x), w.q, w.scale, w.minv, R, w.K, d, w.G, r, eps, T, h, w_in, inv);
+                return;
+            }
+        }
+        hc_down_kernel<TT, BITS, MTV, 1, kRW><<<grid, kThreads, 0, stream>>>(
+            static_cast<const TT *>(x), w.q, w.scale, w.minv, R, w.K, d, w.G, r, eps, T, h, w_in, inv);
     };
     auto by_mt = [&](auto tc) {
         switch (MT) {
