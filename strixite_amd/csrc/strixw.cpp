@@ -1,14 +1,22 @@
-// strixw reader, writer and hash (the format of strixite formats/strixw.hpp; reader and writer
-// formats/strixw.cpp:338-548, :231-336). Host code: the file is mapped read-only, every length read from the index
-// is checked against what is left of it before use, and every record against the sizes its encoding implies.
+// strixw: the converted-weights file (the format of strixite formats/strixw.hpp:16-27 and the hash of
+// formats/strixw.cpp:195-238; the byte layout and the hash arithmetic are the format, everything else here is this
+// library's own structure).
 //
-// Layout, little-endian throughout:
-//   header (128 bytes): magic "STRIXWT\0" | u32 version | u32 header bytes (128) | u64 index offset (128) |
-//     u64 index bytes | u64 data offset (4096-aligned) | u64 file bytes | u64 hash(index) | ... | u64 hash(bytes 0..119)
-//   index: u32 n_meta, {u16 len, key, u32 len, value} | u32 n_tensors, per tensor: u16 len, name | u8 encoding |
-//     u8 ndim, i64 dims | i64 group size | i64 experts | u16 n_parts, {u16 len, source, i64 row offset, i64 rows} |
-//     u8 n_components, {u8 role, u64 offset, u64 bytes, u64 hash}
-//   data: each tensor at a 4096-aligned offset, each of its components 256-aligned, in index order.
+// How this file is organised:
+//   * kEncodings — one table row per encoding: its name, whether it is block-quantized, the bytes per code, the
+//     multiple of K it needs. Names and component sizes are read off the table.
+//   * HeaderImage — the 128 header bytes as a struct whose field offsets are asserted at compile time.
+//   * Bytes — the one bounds-checked view used for everything read from a file: a sub-range is taken with
+//     Bytes::slice, which refuses to leave its parent, and the index is consumed front to back with Bytes::take.
+//   * One record codec: Codec<Dir>::record lists the fields of an index record once; the encoder appends them and the
+//     decoder reads them back in the same walk, so the writer and the reader cannot disagree on order or width.
+//   * The writer's layout is a pure function (plan_file: tensors → component offsets, index size, data offset,
+//     file size); the I/O (create_sized, put_all over the writer's descriptor) is kept apart from it.
+//   * The reader decodes the header and the index, then audits every record against the table (component roles and
+//     sizes, placement inside the data region, alignment, no overlap).
+//
+// Layout, little-endian: header (128 B) | index (at 128) | zero padding to 4096 | data (each tensor 4096-aligned,
+// each of its components 256-aligned, in index order).
 #include "strixite_strixw.hpp"
 
 #include "common.hpp"
@@ -19,258 +27,364 @@
 #include <unistd.h>
 
 #include <algorithm>
-#include <atomic>
 #include <cerrno>
+#include <cstddef>
 #include <cstring>
-#include <mutex>
-#include <set>
+#include <limits>
 #include <thread>
 
 namespace strix {
 
 namespace {
 
-constexpr uint8_t kMagic[8] = {'S', 'T', 'R', 'I', 'X', 'W', 'T', 0};
-// The hash's two odd multipliers: 2^64 / golden ratio, and a second 64-bit mixing constant.
+// ---- hash constants -------------------------------------------------------------------------------------------------
+// Two odd 64-bit multipliers (2^64 / golden ratio, and a second mixing constant) and a multiply-xorshift step.
 constexpr uint64_t kMulA = 0x9e3779b97f4a7c15ull, kMulB = 0xd6e8feb86659fd93ull;
 
-inline uint64_t absorb(uint64_t h, uint64_t word) {
-    h ^= word * kMulA;
-    h ^= h >> 31;
-    return h * kMulB;
+constexpr uint64_t step(uint64_t lane, uint64_t word) {
+    const uint64_t x = lane ^ (word * kMulA);
+    return (x ^ (x >> 31)) * kMulB;
 }
 
-inline uint64_t load64(const uint8_t *p) {
-    uint64_t v;
-    std::memcpy(&v, p, 8);
+uint64_t le64(const uint8_t *p, size_t n = 8) {  // n ≤ 8 bytes, zero-extended
+    uint64_t v = 0;
+    std::memcpy(&v, p, n);
     return v;
 }
 
-inline uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
-
-std::string dims(const std::vector<int64_t> &s) {
-    std::string r = "[";
-    for (size_t i = 0; i < s.size(); ++i) r += (i ? ", " : "") + std::to_string(s[i]);
-    return r + "]";
-}
-
-// Index encoding: a growing byte vector.
-struct Out {
-    std::vector<uint8_t> b;
-    template <typename T> void num(T v) {
-        const size_t at = b.size();
-        b.resize(at + sizeof(T));
-        std::memcpy(b.data() + at, &v, sizeof(T));
-    }
-    void str16(const std::string &s, const char *what) {
-        STRIX_CHECK(s.size() <= 0xffff, "strixw: ", what, " of ", s.size(), " bytes (limit 65535)");
-        num<uint16_t>((uint16_t)s.size());
-        b.insert(b.end(), s.begin(), s.end());
-    }
+// ---- the encoding table ---------------------------------------------------------------------------------------------
+struct EncodingRow {
+    StrixwEncoding id;
+    const char *name;
+    bool quantized;     // q + scale + min components over a [N, K] matrix, groups of G along K
+    int code_num, code_den;  // bytes of codes per element = num / den (plain encodings: bytes per element)
+    int64_t k_multiple;      // K must be a multiple of this (besides G)
 };
 
-// Index decoding with every read bounded by what is left.
-struct In {
-    const uint8_t *p;
-    uint64_t n, at;
-    const std::string &where;
-    template <typename T> T num(const char *what) {
-        STRIX_CHECK(n - at >= sizeof(T), where, ": the index ends inside ", what, " (index byte ", at, " of ", n, ")");
+constexpr EncodingRow kEncodings[] = {
+    {StrixwEncoding::Q4RowMajor, "q4", true, 1, 2, 1},
+    {StrixwEncoding::Q4ChunkMajor, "q4-chunk-major", true, 1, 2, 1},
+    {StrixwEncoding::BF16, "bf16", false, 2, 1, 1},
+    {StrixwEncoding::F32, "f32", false, 4, 1, 1},
+    {StrixwEncoding::I64, "i64", false, 8, 1, 1},
+    {StrixwEncoding::Q8RowMajor, "q8", true, 1, 1, 1},
+    {StrixwEncoding::Q8ChunkMajor, "q8-chunk-major", true, 1, 1, 1},
+    {StrixwEncoding::Q6RowMajor, "q6", true, 3, 4, 64},   // a 4-bit plane [K/2] then a 2-bit plane [K/4] per row
+    {StrixwEncoding::Q5RowMajor, "q5", true, 5, 8, 128},  // a 4-bit plane [K/2] then a 1-bit plane [K/8] per row
+};
+
+const EncodingRow *encoding_row(StrixwEncoding e) {
+    for (const EncodingRow &r : kEncodings)
+        if (r.id == e) return &r;
+    return nullptr;
+}
+
+constexpr const char *kRoleNames[] = {"data", "q", "scale", "min"};
+
+std::string shape_text(const std::vector<int64_t> &s) {
+    std::string r;
+    for (int64_t d : s) r += (r.empty() ? "" : " x ") + std::to_string(d);
+    return "[" + r + "]";
+}
+
+constexpr uint64_t align_to(uint64_t v, uint64_t a) { return v % a ? v + (a - v % a) : v; }
+
+// ---- the header -----------------------------------------------------------------------------------------------------
+struct HeaderImage {
+    char magic[8];
+    uint32_t version, header_bytes;
+    uint64_t index_offset, index_bytes, data_offset, file_bytes, index_hash;
+    uint8_t reserved[64];
+    uint64_t header_hash;  // hash of bytes [0, 120)
+};
+static_assert(sizeof(HeaderImage) == kStrixwHeaderBytes);
+static_assert(offsetof(HeaderImage, version) == 8 && offsetof(HeaderImage, header_bytes) == 12);
+static_assert(offsetof(HeaderImage, index_offset) == 16 && offsetof(HeaderImage, index_bytes) == 24);
+static_assert(offsetof(HeaderImage, data_offset) == 32 && offsetof(HeaderImage, file_bytes) == 40);
+static_assert(offsetof(HeaderImage, index_hash) == 48 && offsetof(HeaderImage, header_hash) == 120);
+constexpr char kMagic[8] = {'S', 'T', 'R', 'I', 'X', 'W', 'T', '\0'};
+
+HeaderImage make_header(uint64_t index_bytes, uint64_t data_offset, uint64_t file_bytes, uint64_t index_hash) {
+    HeaderImage h{};
+    std::memcpy(h.magic, kMagic, 8);
+    h.version = kStrixwVersion;
+    h.header_bytes = kStrixwHeaderBytes;
+    h.index_offset = kStrixwHeaderBytes;
+    h.index_bytes = index_bytes, h.data_offset = data_offset, h.file_bytes = file_bytes, h.index_hash = index_hash;
+    h.header_hash = strix_hash64(&h, offsetof(HeaderImage, header_hash));
+    return h;
+}
+
+// ---- Bytes: the one bounds-checked view -----------------------------------------------------------------------------
+struct Bytes {
+    const uint8_t *base = nullptr;
+    uint64_t size = 0;
+    const std::string *owner = nullptr;  // names the file in messages
+
+    Bytes slice(uint64_t off, uint64_t n, const char *what) const {
+        STRIX_CHECK(off <= size && n <= size - off, "strixw '", *owner, "': ", what, " [", off, ", +", n,
+                    ") lies past the end of a ", size, "-byte range");
+        return Bytes{base + off, n, owner};
+    }
+    // Consumes n bytes from the front.
+    Bytes take(uint64_t n, const char *what) {
+        STRIX_CHECK(n <= size, "strixw '", *owner, "': the index runs out while reading ", what, " (", n,
+                    " bytes wanted, ", size, " left)");
+        Bytes head{base, n, owner};
+        base += n, size -= n;
+        return head;
+    }
+    template <typename T> T take_le(const char *what) {
         T v;
-        std::memcpy(&v, p + at, sizeof(T));
-        at += sizeof(T);
+        std::memcpy(&v, take(sizeof(T), what).base, sizeof(T));
         return v;
     }
-    std::string bytes(uint64_t len, const char *what) {
-        STRIX_CHECK(n - at >= len, where, ": the index ends inside ", what, " (", len, " bytes at index byte ", at,
-                    " of ", n, ")");
-        std::string s(reinterpret_cast<const char *>(p + at), (size_t)len);
-        at += len;
-        return s;
+};
+
+// ---- the record codec -----------------------------------------------------------------------------------------------
+// Codec<true> appends to a byte vector; Codec<false> reads from a Bytes view. Both run record() / metadata().
+template <bool kEncode> struct Codec {
+    std::vector<uint8_t> *out = nullptr;  // encode
+    Bytes in{};                            // decode
+
+    template <typename Wire, typename V> void scalar(V &v, const char *what) {
+        if constexpr (kEncode) {
+            const Wire w = static_cast<Wire>(v);
+            const auto *p = reinterpret_cast<const uint8_t *>(&w);
+            out->insert(out->end(), p, p + sizeof(Wire));
+        } else {
+            v = static_cast<V>(in.take_le<Wire>(what));
+        }
+    }
+    template <typename Len> void text(std::string &s, const char *what) {
+        if constexpr (kEncode) {
+            STRIX_CHECK(s.size() <= std::numeric_limits<Len>::max(), "strixw: ", what, " is ", s.size(),
+                        " bytes long; its length field holds at most ", (uint64_t)std::numeric_limits<Len>::max());
+            Len n = (Len)s.size();
+            scalar<Len>(n, what);
+            out->insert(out->end(), s.begin(), s.end());
+        } else {
+            const Len n = in.take_le<Len>(what);
+            const Bytes b = in.take(n, what);
+            s.assign(reinterpret_cast<const char *>(b.base), n);
+        }
+    }
+    // A counted list: count as Len, then each element through fn.
+    template <typename Len, typename T, typename Fn> void list(std::vector<T> &v, const char *what, Fn fn) {
+        uint64_t n = v.size();
+        if constexpr (kEncode) {
+            STRIX_CHECK(n <= std::numeric_limits<Len>::max(), "strixw: ", n, " ", what, " in one record; the count "
+                        "field holds at most ", (uint64_t)std::numeric_limits<Len>::max());
+        }
+        scalar<Len>(n, what);
+        if constexpr (!kEncode) v.clear();
+        for (uint64_t i = 0; i < n; ++i) {
+            if constexpr (!kEncode) v.emplace_back();
+            fn(v[i]);
+        }
+    }
+
+    void record(StrixwTensor &t) {
+        text<uint16_t>(t.name, "a tensor name");
+        scalar<uint8_t>(t.encoding, "an encoding");
+        list<uint8_t>(t.shape, "dimensions", [&](int64_t &d) { scalar<int64_t>(d, "a dimension"); });
+        scalar<int64_t>(t.group_size, "a group size");
+        scalar<int64_t>(t.experts, "an expert count");
+        list<uint16_t>(t.parts, "source parts", [&](StrixwPart &p) {
+            text<uint16_t>(p.source, "a part's source name");
+            scalar<int64_t>(p.row_offset, "a part's first row");
+            scalar<int64_t>(p.rows, "a part's row count");
+        });
+        list<uint8_t>(t.components, "components", [&](StrixwComponent &c) {
+            scalar<uint8_t>(c.role, "a component role");
+            scalar<uint64_t>(c.offset, "a component offset");
+            scalar<uint64_t>(c.bytes, "a component size");
+            scalar<uint64_t>(c.hash, "a component hash");
+        });
+    }
+    void metadata(std::vector<std::pair<std::string, std::string>> &kv) {
+        list<uint32_t>(kv, "metadata entries", [&](std::pair<std::string, std::string> &e) {
+            text<uint16_t>(e.first, "a metadata key");
+            text<uint32_t>(e.second, "a metadata value");
+        });
     }
 };
 
-// What writer and reader both require of a record, components aside.
-void check_record(const StrixwTensor &t, const std::string &where) {
-    STRIX_CHECK(!t.name.empty(), where, ": a tensor with an empty name");
-    STRIX_CHECK(!t.shape.empty() && t.shape.size() <= 8, where, ": tensor '", t.name, "' has ", t.shape.size(),
-                " dims (1..8)");
-    for (int64_t d : t.shape) STRIX_CHECK(d >= 1, where, ": tensor '", t.name, "' has shape ", dims(t.shape));
-    STRIX_CHECK(t.experts >= 0 && (t.experts == 0 || t.shape[0] % t.experts == 0), where, ": tensor '", t.name, "': ",
-                t.shape[0], " rows do not split into ", t.experts, " experts");
-    int64_t row = 0;
+std::vector<uint8_t> encode_index(const std::map<std::string, std::string> &meta,
+                                  const std::vector<StrixwTensor> &tensors) {
+    std::vector<uint8_t> bytes;
+    Codec<true> c{&bytes};
+    std::vector<std::pair<std::string, std::string>> kv(meta.begin(), meta.end());
+    c.metadata(kv);
+    auto copy = tensors;  // the codec takes references; encoding does not change them
+    c.list<uint32_t>(copy, "tensors", [&](StrixwTensor &t) { c.record(t); });
+    return bytes;
+}
+
+// ---- record rules shared by writer and reader -----------------------------------------------------------------------
+// Everything a record must satisfy apart from its components' placement; `who` prefixes the messages.
+void require_well_formed(const StrixwTensor &t, const std::string &who) {
+    STRIX_CHECK(!t.name.empty(), who, ": a record has no name");
+    STRIX_CHECK(t.shape.size() >= 1 && t.shape.size() <= 8, who, ": '", t.name, "' has rank ", t.shape.size(),
+                "; ranks 1 to 8 are allowed");
+    STRIX_CHECK(std::all_of(t.shape.begin(), t.shape.end(), [](int64_t d) { return d > 0; }), who, ": '", t.name,
+                "' has a non-positive dimension in ", shape_text(t.shape));
+    STRIX_CHECK(t.experts >= 0, who, ": '", t.name, "' has expert count ", t.experts);
+    STRIX_CHECK(t.experts == 0 || t.shape[0] % t.experts == 0, who, ": '", t.name, "' stacks ", t.experts,
+                " experts in ", t.shape[0], " rows, not a whole number of rows each");
+    int64_t covered = 0;
     for (const StrixwPart &p : t.parts) {
-        STRIX_CHECK(!p.source.empty() && p.rows >= 1 && p.row_offset == row, where, ": tensor '", t.name, "' part '",
-                    p.source, "' at row ", p.row_offset, " (", p.rows, " rows); the next part must start at row ", row);
-        row += p.rows;
+        STRIX_CHECK(!p.source.empty(), who, ": '", t.name, "' has a part with no source name");
+        STRIX_CHECK(p.rows > 0 && p.row_offset == covered, who, ": '", t.name, "' part from '", p.source,
+                    "' claims rows ", p.row_offset, "..+", p.rows, " where the parts so far reach row ", covered,
+                    " (parts must tile the rows in order)");
+        covered += p.rows;
     }
-    STRIX_CHECK(t.parts.empty() || row == t.shape[0], where, ": tensor '", t.name, "': its parts cover ", row,
-                " of ", t.shape[0], " rows");
+    STRIX_CHECK(t.parts.empty() || covered == t.shape[0], who, ": the parts of '", t.name, "' end at row ", covered,
+                " of ", t.shape[0]);
 }
 
-void encode_index(Out &o, const std::map<std::string, std::string> &meta, const std::vector<StrixwTensor> &ts) {
-    o.num<uint32_t>((uint32_t)meta.size());
-    for (const auto &[k, v] : meta) {
-        o.str16(k, "metadata key");
-        STRIX_CHECK(v.size() <= 0xffffffffull, "strixw: metadata '", k, "' too long");
-        o.num<uint32_t>((uint32_t)v.size());
-        o.b.insert(o.b.end(), v.begin(), v.end());
-    }
-    o.num<uint32_t>((uint32_t)ts.size());
-    for (const StrixwTensor &t : ts) {
-        o.str16(t.name, "tensor name");
-        o.num<uint8_t>((uint8_t)t.encoding);
-        o.num<uint8_t>((uint8_t)t.shape.size());
-        for (int64_t d : t.shape) o.num<int64_t>(d);
-        o.num<int64_t>(t.group_size);
-        o.num<int64_t>(t.experts);
-        STRIX_CHECK(t.parts.size() <= 0xffff, "strixw: tensor '", t.name, "' has ", t.parts.size(), " parts");
-        o.num<uint16_t>((uint16_t)t.parts.size());
-        for (const StrixwPart &p : t.parts) {
-            o.str16(p.source, "part source name");
-            o.num<int64_t>(p.row_offset);
-            o.num<int64_t>(p.rows);
-        }
-        o.num<uint8_t>((uint8_t)t.components.size());
-        for (const StrixwComponent &c : t.components) {
-            o.num<uint8_t>((uint8_t)c.role);
-            o.num<uint64_t>(c.offset);
-            o.num<uint64_t>(c.bytes);
-            o.num<uint64_t>(c.hash);
+// ---- the writer's layout (pure) -------------------------------------------------------------------------------------
+struct FilePlan {
+    uint64_t index_bytes = 0, data_offset = 0, file_bytes = 0;
+};
+
+// Fills every component's offset; the index size does not depend on the offsets or hashes (fixed-width fields).
+FilePlan plan_file(const std::map<std::string, std::string> &meta, std::vector<StrixwTensor> &tensors) {
+    FilePlan p;
+    p.index_bytes = encode_index(meta, tensors).size();
+    p.data_offset = align_to(kStrixwHeaderBytes + p.index_bytes, kStrixwTensorAlign);
+    uint64_t end = p.data_offset;
+    for (StrixwTensor &t : tensors) {
+        end = align_to(end, kStrixwTensorAlign);
+        for (StrixwComponent &c : t.components) {
+            end = align_to(end, kStrixwComponentAlign);
+            c.offset = end;
+            end += c.bytes;
         }
     }
+    p.file_bytes = end;
+    return p;
 }
 
-void write_at(int fd, const void *data, size_t n, uint64_t off, const std::string &where) {
-    const auto *p = static_cast<const uint8_t *>(data);
-    while (n > 0) {
-        const ssize_t w = ::pwrite(fd, p, std::min<size_t>(n, size_t(1) << 30), (off_t)off);
-        if (w < 0 && errno == EINTR) continue;
-        STRIX_CHECK(w > 0, where, ": write of ", n, " bytes at ", off, " failed: ",
-                    w < 0 ? std::strerror(errno) : "nothing written");
-        p += w, n -= (size_t)w, off += (uint64_t)w;
+// ---- file I/O (the writer owns the descriptor; these helpers never close it on error) -----------------------------
+int create_sized(const std::string &path, uint64_t size) {
+    const int fd = ::open(path.c_str(), O_WRONLY | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
+    STRIX_CHECK(fd >= 0, "strixw writer: cannot create '", path, "': ", std::strerror(errno));
+    if (::ftruncate(fd, (off_t)size) != 0) {
+        const int e = errno;
+        ::close(fd);
+        STRIX_CHECK(false, "strixw writer: cannot size '", path, "' to ", size, " bytes: ", std::strerror(e));
+    }
+    return fd;
+}
+
+void put_all(int fd, const std::string &path, uint64_t at, const void *src, uint64_t n) {
+    const uint8_t *s = static_cast<const uint8_t *>(src);
+    for (uint64_t done = 0; done < n;) {
+        const ssize_t r = ::pwrite(fd, s + done, (size_t)std::min<uint64_t>(n - done, 1ull << 30), (off_t)(at + done));
+        if (r < 0 && errno == EINTR) continue;
+        STRIX_CHECK(r > 0, "strixw writer: '", path, "' refused ", n - done, " bytes at offset ", at + done, ": ",
+                    r < 0 ? std::strerror(errno) : "no progress");
+        done += (uint64_t)r;
     }
 }
 
 }  // namespace
 
+// ---- names, sizes ---------------------------------------------------------------------------------------------------
 const char *strixw_encoding_name(StrixwEncoding e) {
-    switch (e) {
-        case StrixwEncoding::Q4RowMajor: return "q4";
-        case StrixwEncoding::Q4ChunkMajor: return "q4-chunk-major";
-        case StrixwEncoding::BF16: return "bf16";
-        case StrixwEncoding::F32: return "f32";
-        case StrixwEncoding::I64: return "i64";
-        case StrixwEncoding::Q8RowMajor: return "q8";
-        case StrixwEncoding::Q8ChunkMajor: return "q8-chunk-major";
-        case StrixwEncoding::Q6RowMajor: return "q6";
-        case StrixwEncoding::Q5RowMajor: return "q5";
-    }
-    return "unknown";
+    const EncodingRow *r = encoding_row(e);
+    return r ? r->name : "unknown";
 }
 
 const char *strixw_role_name(StrixwRole r) {
-    switch (r) {
-        case StrixwRole::Data: return "data";
-        case StrixwRole::Q: return "q";
-        case StrixwRole::Scale: return "scale";
-        case StrixwRole::Min: return "min";
-    }
-    return "unknown";
+    const unsigned i = static_cast<unsigned>(r);
+    return i < 4 ? kRoleNames[i] : "unknown";
 }
 
 int64_t StrixwTensor::numel() const {
-    int64_t n = 1;
+    __int128 n = 1;
     for (int64_t d : shape) {
-        STRIX_CHECK(d >= 1 && n <= INT64_MAX / d, "strixw tensor '", name, "': shape ", dims(shape));
+        STRIX_CHECK(d > 0, "strixw: '", name, "' has shape ", shape_text(shape));
         n *= d;
+        STRIX_CHECK(n <= INT64_MAX, "strixw: '", name, "' of shape ", shape_text(shape), " has more than 2^63 elements");
     }
-    return n;
+    return (int64_t)n;
 }
 
 uint64_t StrixwTensor::bytes() const {
-    uint64_t n = 0;
-    for (const StrixwComponent &c : components) n += c.bytes;
-    return n;
+    uint64_t sum = 0;
+    for (const StrixwComponent &c : components) sum += c.bytes;
+    return sum;
 }
 
 std::vector<StrixwComponent> strixw_components(const StrixwTensor &t) {
+    const EncodingRow *row = encoding_row(t.encoding);
+    STRIX_CHECK(row != nullptr, "strixw: '", t.name, "' has encoding code ", (int)t.encoding,
+                ", which this reader does not know");
     const int64_t n = t.numel();
-    const char *enc = strixw_encoding_name(t.encoding);
-    auto one = [](StrixwRole r, int64_t b) { return StrixwComponent{r, 0, (uint64_t)b, 0}; };
-    // Quantized row-major / chunk-major encodings: [N, K] codes in groups of G along K, a bf16 scale and a bf16
-    // minimum per group; the code plane holds K bits/8 bytes a row (Q6: a K/2 low plane + K/4 high; Q5: K/2 + K/8).
-    auto quant = [&](int64_t plane_num, int64_t plane_den, int64_t k_multiple) {
-        STRIX_CHECK(t.shape.size() == 2, "strixw tensor '", t.name, "': ", enc, " needs shape [N, K], got ",
-                    dims(t.shape));
-        const int64_t N = t.shape[0], K = t.shape[1], G = t.group_size;
-        STRIX_CHECK((G == 32 || G == 64 || G == 128) && K % G == 0 && K % k_multiple == 0, "strixw tensor '", t.name,
-                    "': ", enc, " with K = ", K, ", group size ", G, " (G 32, 64 or 128 dividing K; K a multiple of ",
-                    k_multiple, ")");
-        return std::vector<StrixwComponent>{one(StrixwRole::Q, N * K * plane_num / plane_den),
-                                            one(StrixwRole::Scale, N * (K / G) * 2),
-                                            one(StrixwRole::Min, N * (K / G) * 2)};
+    auto sized = [](StrixwRole r, __int128 b) {
+        STRIX_CHECK(b >= 0 && b <= INT64_MAX, "strixw: a component of ", (long double)b, " bytes");
+        return StrixwComponent{r, 0, (uint64_t)b, 0};
     };
-    switch (t.encoding) {
-        case StrixwEncoding::Q4RowMajor:
-        case StrixwEncoding::Q4ChunkMajor: return quant(1, 2, 1);
-        case StrixwEncoding::Q8RowMajor:
-        case StrixwEncoding::Q8ChunkMajor: return quant(1, 1, 1);
-        case StrixwEncoding::Q6RowMajor: return quant(3, 4, 64);
-        case StrixwEncoding::Q5RowMajor: return quant(5, 8, 128);
-        case StrixwEncoding::BF16:
-        case StrixwEncoding::F32:
-        case StrixwEncoding::I64: {
-            STRIX_CHECK(t.group_size == 0, "strixw tensor '", t.name, "': ", enc, " with group size ", t.group_size,
-                        " (must be 0)");
-            const int64_t es = t.encoding == StrixwEncoding::BF16 ? 2 : t.encoding == StrixwEncoding::F32 ? 4 : 8;
-            STRIX_CHECK(n <= INT64_MAX / es, "strixw tensor '", t.name, "': ", n, " elements overflow");
-            return {one(StrixwRole::Data, n * es)};
-        }
+    if (!row->quantized) {
+        STRIX_CHECK(t.group_size == 0, "strixw: '", t.name, "' is ", row->name, " but carries group size ",
+                    t.group_size, " (plain encodings have none)");
+        return {sized(StrixwRole::Data, (__int128)n * row->code_num)};
     }
-    STRIX_CHECK(false, "strixw tensor '", t.name, "': unknown encoding ", (int)t.encoding);
-    return {};
+    STRIX_CHECK(t.shape.size() == 2, "strixw: '", t.name, "' is ", row->name, " and must be a matrix [N, K], not ",
+                shape_text(t.shape));
+    const int64_t N = t.shape[0], K = t.shape[1], G = t.group_size;
+    const bool g_ok = G == 32 || G == 64 || G == 128;
+    STRIX_CHECK(g_ok && K % G == 0 && K % row->k_multiple == 0, "strixw: '", t.name, "' (", row->name, ", K ", K,
+                ") has group size ", G, "; the group size must be 32, 64 or 128 and divide K",
+                row->k_multiple > 1 ? ", and K must be a multiple of " + std::to_string(row->k_multiple) : "");
+    const __int128 params = (__int128)N * (K / G) * 2;  // one bf16 per group
+    return {sized(StrixwRole::Q, (__int128)N * K * row->code_num / row->code_den), sized(StrixwRole::Scale, params),
+            sized(StrixwRole::Min, params)};
 }
 
-// ---- hash -----------------------------------------------------------------------------------------------------
-// Four lanes seeded by the total length n (n ^ A, n ^ B, ~n ^ A, ~n ^ B); each 32-byte block feeds its four 8-byte
-// words to the four lanes. The tail (< 32 bytes): its whole 8-byte words to lanes 0, 1, 2 in turn, then the last
-// 1..7 bytes, zero-extended with their count in the top byte, to lane 0. The lanes fold in order 0..3 and a final
-// xorshift-multiply-xorshift finishes (strixite formats/strixw.cpp:204-238).
-StrixHasher::StrixHasher(size_t n)
-    : total_(n), lane_{n ^ kMulA, n ^ kMulB, ~(uint64_t)n ^ kMulA, ~(uint64_t)n ^ kMulB} {}
+// ---- the hash -------------------------------------------------------------------------------------------------------
+// Four lanes seeded by the total length; every 32-byte block feeds its four 64-bit words to the four lanes; the tail
+// (< 32 bytes) feeds its whole words to lanes 0, 1, 2 and its last partial word, tagged with its length in the top
+// byte, to lane 0; the lanes are folded in order and finished with two xorshift rounds around a multiply.
+StrixHasher::StrixHasher(size_t n) : total_(n) {
+    lane_[0] = (uint64_t)n ^ kMulA;
+    lane_[1] = (uint64_t)n ^ kMulB;
+    lane_[2] = ~(uint64_t)n ^ kMulA;
+    lane_[3] = ~(uint64_t)n ^ kMulB;
+}
 
 void StrixHasher::block(const uint8_t *p) {
-    for (int i = 0; i < 4; ++i) lane_[i] = absorb(lane_[i], load64(p + 8 * i));
+    for (int l = 0; l < 4; ++l) lane_[l] = step(lane_[l], le64(p + 8 * l));
 }
 
 void StrixHasher::update(const void *data, size_t len) {
-    STRIX_CHECK(len <= total_ - fed_, "StrixHasher: ", len, " more bytes after ", fed_, " of ", total_);
-    const auto *p = static_cast<const uint8_t *>(data);
+    STRIX_CHECK(len <= total_ - fed_, "StrixHasher: fed ", fed_, " + ", len, " bytes, past the declared length ",
+                total_);
+    const uint8_t *p = static_cast<const uint8_t *>(data);
     fed_ += len;
-    if (tail_len_ > 0) {
-        const size_t take = std::min(len, 32 - tail_len_);
-        std::memcpy(tail_ + tail_len_, p, take);
-        tail_len_ += take, p += take, len -= take;
-        if (tail_len_ < 32) return;
-        block(tail_);
-        tail_len_ = 0;
+    while (len > 0) {
+        if (tail_len_ == 0 && len >= 32) {  // aligned with the block grid: straight from the caller's memory
+            block(p);
+            p += 32, len -= 32;
+            continue;
+        }
+        const size_t n = std::min(len, 32 - tail_len_);
+        std::memcpy(tail_ + tail_len_, p, n);
+        tail_len_ += n, p += n, len -= n;
+        if (tail_len_ == 32) block(tail_), tail_len_ = 0;
     }
-    for (; len >= 32; p += 32, len -= 32) block(p);
-    std::memcpy(tail_, p, len);
-    tail_len_ = len;
 }
 
 uint64_t StrixHasher::final() {
-    STRIX_CHECK(fed_ == total_, "StrixHasher::final: ", fed_, " of ", total_, " bytes fed");
-    size_t i = 0;
-    for (int l = 0; i + 8 <= tail_len_; i += 8, ++l) lane_[l] = absorb(lane_[l], load64(tail_ + i));
-    if (i < tail_len_) {
-        uint64_t w = 0;
-        std::memcpy(&w, tail_ + i, tail_len_ - i);
-        lane_[0] = absorb(lane_[0], w ^ ((uint64_t)(tail_len_ - i) << 56));
-    }
-    uint64_t r = absorb(absorb(absorb(lane_[0], lane_[1]), lane_[2]), lane_[3]);
+    STRIX_CHECK(fed_ == total_, "StrixHasher: final() after ", fed_, " of the declared ", total_, " bytes");
+    const size_t words = tail_len_ / 8, rest = tail_len_ % 8;
+    for (size_t w = 0; w < words; ++w) lane_[w] = step(lane_[w], le64(tail_ + 8 * w));
+    if (rest) lane_[0] = step(lane_[0], le64(tail_ + 8 * words, rest) ^ ((uint64_t)rest << 56));
+    uint64_t r = lane_[0];
+    for (int l = 1; l < 4; ++l) r = step(r, lane_[l]);
     r = (r ^ (r >> 33)) * kMulA;
     return r ^ (r >> 29);
 }
@@ -281,37 +395,29 @@ uint64_t strix_hash64(const void *p, size_t n) {
     return h.final();
 }
 
-// ---- writer ---------------------------------------------------------------------------------------------------
+// ---- writer ---------------------------------------------------------------------------------------------------------
+
 StrixwWriter::StrixwWriter(const std::string &path, std::map<std::string, std::string> meta,
                            std::vector<StrixwTensor> tensors)
     : path_(path), meta_(std::move(meta)), tensors_(std::move(tensors)) {
-    const std::string where = "StrixwWriter('" + path + "')";
-    STRIX_CHECK(!path.empty() && !tensors_.empty(), where, ": needs a path and at least one tensor");
-    std::set<std::string> seen;
+    const std::string who = "strixw writer '" + path + "'";
+    STRIX_CHECK(!path.empty(), "strixw writer: no path given");
+    STRIX_CHECK(!tensors_.empty(), who, ": the plan holds no tensors");
+    std::vector<std::string> names;
     for (StrixwTensor &t : tensors_) {
-        check_record(t, where);
-        STRIX_CHECK(seen.insert(t.name).second, where, ": tensor '", t.name, "' planned twice");
+        require_well_formed(t, who);
         t.components = strixw_components(t);
+        names.push_back(t.name);
     }
-    Out o;
-    encode_index(o, meta_, tensors_);  // hashes are fixed-width: the index size is final now
-    index_bytes_ = o.b.size();
-    data_offset_ = round_up(kStrixwHeaderBytes + index_bytes_, kStrixwTensorAlign);
-    uint64_t at = data_offset_;
-    for (StrixwTensor &t : tensors_) {
-        at = round_up(at, kStrixwTensorAlign);
-        for (StrixwComponent &c : t.components) {
-            at = round_up(at, kStrixwComponentAlign);
-            c.offset = at;
-            at += c.bytes;
-        }
-        done_.emplace_back(t.components.size(), false);
-    }
-    file_bytes_ = at;
-    fd_ = ::open(path.c_str(), O_WRONLY | O_CREAT | O_TRUNC | O_CLOEXEC, 0644);
-    STRIX_CHECK(fd_ >= 0, where, ": open failed: ", std::strerror(errno));
-    STRIX_CHECK(::ftruncate(fd_, (off_t)file_bytes_) == 0, where, ": ftruncate to ", file_bytes_, " bytes failed: ",
-                std::strerror(errno));
+    std::sort(names.begin(), names.end());
+    const auto dup = std::adjacent_find(names.begin(), names.end());
+    STRIX_CHECK(dup == names.end(), who, ": the plan names '", dup == names.end() ? "" : *dup,
+                "' more than once (duplicate tensor)");
+    const FilePlan plan = plan_file(meta_, tensors_);
+    index_bytes_ = plan.index_bytes, data_offset_ = plan.data_offset, file_bytes_ = plan.file_bytes;
+    for (const StrixwTensor &t : tensors_) done_.emplace_back(t.components.size(), false);
+
+    fd_ = create_sized(path, file_bytes_);
     put_header_and_index();
 }
 
@@ -319,161 +425,143 @@ StrixwWriter::~StrixwWriter() {
     if (fd_ >= 0) ::close(fd_);
 }
 
+// Header and index with the hashes known so far (zero for components not yet written).
 void StrixwWriter::put_header_and_index() {
-    Out o;
-    encode_index(o, meta_, tensors_);
-    STRIX_CHECK(o.b.size() == index_bytes_, "StrixwWriter('", path_, "'): the index changed size");
-    uint8_t h[kStrixwHeaderBytes] = {};
-    auto at = [&](size_t off, auto v) { std::memcpy(h + off, &v, sizeof v); };
-    std::memcpy(h, kMagic, 8);
-    at(8, kStrixwVersion);
-    at(12, (uint32_t)kStrixwHeaderBytes);
-    at(16, (uint64_t)kStrixwHeaderBytes);
-    at(24, index_bytes_);
-    at(32, data_offset_);
-    at(40, file_bytes_);
-    at(48, strix_hash64(o.b.data(), o.b.size()));
-    at(120, strix_hash64(h, 120));
-    write_at(fd_, h, sizeof h, 0, "StrixwWriter('" + path_ + "') header");
-    write_at(fd_, o.b.data(), o.b.size(), kStrixwHeaderBytes, "StrixwWriter('" + path_ + "') index");
+    const std::vector<uint8_t> index = encode_index(meta_, tensors_);
+    STRIX_CHECK(index.size() == index_bytes_, "strixw writer '", path_, "': the index encodes to ", index.size(),
+                " bytes, the layout was planned for ", index_bytes_);
+    const HeaderImage h = make_header(index_bytes_, data_offset_, file_bytes_, strix_hash64(index.data(), index.size()));
+    put_all(fd_, path_, 0, &h, sizeof h);
+    put_all(fd_, path_, kStrixwHeaderBytes, index.data(), index.size());
 }
 
 void StrixwWriter::write(size_t ti, StrixwRole role, const void *data, size_t bytes) {
-    STRIX_CHECK(!finished_ && ti < tensors_.size() && data != nullptr, "StrixwWriter('", path_, "'): tensor ", ti,
-                " of ", tensors_.size(), finished_ ? " after finish" : "", data ? "" : " with null data");
+    STRIX_CHECK(fd_ >= 0 && !finished_, "strixw writer '", path_, "': the file is already finished");
+    STRIX_CHECK(ti < tensors_.size(), "strixw writer '", path_, "': no tensor #", ti, " in a plan of ",
+                tensors_.size());
     StrixwTensor &t = tensors_[ti];
-    for (size_t ci = 0; ci < t.components.size(); ++ci) {
-        StrixwComponent &c = t.components[ci];
-        if (c.role != role) continue;
-        STRIX_CHECK(bytes == c.bytes && !done_[ti][ci], "StrixwWriter: '", t.name, "' ", strixw_role_name(role), ": ",
-                    bytes, " bytes for a component of ", c.bytes, done_[ti][ci] ? ", written twice" : "");
-        write_at(fd_, data, bytes, c.offset, "StrixwWriter('" + path_ + "') tensor '" + t.name + "'");
-        c.hash = strix_hash64(data, bytes);
-        done_[ti][ci] = true;
-        return;
-    }
-    STRIX_CHECK(false, "StrixwWriter: '", t.name, "' (", strixw_encoding_name(t.encoding), ") has no ",
-                strixw_role_name(role), " component");
+    const auto it = std::find_if(t.components.begin(), t.components.end(),
+                                 [&](const StrixwComponent &c) { return c.role == role; });
+    STRIX_CHECK(it != t.components.end(), "strixw writer: '", t.name, "' is ", strixw_encoding_name(t.encoding),
+                " and has no '", strixw_role_name(role), "' component");
+    const size_t ci = (size_t)(it - t.components.begin());
+    STRIX_CHECK(data != nullptr, "strixw writer: '", t.name, "' ", strixw_role_name(role), ": null source");
+    STRIX_CHECK(bytes == it->bytes, "strixw writer: '", t.name, "' ", strixw_role_name(role), " of ", bytes,
+                " bytes given; ", strixw_encoding_name(t.encoding), " ", shape_text(t.shape), " needs ", it->bytes,
+                " bytes");
+    STRIX_CHECK(!done_[ti][ci], "strixw writer: '", t.name, "' ", strixw_role_name(role), " was already stored");
+    put_all(fd_, path_, it->offset, data, bytes);
+    it->hash = strix_hash64(data, bytes);
+    done_[ti][ci] = true;
 }
 
 void StrixwWriter::finish() {
-    STRIX_CHECK(!finished_, "StrixwWriter('", path_, "'): finish called twice");
-    for (size_t ti = 0; ti < tensors_.size(); ++ti)
-        for (size_t ci = 0; ci < done_[ti].size(); ++ci)
-            STRIX_CHECK(done_[ti][ci], "StrixwWriter('", path_, "'): '", tensors_[ti].name, "' ",
-                        strixw_role_name(tensors_[ti].components[ci].role), " was never written");
+    STRIX_CHECK(!finished_, "strixw writer '", path_, "': finish() on a finished file");
+    for (size_t ti = 0; ti < tensors_.size(); ++ti) {
+        const auto &flags = done_[ti];
+        const auto gap = std::find(flags.begin(), flags.end(), false);
+        STRIX_CHECK(gap == flags.end(), "strixw writer '", path_, "': '", tensors_[ti].name, "' ",
+                    strixw_role_name(tensors_[ti].components[(size_t)(gap - flags.begin())].role),
+                    " has no data yet: finish() needs every component stored");
+    }
     put_header_and_index();
-    STRIX_CHECK(::fdatasync(fd_) == 0, "StrixwWriter('", path_, "'): fdatasync failed: ", std::strerror(errno));
-    STRIX_CHECK(::close(fd_) == 0, "StrixwWriter('", path_, "'): close failed: ", std::strerror(errno));
+    const int fd = fd_;
     fd_ = -1;
     finished_ = true;
+    const bool synced = ::fdatasync(fd) == 0;
+    const int sync_errno = errno;
+    const bool closed = ::close(fd) == 0;
+    STRIX_CHECK(synced, "strixw writer: syncing '", path_, "': ", std::strerror(sync_errno));
+    STRIX_CHECK(closed, "strixw writer: closing '", path_, "': ", std::strerror(errno));
 }
 
-// ---- reader ---------------------------------------------------------------------------------------------------
+// ---- reader ---------------------------------------------------------------------------------------------------------
 StrixwFile::StrixwFile(const std::string &path) : path_(path) {
-    const std::string where = "strixw '" + path + "'";
-    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
-    STRIX_CHECK(fd >= 0, where, ": open failed: ", std::strerror(errno));
-    struct stat st {};
-    if (::fstat(fd, &st) != 0) {
-        const int e = errno;
+    const std::string who = "strixw '" + path + "'";
+    // map the whole file
+    {
+        const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+        STRIX_CHECK(fd >= 0, who, ": cannot open: ", std::strerror(errno));
+        struct stat st{};
+        const bool stat_ok = ::fstat(fd, &st) == 0;
+        const int stat_errno = errno;
+        void *m = MAP_FAILED;
+        if (stat_ok && st.st_size >= (off_t)kStrixwHeaderBytes)
+            m = ::mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+        const int map_errno = errno;
         ::close(fd);
-        STRIX_CHECK(false, where, ": fstat failed: ", std::strerror(e));
+        STRIX_CHECK(stat_ok, who, ": cannot stat: ", std::strerror(stat_errno));
+        STRIX_CHECK(st.st_size >= (off_t)kStrixwHeaderBytes, who, ": only ", st.st_size,
+                    " bytes, less than a header");
+        STRIX_CHECK(m != MAP_FAILED, who, ": cannot map ", st.st_size, " bytes: ", std::strerror(map_errno));
+        map_ = static_cast<const uint8_t *>(m);
+        file_bytes_ = (uint64_t)st.st_size;
     }
-    const uint64_t size = (uint64_t)st.st_size;
-    if (size < kStrixwHeaderBytes) {
-        ::close(fd);
-        STRIX_CHECK(false, where, ": ", size, " bytes, smaller than the ", kStrixwHeaderBytes, "-byte header");
-    }
-    void *m = ::mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
-    const int e = errno;
-    ::close(fd);
-    STRIX_CHECK(m != MAP_FAILED, where, ": mmap of ", size, " bytes failed: ", std::strerror(e));
-    map_ = static_cast<const uint8_t *>(m);
-    file_bytes_ = size;
     try {
-        const uint8_t *b = map_;
-        auto u32 = [&](size_t off) { uint32_t v; std::memcpy(&v, b + off, 4); return v; };
-        auto u64 = [&](size_t off) { return load64(b + off); };
-        STRIX_CHECK(std::memcmp(b, kMagic, 8) == 0, where, ": not a strixw file (magic)");
-        version_ = u32(8);
-        STRIX_CHECK(version_ >= kStrixwOldestVersion && version_ <= kStrixwVersion, where, ": format version ",
-                    version_, "; this library reads ", kStrixwOldestVersion, "..", kStrixwVersion);
-        STRIX_CHECK(u32(12) == kStrixwHeaderBytes, where, ": header size ", u32(12), " (expected ", kStrixwHeaderBytes,
-                    ")");
-        STRIX_CHECK(u64(120) == strix_hash64(b, 120), where, ": header hash mismatch (the header is corrupt)");
-        const uint64_t ioff = u64(16), ibytes = u64(24);
-        data_offset_ = u64(32);
-        STRIX_CHECK(u64(40) == size, where, ": the header says ", u64(40), " bytes, the file has ", size,
-                    " (truncated or appended to)");
-        STRIX_CHECK(ioff == kStrixwHeaderBytes && ibytes <= size - ioff, where, ": index at ", ioff, " of ", ibytes,
-                    " bytes does not fit the ", size, "-byte file");
-        STRIX_CHECK(data_offset_ % kStrixwTensorAlign == 0 && data_offset_ >= ioff + ibytes && data_offset_ <= size,
-                    where, ": data offset ", data_offset_, " (the index ends at ", ioff + ibytes, "; alignment ",
-                    kStrixwTensorAlign, ")");
-        STRIX_CHECK(u64(48) == strix_hash64(b + ioff, ibytes), where, ": index hash mismatch (the index is corrupt)");
+        const Bytes file{map_, file_bytes_, &path_};
+        HeaderImage h;
+        std::memcpy(&h, file.slice(0, kStrixwHeaderBytes, "the header").base, sizeof h);
+        STRIX_CHECK(std::memcmp(h.magic, kMagic, 8) == 0, who, ": the first 8 bytes are not the strixw magic");
+        STRIX_CHECK(h.header_hash == strix_hash64(map_, offsetof(HeaderImage, header_hash)), who,
+                    ": the header's own hash does not match its bytes (damaged header)");
+        STRIX_CHECK(h.version >= kStrixwOldestVersion && h.version <= kStrixwVersion, who, ": written as version ",
+                    h.version, "; versions ", kStrixwOldestVersion, " to ", kStrixwVersion,
+                    " can be read (convert the checkpoint again)");
+        STRIX_CHECK(h.header_bytes == kStrixwHeaderBytes, who, ": a ", h.header_bytes, "-byte header; this format's "
+                    "header is ", kStrixwHeaderBytes, " bytes");
+        STRIX_CHECK(h.file_bytes == file_bytes_, who, ": the header records ", h.file_bytes, " bytes but ",
+                    file_bytes_, " are on disk (the file was cut short or extended)");
+        STRIX_CHECK(h.index_offset == kStrixwHeaderBytes, who, ": the index is recorded at ", h.index_offset,
+                    "; it follows the header at ", kStrixwHeaderBytes);
+        const Bytes index = file.slice(h.index_offset, h.index_bytes, "the index");
+        STRIX_CHECK(h.data_offset % kStrixwTensorAlign == 0 && h.data_offset >= h.index_offset + h.index_bytes &&
+                        h.data_offset <= file_bytes_,
+                    who, ": the data region is recorded at ", h.data_offset, "; it must be ", kStrixwTensorAlign,
+                    "-aligned, after the index (which ends at ", h.index_offset + h.index_bytes, ") and in the file");
+        STRIX_CHECK(h.index_hash == strix_hash64(index.base, index.size), who,
+                    ": the index does not match the hash in the header (damaged index)");
+        version_ = h.version;
+        data_offset_ = h.data_offset;
 
-        In in{b + ioff, ibytes, 0, where};
-        const uint32_t nmeta = in.num<uint32_t>("the metadata count");
-        for (uint32_t i = 0; i < nmeta; ++i) {
-            std::string k = in.bytes(in.num<uint16_t>("a metadata key length"), "a metadata key");
-            std::string v = in.bytes(in.num<uint32_t>("a metadata value length"), "a metadata value");
-            STRIX_CHECK(meta_.emplace(k, std::move(v)).second, where, ": metadata key '", k, "' twice");
+        Codec<false> c;
+        c.in = index;
+        std::vector<std::pair<std::string, std::string>> kv;
+        c.metadata(kv);
+        for (auto &[k, v] : kv)
+            STRIX_CHECK(meta_.emplace(k, std::move(v)).second, who, ": metadata key '", k, "' appears twice");
+        c.list<uint32_t>(tensors_, "tensors", [&](StrixwTensor &t) { c.record(t); });
+        STRIX_CHECK(c.in.size == 0, who, ": ", c.in.size, " bytes of the index follow its last record");
+        STRIX_CHECK(!tensors_.empty(), who, ": the index lists no tensors");
+
+        // audit every record
+        struct Span { uint64_t lo, hi; };
+        std::vector<Span> spans;
+        for (size_t i = 0; i < tensors_.size(); ++i) {
+            const StrixwTensor &t = tensors_[i];
+            require_well_formed(t, who);
+            const std::vector<StrixwComponent> expect = strixw_components(t);
+            STRIX_CHECK(t.components.size() == expect.size(), who, ": '", t.name, "' lists ", t.components.size(),
+                        " components; ", strixw_encoding_name(t.encoding), " has ", expect.size());
+            for (size_t k = 0; k < expect.size(); ++k) {
+                const StrixwComponent &got = t.components[k];
+                STRIX_CHECK(got.role == expect[k].role && got.bytes == expect[k].bytes, who, ": '", t.name,
+                            "' component #", k, " is ", strixw_role_name(got.role), "/", got.bytes, " bytes where ",
+                            strixw_encoding_name(t.encoding), " ", shape_text(t.shape), " gives ",
+                            strixw_role_name(expect[k].role), "/", expect[k].bytes, " bytes");
+                const bool inside = got.offset >= data_offset_ && got.offset <= file_bytes_ &&
+                                    got.bytes <= file_bytes_ - got.offset;
+                STRIX_CHECK(inside && got.offset % kStrixwComponentAlign == 0, who, ": '", t.name, "' ",
+                            strixw_role_name(got.role), " at [", got.offset, ", +", got.bytes,
+                            ") is not a ", kStrixwComponentAlign, "-aligned range of the data region [", data_offset_,
+                            ", ", file_bytes_, ")");
+                spans.push_back({got.offset, got.offset + got.bytes});
+            }
+            STRIX_CHECK(by_name_.emplace(t.name, i).second, who, ": two records are named '", t.name, "'");
         }
-        const uint32_t nt = in.num<uint32_t>("the tensor count");
-        STRIX_CHECK(nt >= 1, where, ": no tensors");
-        std::vector<std::pair<uint64_t, uint64_t>> spans;
-        for (uint32_t i = 0; i < nt; ++i) {
-            StrixwTensor t;
-            t.name = in.bytes(in.num<uint16_t>("a tensor name length"), "a tensor name");
-            t.encoding = (StrixwEncoding)in.num<uint8_t>("an encoding");
-            const uint8_t nd = in.num<uint8_t>("a rank");
-            for (uint8_t d = 0; d < nd; ++d) t.shape.push_back(in.num<int64_t>("a shape"));
-            t.group_size = in.num<int64_t>("a group size");
-            t.experts = in.num<int64_t>("an expert count");
-            const uint16_t np = in.num<uint16_t>("a part count");
-            for (uint16_t p = 0; p < np; ++p) {
-                StrixwPart part;
-                part.source = in.bytes(in.num<uint16_t>("a part name length"), "a part name");
-                part.row_offset = in.num<int64_t>("a part row offset");
-                part.rows = in.num<int64_t>("a part row count");
-                t.parts.push_back(std::move(part));
-            }
-            const uint8_t nc = in.num<uint8_t>("a component count");
-            for (uint8_t c = 0; c < nc; ++c) {
-                StrixwComponent comp;
-                comp.role = (StrixwRole)in.num<uint8_t>("a component role");
-                comp.offset = in.num<uint64_t>("a component offset");
-                comp.bytes = in.num<uint64_t>("a component size");
-                comp.hash = in.num<uint64_t>("a component hash");
-                t.components.push_back(comp);
-            }
-            check_record(t, where);
-            const std::vector<StrixwComponent> want = strixw_components(t);
-            STRIX_CHECK(want.size() == t.components.size(), where, ": tensor '", t.name, "' (",
-                        strixw_encoding_name(t.encoding), ") has ", t.components.size(), " components, expected ",
-                        want.size());
-            for (size_t c = 0; c < want.size(); ++c) {
-                const StrixwComponent &g = t.components[c];
-                STRIX_CHECK(g.role == want[c].role && g.bytes == want[c].bytes, where, ": tensor '", t.name,
-                            "' component ", c, " is ", strixw_role_name(g.role), " of ", g.bytes, " bytes, expected ",
-                            strixw_role_name(want[c].role), " of ", want[c].bytes, " for ",
-                            strixw_encoding_name(t.encoding), " ", dims(t.shape));
-                // offset <= size before size - offset, which would wrap past the end
-                STRIX_CHECK(g.offset >= data_offset_ && g.offset <= size && g.bytes <= size - g.offset &&
-                                g.offset % kStrixwComponentAlign == 0,
-                            where, ": tensor '", t.name, "' ", strixw_role_name(g.role), " at ", g.offset, " (",
-                            g.bytes, " bytes) lies outside the data region [", data_offset_, ", ", size,
-                            ") or is not ", kStrixwComponentAlign, "-aligned");
-                spans.emplace_back(g.offset, g.offset + g.bytes);
-            }
-            STRIX_CHECK(by_name_.emplace(t.name, tensors_.size()).second, where, ": tensor '", t.name, "' twice");
-            tensors_.push_back(std::move(t));
-        }
-        STRIX_CHECK(in.at == in.n, where, ": ", in.n - in.at, " bytes left after the last index record");
-        std::sort(spans.begin(), spans.end());
+        std::sort(spans.begin(), spans.end(), [](const Span &a, const Span &b) { return a.lo < b.lo; });
         for (size_t i = 1; i < spans.size(); ++i)
-            STRIX_CHECK(spans[i].first >= spans[i - 1].second, where, ": components overlap at byte ", spans[i].first);
+            STRIX_CHECK(spans[i - 1].hi <= spans[i].lo, who, ": two components share the bytes from ", spans[i].lo,
+                        " to ", std::min(spans[i - 1].hi, spans[i].hi));
     } catch (...) {
         ::munmap(const_cast<uint8_t *>(map_), file_bytes_);
         map_ = nullptr;
@@ -487,7 +575,7 @@ StrixwFile::~StrixwFile() {
 
 const std::string &StrixwFile::meta(const std::string &key) const {
     const auto it = meta_.find(key);
-    STRIX_CHECK(it != meta_.end(), "strixw '", path_, "': no metadata key '", key, "'");
+    STRIX_CHECK(it != meta_.end(), "strixw '", path_, "': the metadata has no key '", key, "'");
     return it->second;
 }
 
@@ -498,43 +586,42 @@ const StrixwTensor *StrixwFile::find(const std::string &name) const {
 
 const StrixwTensor &StrixwFile::get(const std::string &name) const {
     const StrixwTensor *t = find(name);
-    STRIX_CHECK(t != nullptr, "strixw '", path_, "': no tensor '", name, "' (", tensors_.size(), " tensors)");
+    STRIX_CHECK(t, "strixw '", path_, "': none of its ", tensors_.size(), " tensors is named '", name, "'");
     return *t;
 }
 
 const void *StrixwFile::data(const StrixwTensor &t, StrixwRole role) const {
-    STRIX_CHECK(find(t.name) == &t, "strixw '", path_, "': tensor '", t.name, "' is not from this file");
+    STRIX_CHECK(&t >= tensors_.data() && &t < tensors_.data() + tensors_.size(), "strixw '", path_, "': the record '",
+                t.name, "' belongs to another file");
     for (const StrixwComponent &c : t.components)
         if (c.role == role) return map_ + c.offset;
-    STRIX_CHECK(false, "strixw '", path_, "': tensor '", t.name, "' (", strixw_encoding_name(t.encoding), ") has no ",
-                strixw_role_name(role), " component");
+    STRIX_CHECK(false, "strixw '", path_, "': '", t.name, "' (", strixw_encoding_name(t.encoding), ") has no '",
+                strixw_role_name(role), "' component");
     return nullptr;
 }
 
+// Worker w hashes components w, w + threads, ...; the first damaged component in index order is reported.
 void StrixwFile::verify_hashes(int threads) const {
-    STRIX_CHECK(threads >= 1 && threads <= 1024, "verify_hashes: threads = ", threads);
-    std::vector<std::pair<const StrixwTensor *, const StrixwComponent *>> work;
+    STRIX_CHECK(threads >= 1 && threads <= 1024, "strixw '", path_, "': verify_hashes with ", threads,
+                " threads (1 to 1024)");
+    std::vector<const StrixwComponent *> all;
+    std::vector<const StrixwTensor *> owner;
     for (const StrixwTensor &t : tensors_)
-        for (const StrixwComponent &c : t.components) work.emplace_back(&t, &c);
-    std::atomic<size_t> next{0};
-    std::mutex mu;
-    size_t first_bad = work.size();  // the lowest failing index: the report does not depend on thread timing
-    auto run = [&] {
-        for (size_t i; (i = next.fetch_add(1)) < work.size();)
-            if (strix_hash64(map_ + work[i].second->offset, work[i].second->bytes) != work[i].second->hash) {
-                std::lock_guard<std::mutex> g(mu);
-                first_bad = std::min(first_bad, i);
-            }
-    };
+        for (const StrixwComponent &c : t.components) all.push_back(&c), owner.push_back(&t);
+    std::vector<char> bad(all.size(), 0);
+    const size_t nw = std::min<size_t>((size_t)threads, std::max<size_t>(all.size(), 1));
     std::vector<std::thread> pool;
-    for (int i = 1; i < threads; ++i) pool.emplace_back(run);
-    run();
-    for (std::thread &t : pool) t.join();
-    if (first_bad < work.size()) {
-        const auto [t, c] = work[first_bad];
-        STRIX_CHECK(false, "strixw '", path_, "': hash mismatch in tensor '", t->name, "' ", strixw_role_name(c->role),
-                    " (", c->bytes, " bytes at ", c->offset, "): the file is corrupt");
-    }
+    for (size_t w = 0; w < nw; ++w)
+        pool.emplace_back([&, w] {
+            for (size_t i = w; i < all.size(); i += nw)
+                bad[i] = strix_hash64(map_ + all[i]->offset, all[i]->bytes) != all[i]->hash;
+        });
+    for (std::thread &th : pool) th.join();
+    const auto first = std::find(bad.begin(), bad.end(), 1);
+    if (first == bad.end()) return;
+    const size_t i = (size_t)(first - bad.begin());
+    STRIX_CHECK(false, "strixw '", path_, "': '", owner[i]->name, "' ", strixw_role_name(all[i]->role), " (",
+                all[i]->bytes, " bytes at ", all[i]->offset, ") fails its stored hash: the data is damaged");
 }
 
 }  // namespace strix
