@@ -815,12 +815,13 @@ __global__ void __launch_bounds__(1024)
     const int64_t item = (int64_t)blockIdx.x * ipb + threadIdx.x / kWave;
     if ((int)threadIdx.x / kWave < ipb && item < ld * mg)  // items in row-major order: the waves of a block share weight rows through L1
         rsmall::router_small_wave<float, 4, 1, NCH, true>(x, wr, logits, M, ld, H, item / mg, item % mg * 4, bias, E);
-    // the block's logits before its ticket: the logits are stored device-coherent (write-through the XCD's L2), every
-    // wave waits for its stores' acknowledgements (vmcnt 0), then the barrier; no L2 write-back (a device-scope
-    // release fence a block measured +8 us at 129 blocks, +55 us at 1026: the write-backs serialise)
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    // the block's logits before its ticket, by the memory model: the barrier orders every wave's stores before thread
+    // 0, whose agent-scope release fence then makes them visible device-wide before its arrival is counted (the
+    // logits are also stored write-through the XCD's L2, so the fence finds few dirty lines to write back); the last
+    // block's agent-scope acquire below pairs with it
     __syncthreads();
     if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         const bool is_last = (int)arrive(ticket, epoch) == nrb;
         if (is_last) *reinterpret_cast<volatile unsigned long long *>(ticket) = 0;  // every block has arrived
         last = is_last;
@@ -1601,8 +1602,9 @@ void linear_q5_experts_combine_grouped(const void *h, const Q5DeviceView &w, int
                 moe_route_workspace_bytes(M, A, E));
     STRIX_CHECK(N % 8 == 0 && reinterpret_cast<uintptr_t>(partial) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0,
                 fn, ": N = ", N, " must be a multiple of 8, partial and y 16-byte aligned");
-    STRIX_CHECK(disjoint(partial, M * A * N * 4, y, M * N * es) && disjoint(y, M * N * es, h, M * A * v.K * es), fn,
-                ": partial, y and h must not overlap");
+    STRIX_CHECK(disjoint(partial, M * A * N * 4, y, M * N * es) && disjoint(partial, M * A * N * 4, h, M * A * v.K * es) &&
+                    disjoint(y, M * N * es, h, M * A * v.K * es),
+                fn, ": partial, y and h must not overlap");
     if (shared != nullptr)
         STRIX_CHECK(shared->s != nullptr && shared->gate_logit != nullptr && shared->err != nullptr &&
                         shared->gate_ld >= 1 && reinterpret_cast<uintptr_t>(shared->s) % 16 == 0,
@@ -1790,15 +1792,28 @@ size_t moe_layer_workspace_bytes(const MoeLayerWeights &w, int64_t M) {
 // leave most of the chip idle at prefill sizes: forked from the caller's stream with an event and joined back before
 // the combine. The context is created explicitly (before any graph capture: a stream created during capture would
 // break it) and used by one host thread at a time, like a stream.
+// STRIX_FUSED_ROUTE=1 in the environment turns the decode-size fused routing launch on; read once a process (the
+// default of calls without a context) and once a layer context, never per forward
+bool read_fused_route_env() {
+    const char *fr = getenv("STRIX_FUSED_ROUTE");
+    return fr != nullptr && atoi(fr) != 0;
+}
+bool fused_route_default() {
+    static const bool on = read_fused_route_env();
+    return on;
+}
+
 struct MoeLayerContext {
     int device = 0;
     hipStream_t s = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
+    bool fused_route = false;  // STRIX_FUSED_ROUTE at creation
 };
 
 MoeLayerContext *moe_layer_context_create() {
     const char *fn = "moe_layer_context_create";
     auto *c = new MoeLayerContext;
+    c->fused_route = read_fused_route_env();
     try {
         STRIX_HIP_CHECK(hipGetDevice(&c->device), fn, ": hipGetDevice");
         STRIX_HIP_CHECK(hipStreamCreateWithFlags(&c->s, hipStreamNonBlocking), fn, ": helper stream");
@@ -1970,8 +1985,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         // Off by default: measured on MI355X at 16 tokens, H 3072, 513 router rows, it takes 24.9 us against 6.0 +
         // 11.9 us for the two launches (the top-k cannot start before the last router block, and the router's waves
         // in 1024-thread blocks take ~8 us of work against ~4 in its own launch)
-        const char *fr = getenv("STRIX_FUSED_ROUTE");
-        const bool fused_route = fr != nullptr && atoi(fr) != 0;
+        const bool fused_route = ctx != nullptr ? ctx->fused_route : fused_route_default();
         if (!routed && fused_route && fold && M * A <= 1024 && kernels::route_fused_fits(x, w.router, H)) {
             launch_route_fused(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(w.router),
                                w.router_bias, logits, ld, M, E, H, k, ids, coef, route, L.route_bytes, err_router,

@@ -131,7 +131,7 @@ def reference_declarations():
     return decls
 
 
-@pytest.mark.skipif(not os.path.isdir(REF), reason="the reference tree is only in the build container")
+@pytest.mark.skipif(not os.path.isdir(REF), reason="needs the reference's kernel headers under /root/reference, which exist only in the build container (the GPU box has no copy); the CPU suite runs it there")
 def test_exports_match_reference_declarations():
     """Every launcher the reference's kernel headers declare (kernels/moe_router, moe_grouped, linear_q4, swiglu,
     linear_q8, linear, hc .hpp) is exported with the same demangled C++ signature, so strixite's call sites link against
@@ -171,3 +171,22 @@ def test_strixw_exports_reference_names():
                  "strix::StrixwDevice::q4", "strix::StrixwDevice::q8", "strix::StrixwDevice::f32",
                  "strix::StrixwDevice::bf16"]:
         assert any(e.startswith(name + "(") for e in exported), name
+
+
+def test_q5_combine_refuses_partial_overlapping_h():
+    """The Q5 grouped combine refuses FP32 partials whose bytes overlap h anywhere, also in the upper half that a
+    BF16-sized check would miss (the down projection would overwrite h while still reading it)."""
+    from strixite_amd import _lib
+
+    L = _lib.lib()
+    buf = (C.c_uint8 * 16384)()
+    p = (C.addressof(buf) + 255) // 256 * 256
+    E, M, A, N, K = 2, 1, 2, 64, 128
+    v = _lib.QView(p, p, p, E * N, K, 32)
+    ws = p + 4096
+    partial = p + 8192                    # M A N floats = 512 bytes
+    h = partial + 384                     # inside partial's upper half
+    y = p + 12288
+    rc = L.strix_linear_q5_experts_combine_grouped(h, C.byref(v), E, p + 2048, p + 2560, ws, 4096, partial, M, A, y,
+                                                   1, 0, None, None, 0)
+    assert rc == 1 and b"must not overlap" in L.strix_moe_last_error(), L.strix_moe_last_error()

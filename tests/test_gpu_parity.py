@@ -525,6 +525,7 @@ def test_layer_fused_router_launch(M, H, biased, monkeypatch):
     want = layer.forward(x, logits_in=lg)
     torch.cuda.synchronize()
     monkeypatch.setenv("STRIX_FUSED_ROUTE", "1")
+    ctx = moe.LayerContext()  # reads STRIX_FUSED_ROUTE once, at its creation
 
     def check(out, what):
         assert np.array_equal(to_np(out["ids"]), to_np(rids)), what
@@ -534,7 +535,7 @@ def test_layer_fused_router_launch(M, H, biased, monkeypatch):
 
     ws = torch.from_numpy(rng.integers(0, 256, layer.workspace_bytes(M), dtype=np.uint8)).to(DEV)
     for call in range(2):
-        out = layer.forward(x, ws=ws)
+        out = layer.forward(x, ws=ws, ctx=ctx)
         torch.cuda.synchronize()
         check(out, ("call", call))
     # graph replays: the same launch arguments (epoch included) every replay
@@ -542,19 +543,19 @@ def test_layer_fused_router_launch(M, H, biased, monkeypatch):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        layer.forward(x, ws=ws, out=out)  # warm-up outside the capture
+        layer.forward(x, ws=ws, out=out, ctx=ctx)  # warm-up outside the capture
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        layer.forward(x, ws=ws, out=out)
+        layer.forward(x, ws=ws, out=out, ctx=ctx)
     for rep in range(3):
         for t in out.values():
             t.zero_()
         g.replay()
         torch.cuda.synchronize()
         check(out, ("replay", rep))
-        layer.forward(x, ws=ws)  # eager work on the same workspace between replays
+        layer.forward(x, ws=ws, ctx=ctx)  # eager work on the same workspace between replays
         torch.cuda.synchronize()
 
 
@@ -645,13 +646,16 @@ def test_layer_config4_zipf_prefill():
 
 
 def test_layer_config5_stack_decode_then_prefill():
-    """a stack of consecutive layers with independent per-layer weights and Zipf router biases
-    drawn from the seed, run as a 16-token decode step and then a 4096-token prefill step back to back (both steps'
-    buffers and one shared workspace a step live). Each layer takes its own seeded input, as the bench does (the
-    sublayer has no normalization, so feeding x_out on unnormalized synthetic weights would grow without bound).
-    Every layer: ids bit-exact on every token, and the output on seeded tokens against the oracle."""
+    """BASELINE config 5 as the bench runs it: a stack of 8 consecutive layers with independent per-layer weights and
+    Zipf router biases drawn from the seed, a 16-token decode step and then a 4096-token prefill step back to back,
+    captured as ONE HIP graph (one workspace a step, the buffers of every layer live). The graph is replayed twice
+    with every output poisoned in between (a fill kernel, so the checked values come from the second replay). Each
+    layer takes its own seeded input, as the bench does (the sublayer has no normalization, so feeding x_out on
+    unnormalized synthetic weights would grow without bound). Every layer of both steps: ids bit-exact on every token,
+    y and x_out on sampled tokens against the oracle, no error words (the reference's per-layer order,
+    strixite runtime/qwen4exp.cpp:3143-3217)."""
     say("layer cfg5")
-    NL, H, E, k, I = 4, 3072, 512, 10, 512
+    NL, H, E, k, I = 8, 3072, 512, 10, 512
     layers = []
     for l in range(NL):
         bias = torch.from_numpy(zipf_bias(l, E, 1.0)).to(DEV)
@@ -660,13 +664,41 @@ def test_layer_config5_stack_decode_then_prefill():
     steps = {}
     for M in (16, 4096):
         ws = layers[0].workspace(M)
-        ins, outs = [], []
-        for l in range(NL):
-            ins.append(moe.synth_bf16_normal(5, "x", 100 * M + l, (M, H), 1.0))
-            outs.append(layers[l].forward(ins[-1], ws=ws, ctx=ctx))
-        steps[M] = (ins, outs)
+        ins = [moe.synth_bf16_normal(5, "x", 100 * M + l, (M, H), 1.0) for l in range(NL)]
+        outs = [layers[l].forward(ins[l], ws=ws, ctx=ctx) for l in range(NL)]  # eager: allocates the outputs
+        steps[M] = (ins, outs, ws)
     torch.cuda.synchronize()
-    for M, (ins, outs) in steps.items():
+
+    def stack():
+        for M in (16, 4096):
+            ins, outs, ws = steps[M]
+            for l in range(NL):
+                layers[l].forward(ins[l], ws=ws, out=outs[l], ctx=ctx)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        stack()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        stack()
+    torch.cuda.synchronize()
+    say("cfg5 captured")
+    for rep in range(2):
+        for M in (16, 4096):
+            for o in steps[M][1]:
+                o["ids"].fill_(-7)
+                o["coef"].fill_(float("nan"))
+                o["y"].fill_(float("nan"))
+                o["x_out"].fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        say("cfg5 replay", rep)
+    for M in (16, 4096):
+        ins, outs, _ = steps[M]
         for l in range(NL):
             say("cfg5 check", M, l)
             w = oracle_weights(layers[l])
@@ -680,6 +712,7 @@ def test_layer_config5_stack_decode_then_prefill():
             assert rel_err(to_np(outs[l]["y"])[rows], o["y"]) < 1e-2, (M, l)
             assert rel_err(to_np(outs[l]["x_out"])[rows], o["out"]) < 1e-2, (M, l)
             assert to_np(outs[l]["err"])[0] == 0 and to_np(outs[l]["err"])[3] == 0
+    del g
     # the routed experts made visible in y: the first layer again, balanced, at both sizes
     for M in (16, 4096):
         lb = balanced(layers[0])
