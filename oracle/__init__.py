@@ -15,7 +15,7 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB = os.path.join(_HERE, "liboracle_moe.so")
+_LIB = os.environ.get("ORACLE_LIB") or os.path.join(_HERE, "liboracle_moe.so")  # ORACLE_LIB: the sanitizer build
 _REF = os.path.join(_HERE, "_ref", "libref_formats.so")
 
 _i64, _u64, _u32, _f32, _i32 = C.c_int64, C.c_uint64, C.c_uint32, C.c_float, C.c_int32
