@@ -249,38 +249,46 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     float ex[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) ex[j] = 0.f;
-    // one candidate at a time; the next one's row loads are issued before this one's chain and butterfly
-    auto load = [&](int e, uint4 (&c)[NCH]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < NCH; ++i)
-            c[i] = *reinterpret_cast<const uint4 *>(w + (int64_t)e * K + (lane + i * kWave) * 8);
-    };
-    uint4 cur[NCH], nxt[NCH];
+    // the candidates in batches of kBatch: a batch's rows are loaded together (one L2 round trip for the batch, the
+    // loads unconditional: a slot past the list repeats the batch's first candidate and is not stored), then their
+    // chains and butterflies run interleaved (independent, so they overlap); each chain is the canonical order
+    constexpr int kBatch = 6;
     float sd = 0.f;  // the shared gate logit (wave-uniform)
-    int ec = __builtin_amdgcn_readfirstlane(cl[0]);
-    load(ec, cur);
-    for (int s2 = 0; s2 < nc; ++s2) {
-        const int en = s2 + 1 < nc ? __builtin_amdgcn_readfirstlane(cl[s2 + 1]) : ec;
-        if (s2 + 1 < nc) load(en, nxt);
-        float d = lane_chain<NCH>(xr, cur);
+    for (int b0 = 0; b0 < nc; b0 += kBatch) {
+        uint4 rows[kBatch][NCH];
+        int ecs[kBatch];
 #pragma unroll
-        for (int off = kWave / 2; off > 0; off >>= 1) d = d + __shfl_xor(d, off, kWave);
-        if (ec == E) {
-            sd = d;
-            if (lane == 0) row[E] = d;  // the shared gate logit, unbiased
-        } else {
-            const float vb = bias ? d + bias[ec] : d;  // one FP32 add, as the unfused path
-            if (lane == ec % kWave) {
-                const int js = ec / kWave;
+        for (int i = 0; i < kBatch; ++i) {
+            ecs[i] = __builtin_amdgcn_readfirstlane(cl[b0 + i < nc ? b0 + i : b0]);
 #pragma unroll
-                for (int j = 0; j < NV; ++j)
-                    if (j == js) ex[j] = vb;
-                row[ec] = vb;
+            for (int c = 0; c < NCH; ++c)
+                rows[i][c] = *reinterpret_cast<const uint4 *>(w + (int64_t)ecs[i] * K + (lane + c * kWave) * 8);
+        }
+        float d[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) d[i] = lane_chain<NCH>(xr, rows[i]);
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1)
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) d[i] = d[i] + __shfl_xor(d[i], off, kWave);
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            if (b0 + i >= nc) break;
+            const int ec = ecs[i];
+            if (ec == E) {
+                sd = d[i];
+                if (lane == 0) row[E] = d[i];  // the shared gate logit, unbiased
+            } else {
+                const float vb = bias ? d[i] + bias[ec] : d[i];  // one FP32 add, as the unfused path
+                if (lane == ec % kWave) {
+                    const int js = ec / kWave;
+#pragma unroll
+                    for (int j = 0; j < NV; ++j)
+                        if (j == js) ex[j] = vb;
+                    row[ec] = vb;
+                }
             }
         }
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) cur[i] = nxt[i];
-        ec = en;
     }
     int bad = INT_MAX;
     if (exact_all) {
