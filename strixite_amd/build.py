@@ -24,6 +24,10 @@ FLAGS = [
 ]
 
 
+# hipBLASLt: the prefill router's approximate pass (a plain bf16 GEMM)
+LIBS = ["-lhipblaslt"]
+
+
 def sources():
     return sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
@@ -46,7 +50,8 @@ def build(jobs: int | None = None) -> str:
     with cf.ThreadPoolExecutor(max_workers=jobs or min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    r = subprocess.run([HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", tmp, *objs], capture_output=True, text=True)
+    r = subprocess.run([HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", tmp, *objs, *LIBS], capture_output=True,
+                       text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
@@ -99,7 +104,7 @@ def build_asan(jobs: int | None = None, force: bool = False) -> str:
     tmp = LIB_ASAN + ".tmp"
     r = subprocess.run([HIPCC, "-shared", "-fsanitize=address,undefined", "-shared-libsan", "-fno-gpu-sanitize",
                         f"--offload-arch={ARCH}",
-                        "-o", tmp, *objs], capture_output=True, text=True)
+                        "-o", tmp, *objs, *LIBS], capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link (sanitizer build) failed:\n{r.stderr}")
     os.replace(tmp, LIB_ASAN)

@@ -31,6 +31,13 @@ void moe_topk_group_routes_small(const float *logits, int64_t ld, int64_t M, int
 bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
                         int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
                         hipStream_t stream, bool shared_slot = false, void *x16 = nullptr);
+// The same in its two passes, so a caller can start other work between them: the approximate projection (false,
+// nothing launched, for shapes it does not take) and the selection (after a successful approximate pass only).
+bool moe_router_prefill_approx(const void *x, const uint16_t *w, int64_t M, int64_t H, int64_t E, int64_t k,
+                               bool shared, float *logits, float *norms, hipStream_t stream);
+void moe_router_prefill_select(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
+                               int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef,
+                               uint32_t *err, hipStream_t stream, bool shared_slot = false, void *x16 = nullptr);
 }  // namespace kernels
 
 // ---- host-side checks -----------------------------------------------------------------------------------------

@@ -1927,6 +1927,11 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         j1.units = dv.N / 16 * j1.parts;
         j1.blocks = (int)((j1.units + kWaves - 1) / kWaves);
     }
+    // prefill sizes: the router's approximate pass first (the shared expert's GEMMs would otherwise share the CUs with
+    // this short, full-width GEMM; they overlap the latency-bound selection and packing that follow it instead)
+    const bool approx_done = !logits_in && M >= 256 &&
+                             moe_router_prefill_approx(x, w.router, M, H, E, k, w.has_shared || stacked, logits,
+                                                       reinterpret_cast<float *>(base + L.norms), stream);
     // with a context the shared expert runs on its helper stream; without one, on the caller's stream first
     hipStream_t sh_stream = stream;
     if (w.has_shared && !fold) {
@@ -1977,9 +1982,11 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         lg = logits;
         // prefill sizes: bf16 MFMA projection + exact recomputation of the candidates (the same routing bits)
         // (with the F16-math experts it also writes x in their F16 input form, which saves the conversion launch)
-        routed = M >= 256 && moe_router_prefill(x, w.router, w.router_bias, M, H, E, k, w.has_shared || stacked, logits,
-                                                reinterpret_cast<float *>(base + L.norms), ids, coef, err_router,
-                                                stream, stacked, f16p ? base + L.x16 : nullptr);
+        if (approx_done)
+            moe_router_prefill_select(x, w.router, w.router_bias, M, H, E, k, w.has_shared || stacked, logits,
+                                      reinterpret_cast<float *>(base + L.norms), ids, coef, err_router, stream, stacked,
+                                      f16p ? base + L.x16 : nullptr);
+        routed = approx_done;
         x16_done = routed && f16p;
         // decode sizes: router projection, top-k and packing in one launch, when asked for (STRIX_FUSED_ROUTE=1).
         // Off by default: measured on MI355X at 16 tokens, H 3072, 513 router rows, it takes 24.9 us against 6.0 +

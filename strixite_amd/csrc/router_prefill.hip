@@ -5,8 +5,9 @@
 // order (lane l of a wave64 takes the 8-element chunks l, l + 64, ... with fmaf, then a butterfly over the 64 lanes;
 // oracle: orc_router_logits). That order does not map onto MFMA, and at 4096 tokens x 513 rows x 3072 the VALU form
 // costs ~0.3 ms. So the projection runs in two passes:
-//   1. approx: logits a = x . w^T with bf16 MFMA (FP32 accumulation, any internal order), and the 2-norms |w_e|
-//      (|x_m| comes from pass 2, which loads the token's row). For ANY order of summing the K exact bf16 x bf16 products in FP32 - rounded to nearest or toward zero,
+//   1. approx: logits a = x . w^T as a plain bf16 GEMM on the matrix cores (hipBLASLt, FP32 accumulation, any
+//      internal order), and the 2-norms |w_e| (|x_m| comes from pass 2, which loads the token's row). For ANY order of
+//      summing the K exact bf16 x bf16 products in FP32 - rounded to nearest or toward zero,
 //      FP32 denormals kept or flushed - the result differs from the exact sum by at most (2K u) S + K 2^-125 with
 //      u = 2^-24 and S = sum_k |x_k w_k| <= |x| |w| (Cauchy-Schwarz). Both the canonical and the MFMA sums obey it, so
 //      |a - c| <= delta = (4K + 64) u |x| |w| + K 2^-124 (norms rounded up).
@@ -18,11 +19,17 @@
 //      then exactly those of the full exact row. Any non-finite a, b, or norm sends the token to the exact path for
 //      all of its experts (the non-finite handling of strixite kernels/moe_router.hip:40-67).
 // The logits workspace row of a token ends with exact values at the candidates and the shared gate (the entries the
-// layer reads later) and approximate values elsewhere.
+// layer reads later); the approximate values sit in the buffer's second quarter.
 #include "common.hpp"
 #include "topk.hpp"
 
+#include <hipblaslt/hipblaslt.h>
+
 #include <climits>
+#include <cstdlib>
+#include <mutex>
+#include <tuple>
+#include <vector>
 
 namespace strix::kernels {
 namespace {
@@ -30,19 +37,6 @@ namespace {
 using namespace strix::dev;
 constexpr int kWave = 64, kThreads = 256;
 
-
-// ---- pass 1: approximate logits + router row norms ------------------------------------------------------------------
-// Only the E routed rows (the shared gate row is computed exactly by pass 2). kNormRows extra rows of blocks (grid y)
-// only sum the squares of the router rows, so the GEMM blocks carry no norm work. Block tile 128 tokens x 128 rows, K in
-// steps of 64 through LDS (rows padded to 144 bytes: the 16 lanes of a fragment read hit 16 distinct 16-byte bank
-// groups); wave w computes tokens 64 (w / 2) .. + 63 x rows 64 (w % 2) .. + 63 as 4 x 4 v_mfma_f32_16x16x32_bf16
-// tiles whose A and B fragments are both 16-byte row segments (x rows for tokens, w rows for experts). The next K
-// step's tiles are loaded into registers while the current one is multiplied. K is split into kParts parts (grid z),
-// each summed by its own blocks into its own output (the pass is bound by latency and by L2 re-reads of the tiles,
-// which the large tiles keep to 4 reads of x and 32 of w at E 512, M 4096).
-// (parts: 1, 2, 4 measured 139, 122, 124 us for both passes at 4096 x 512 x 3072 on MI355X - more parts shorten this
-// pass but their partial logits push the router rows out of L2 before pass 2 re-reads them)
-constexpr int kBM = 128, kBN = 128, kBK = 64, kLd = kBK + 8, kParts = 2, kNormRows = kBN / 16;
 
 __device__ __forceinline__ float sumsq8(const uint4 &v) {
     const uint32_t d[4] = {v.x, v.y, v.z, v.w};
@@ -54,93 +48,6 @@ __device__ __forceinline__ float sumsq8(const uint4 &v) {
         s = fmaf(b, b, s);
     }
     return s;
-}
-
-__global__ void __launch_bounds__(kThreads)
-    router_approx_kernel(const uint16_t *x, const uint16_t *w, float *a_out, int64_t ld, int64_t M, int64_t N,
-                         int64_t K, float *nw) {
-    __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLd], Bs[kBN * kLd];
-    // K part blockIdx.z of gridDim.z: its sums go to part z of the outputs ([parts][M][ld], [parts][M], [parts][N])
-    const int64_t kp = K / gridDim.z, kbeg = kp * blockIdx.z, kend = kbeg + kp;
-    a_out += (int64_t)blockIdx.z * M * ld, nw += (int64_t)blockIdx.z * N;
-    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave, g = lane / 16, j = lane % 16;
-    const int wm = 64 * (wave / 2), wn = 64 * (wave % 2);
-    const int64_t n0 = (int64_t)blockIdx.x * kBN, m0 = (int64_t)blockIdx.y * kBM;
-    // staging: chunk u covers row (t >> 3) + 32 u, 16 bytes at column 8 (t & 7), of A and of B
-    const int sr = t >> 3, sc = (t & 7) * 8;
-    const int64_t gemm_rows = (int64_t)gridDim.y - kNormRows;
-    if ((int64_t)blockIdx.y >= gemm_rows) {
-        // the last kNormRows rows of blocks: the squared norms of the router rows over this K part, 16 rows a block
-        // (16 threads a row, each summing every 16th 16-byte piece; the tokens' norms come from the select pass,
-        // which loads each token's whole row anyway)
-        const int64_t c = n0 + 16 * (blockIdx.y - gemm_rows) + t / 16;
-        float q = 0.f;
-        if (c < N) {
-            const uint4 *wr = reinterpret_cast<const uint4 *>(w + c * K + kbeg);
-            const int n16 = (int)(kp / 8);
-#pragma unroll 12
-            for (int i = t % 16; i < n16; i += 16) q += sumsq8(wr[i]);
-        }
-        q += __shfl_xor(q, 1, kWave);
-        q += __shfl_xor(q, 2, kWave);
-        q += __shfl_xor(q, 4, kWave);
-        q += __shfl_xor(q, 8, kWave);
-        if (t % 16 == 0 && c < N) nw[c] = q;
-        return;
-    }
-    uint4 ra[4], rb[4];
-    auto load = [&](int64_t k0) __attribute__((always_inline)) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t r = m0 + sr + 32 * u, c = n0 + sr + 32 * u;
-            ra[u] = r < M ? *reinterpret_cast<const uint4 *>(x + r * K + k0 + sc) : make_uint4(0, 0, 0, 0);
-            rb[u] = c < N ? *reinterpret_cast<const uint4 *>(w + c * K + k0 + sc) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    float4v acc[4][4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = float4v{0, 0, 0, 0};
-    load(kbeg);
-    for (int64_t k0 = kbeg; k0 < kend; k0 += kBK) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            *reinterpret_cast<uint4 *>(&As[(sr + 32 * u) * kLd + sc]) = ra[u];
-            *reinterpret_cast<uint4 *>(&Bs[(sr + 32 * u) * kLd + sc]) = rb[u];
-        }
-        __syncthreads();
-        if (k0 + kBK < kend) load(k0 + kBK);
-#pragma unroll
-        for (int s = 0; s < kBK / 32; ++s) {
-            Frag af[4], bf[4];
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(&As[(wm + 16 * a + j) * kLd + 32 * s + 8 * g]);
-                af[a] = Frag{{v.x, v.y, v.z, v.w}};
-            }
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(&Bs[(wn + 16 * b + j) * kLd + 32 * s + 8 * g]);
-                bf[b] = Frag{{v.x, v.y, v.z, v.w}};
-            }
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-#pragma unroll
-                for (int b = 0; b < 4; ++b) acc[a][b] = mfma_bf16(af[a], bf[b], acc[a][b]);
-        }
-        __syncthreads();
-    }
-    // D: lane (j, g) holds tokens 4 g + r of column j
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t m = m0 + wm + 16 * a + 4 * g + r, n = n0 + wn + 16 * b + j;
-                if (m < M && n < N) a_out[m * ld + n] = acc[a][b][r];
-            }
 }
 
 // ---- pass 2: select -------------------------------------------------------------------------------------------------
@@ -162,13 +69,21 @@ __device__ __forceinline__ float lane_chain(const uint4 (&xr)[NCH], const uint4 
     return acc;
 }
 
-// One wave per token. parts: the approx pass's K parts [kParts][M][ld] (part 0 is the layer's logits buffer: the
-// exact values are written there); nw2: the parts' squared norms of the router rows.
+// The approximate logits as pass 1 left them: `parts` K parts (summed here), part p of token m at a[p part_stride +
+// m ld]; the squared router-row norms likewise in parts of N floats.
+struct ApproxIn {
+    const float *a;
+    int64_t ld, part_stride;
+    int parts;
+};
+
+// One wave per token. The exact values are written into the layer's logits row (ld); nw2: the squared norms of the
+// router rows in the approximate pass's parts.
 template <int NV, int NCH>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     router_select_kernel(const uint16_t *x, const uint16_t *w, const float *bias, float *logits, int64_t ld,
                          int64_t M, int E, int k, bool shared, bool shared_slot, const float *nw2,
-                         int32_t *ids, float *coef, uint32_t *err, uint4 *x16) {
+                         int32_t *ids, float *coef, uint32_t *err, uint4 *x16, ApproxIn ap) {
     __shared__ int cand_lds[kThreads / kWave][1040];  // a wave's candidate list (at most E + 1 <= 1025)
     __shared__ uint2 pick_lds[kThreads / kWave][topk::kCandScratch];  // the picks' scratch (topk::wave_picks)
     const int lane = threadIdx.x % kWave;
@@ -208,7 +123,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
         float a = 0.f, n2 = 0.f;
         if (e < E)
 #pragma unroll
-            for (int p = 0; p < kParts; ++p) a += row[p * M * ld + e], n2 += nw2[p * N + e];
+            for (int p = 0; p < ap.parts; ++p) a += ap.a[p * ap.part_stride + m * ap.ld + e], n2 += nw2[p * N + e];
         const float b = e < E && bias ? bias[e] : 0.f, n = sqrtf(n2) * up;
         va[j] = bias ? a + b : a;
         fin = fin && isfinite(va[j]) && isfinite(n);
@@ -323,26 +238,141 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     if (shared_slot && lane == 0) id_row[k] = E, coef_row[k] = 1.0f / (1.0f + expf(-sd));
 }
 
+// ---- pass 1 through hipBLASLt ---------------------------------------------------------------------------------------
+// The approximate logits are a plain bf16 GEMM (any FP32 summation order is within the bound above), so at prefill
+// sizes they come from the library GEMM: C [M, N] (ld N) = x [M, K] w [N, K]^T, FP32 accumulation. Column-major in
+// hipBLASLt's terms: C^T (N x M) = op_T(w as K x N) * (x as K x M). The handle lives per device and the chosen
+// algorithm per shape (no workspace); a shape the library declines returns false and pass 1 runs on the kernel above.
+struct BltShape {
+    int device;
+    int64_t M, N, K;
+    hipblasLtMatrixLayout_t la, lb, lc;
+    hipblasLtMatmulAlgo_t algo;
+};
+struct BltState {
+    std::mutex mu;
+    std::vector<std::pair<int, hipblasLtHandle_t>> handles;
+    std::vector<std::pair<int, hipblasLtMatmulDesc_t>> descs;
+    std::vector<BltShape> shapes;
+    std::vector<std::tuple<int, int64_t, int64_t, int64_t>> declined;
+};
+BltState &blt_state() {
+    static BltState *s = new BltState;  // lives until the process ends (the library's handles with it)
+    return *s;
+}
+
+bool approx_blaslt(const uint16_t *x, const uint16_t *w, float *c, int64_t M, int64_t N, int64_t K,
+                   hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    BltState &st = blt_state();
+    hipblasLtHandle_t h = nullptr;
+    hipblasLtMatmulDesc_t op = nullptr;
+    BltShape use{};
+    {
+        std::lock_guard<std::mutex> lock(st.mu);
+        for (const auto &d : st.declined)
+            if (d == std::make_tuple(dev, M, N, K)) return false;
+        for (auto &e : st.handles)
+            if (e.first == dev) h = e.second;
+        for (auto &e : st.descs)
+            if (e.first == dev) op = e.second;
+        if (h == nullptr) {
+            if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return false;
+            st.handles.emplace_back(dev, h);
+        }
+        if (op == nullptr) {
+            if (hipblasLtMatmulDescCreate(&op, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return false;
+            const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+            hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta);
+            hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
+            st.descs.emplace_back(dev, op);
+        }
+        bool found = false;
+        for (const BltShape &e : st.shapes)
+            if (e.device == dev && e.M == M && e.N == N && e.K == K) use = e, found = true;
+        if (!found) {
+            BltShape ns{dev, M, N, K, nullptr, nullptr, nullptr, {}};
+            bool ok = hipblasLtMatrixLayoutCreate(&ns.la, HIP_R_16BF, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
+                      hipblasLtMatrixLayoutCreate(&ns.lb, HIP_R_16BF, K, M, K) == HIPBLAS_STATUS_SUCCESS &&
+                      hipblasLtMatrixLayoutCreate(&ns.lc, HIP_R_32F, N, M, N) == HIPBLAS_STATUS_SUCCESS;
+            hipblasLtMatmulPreference_t pref = nullptr;
+            ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+            uint64_t wsb = 0;
+            ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
+                                                             sizeof wsb) == HIPBLAS_STATUS_SUCCESS;
+            hipblasLtMatmulHeuristicResult_t res{};
+            int n = 0;
+            ok = ok && hipblasLtMatmulAlgoGetHeuristic(h, op, ns.la, ns.lb, ns.lc, ns.lc, pref, 1, &res, &n) ==
+                           HIPBLAS_STATUS_SUCCESS && n >= 1;
+            if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+            if (!ok) {
+                st.declined.emplace_back(dev, M, N, K);
+                return false;
+            }
+            ns.algo = res.algo;
+            st.shapes.push_back(ns);
+            use = ns;
+        }
+    }
+    const float alpha = 1.0f, beta = 0.0f;
+    return hipblasLtMatmul(h, op, &alpha, w, use.la, x, use.lb, &beta, c, use.lc, c, use.lc, &use.algo, nullptr, 0,
+                           stream) == HIPBLAS_STATUS_SUCCESS;
+}
+
+// The router rows' squared norms (any FP32 order; rounded up by the bound's allowance): 16 rows a block, 16 threads
+// a row
+__global__ void __launch_bounds__(kThreads) router_norms_kernel(const uint16_t *w, int64_t N, int64_t K, float *nw) {
+    const int t = threadIdx.x;
+    const int64_t c = (int64_t)blockIdx.x * 16 + t / 16;
+    float q = 0.f;
+    if (c < N) {
+        const uint4 *wr = reinterpret_cast<const uint4 *>(w + c * K);
+#pragma unroll 12
+        for (int64_t i = t % 16; i < K / 8; i += 16) q += sumsq8(wr[i]);
+    }
+    q += __shfl_xor(q, 1, kWave);
+    q += __shfl_xor(q, 2, kWave);
+    q += __shfl_xor(q, 4, kWave);
+    q += __shfl_xor(q, 8, kWave);
+    if (t % 16 == 0 && c < N) nw[c] = q;
+}
+
 }  // namespace
 
-bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
-                        int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
-                        hipStream_t stream, bool shared_slot, void *x16) {
+namespace {
+bool prefill_shape_fits(const void *x, const uint16_t *w, int64_t H, int64_t E, int64_t k) {
+    const int64_t nch = H / 512;
+    return H % 512 == 0 && (nch == 2 || nch == 4 || nch == 6 || nch == 8) && E <= 1024 && k <= 32 && k <= E &&
+           reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+}
+}  // namespace
+
+bool moe_router_prefill_approx(const void *x, const uint16_t *w, int64_t M, int64_t H, int64_t E, int64_t k,
+                               bool shared, float *logits, float *norms, hipStream_t stream) {
+    if (!prefill_shape_fits(x, w, H, E, k)) return false;
+    const int64_t ld = E + (shared ? 1 : 0);
+    // pass 1: the library GEMM into the logits buffer's second part ([M][E], ld E; parts 1..3 of the [4][M][ld]
+    // buffer are scratch) and the row norms. A shape the library declines: false, and the caller routes through the
+    // canonical-order projection and top-k instead
+    if (!approx_blaslt(static_cast<const uint16_t *>(x), w, logits + M * ld, M, E, H, stream)) return false;
+    router_norms_kernel<<<(unsigned)((E + 15) / 16), kThreads, 0, stream>>>(w, E, H, norms + M);
+    STRIX_HIP_CHECK_LAUNCH("moe_router_prefill (row norms) E=", E, " H=", H);
+    return true;
+}
+
+void moe_router_prefill_select(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
+                               int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef,
+                               uint32_t *err, hipStream_t stream, bool shared_slot, void *x16) {
     const int64_t nch = H / 512, ld = E + (shared ? 1 : 0);
-    if (H % 512 != 0 || nch < 1 || nch > 8 || E > 1024 || k > 32 || k > E || (H / kParts) % kBK != 0 ||
-        reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(w) % 16 != 0)
-        return false;
-    float *nw = norms + (int64_t)kParts * M;  // (the first kParts * M floats: unused)
-    // kNormRows more rows of blocks for the router rows' norms
-    dim3 g1((unsigned)((E + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM + kNormRows), (unsigned)kParts);
-    STRIX_CHECK(g1.y <= 65535, "moe_router_prefill: M = ", M, " too large");
-    router_approx_kernel<<<g1, kThreads, 0, stream>>>(static_cast<const uint16_t *>(x), w, logits, ld, M, E, H, nw);
+    const ApproxIn ap{logits + M * ld, E, 0, 1};
+    const float *nw = norms + M;  // (the first M floats: unused)
     const unsigned g2 = (unsigned)((M + 3) / 4);
     const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
     auto go = [&](auto nvc, auto nchc) {
         router_select_kernel<decltype(nvc)::value, decltype(nchc)::value><<<g2, kThreads, 0, stream>>>(
             static_cast<const uint16_t *>(x), w, bias, logits, ld, M, (int)E, (int)k, shared, shared && shared_slot, nw,
-            ids, coef, err, static_cast<uint4 *>(x16));
+            ids, coef, err, static_cast<uint4 *>(x16), ap);
     };
     auto by_nch = [&](auto nvc) {
         switch (nch) {
@@ -352,7 +382,6 @@ bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int
             default: go(nvc, std::integral_constant<int, 2>{}); break;
         }
     };
-    if (nch != 2 && nch != 4 && nch != 6 && nch != 8) return false;
     switch (nv) {
         case 1: by_nch(std::integral_constant<int, 1>{}); break;
         case 2: by_nch(std::integral_constant<int, 2>{}); break;
@@ -361,6 +390,13 @@ bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int
         default: by_nch(std::integral_constant<int, 16>{}); break;
     }
     STRIX_HIP_CHECK_LAUNCH("moe_router_prefill M=", M, " E=", E, " k=", k, " H=", H);
+}
+
+bool moe_router_prefill(const void *x, const uint16_t *w, const float *bias, int64_t M, int64_t H, int64_t E,
+                        int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef, uint32_t *err,
+                        hipStream_t stream, bool shared_slot, void *x16) {
+    if (!moe_router_prefill_approx(x, w, M, H, E, k, shared, logits, norms, stream)) return false;
+    moe_router_prefill_select(x, w, bias, M, H, E, k, shared, logits, norms, ids, coef, err, stream, shared_slot, x16);
     return true;
 }
 
