@@ -53,7 +53,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--samples", type=int, default=7, help="timed samples; the median is reported")
     ap.add_argument("--layers", type=int, default=8, help="layers in the config-2 / 3 / 4 / 5 rotations")
-    ap.add_argument("--only", default="all", help="comma list of: decode, prefill, cfg1, cfg3, cfg5, kernels")
+    ap.add_argument("--only", default="all", help="comma list of: decode, prefill, cfg1, cfg3, cfg5, kernels (or "
+                    "hc with --hc: the mix timings alone)")
+    ap.add_argument("--hc", action="store_true", help="also time the hyper-connection mix beside the path (logged)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baselines")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--seed", type=int, default=0)
@@ -119,6 +121,35 @@ class Timer:
             self.torch.cuda.synchronize()
             res.append(self.e0.elapsed_time(self.e1) / n)
         return statistics.median(res)
+
+
+def hc_section(torch, moe):
+    """The hyper-connection mix beside the path (hc_mix_down / hc_mix_up) at the reference's shape: hidden d 2560, rank
+    r 320, 4 streams, Q4 and Q8 weights with group size 64, BF16 streams, token counts 1 .. 4096 (synthetic seeded
+    weights; W_up read as chunk-major). Logged only: run under rocprofv3 --kernel-trace for the kernels' durations
+    (these HIP-event figures include the wrappers' output allocations)."""
+    D, R, G = 2560, 320, 64
+    for bits in (4, 8):
+        wd = moe.QWeight.synth(bits, 3, "gu_q", "gu_s", 0, R + 4, 4 * D, G)
+        wu = moe.QWeight.synth(bits, 3, "dn_q", "dn_s", 0, 4 * D, R, G)
+        nw = torch.zeros(4 * D, device="cuda")
+        for T in (1, 5, 16, 64, 512, 4096):
+            x = moe.synth_bf16_normal(3, "x", T, (T, 4 * D), 1.0)
+            h, _, inv = moe.hc_mix_down(x, wd, R, True, 1e-6)
+            moe.hc_mix_up(h, wu, x, nw, inv)
+            torch.cuda.synchronize()
+            reps = 20 if T < 4096 else 5
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            e[0].record()
+            for _ in range(reps):
+                moe.hc_mix_down(x, wd, R, True, 1e-6)
+            e[1].record()
+            for _ in range(reps):
+                moe.hc_mix_up(h, wu, x, nw, inv)
+            e[2].record()
+            torch.cuda.synchronize()
+            log(f"hc Q{bits} T={T}: hc_mix_down {e[0].elapsed_time(e[1]) * 1e3 / reps:.1f} us, hc_mix_up "
+                f"{e[1].elapsed_time(e[2]) * 1e3 / reps:.1f} us (HIP events around the calls)")
 
 
 def capture(torch, fn):
@@ -192,6 +223,11 @@ def main():
         log("measured peaks:", peaks)
         del buf, buf2
         torch.cuda.empty_cache()
+
+    if args.hc:
+        hc_section(torch, moe)
+        if args.only == "hc":
+            return
 
     ctx = moe.LayerContext()
     nl = args.layers

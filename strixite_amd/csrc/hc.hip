@@ -14,8 +14,8 @@
 //
 // Two kernel designs, chosen by the token count:
 //
-// * Matrix-core tiles (T >= 16; the down mix also needs d % 128 == 0). Weights enter the bf16 MFMA
-//   (v_mfma_f32_16x16x32_bf16) as their exact integer codes and each quantization group's partial product D is
+// * Matrix-core tiles (the up mix from 1 token; the down mix from 256 tokens and d % 128 == 0). Weights enter the
+//   bf16 MFMA (v_mfma_f32_16x16x32_bf16) as their exact integer codes and each quantization group's partial product D is
 //   rescaled on the FP32 accumulator: w . x = s D + m' sum(x) (Q4 codes enter as 128 + n with m' = m - 128 s, Q8
 //   codes as c - 128 with m' = m + 128 s). The min terms of a whole K stage are one FP32 MFMA
 //   (v_mfma_f32_16x16x4f32: sums of x per group against m' per group). BF16 activations are exact in bf16; an FP32
@@ -35,10 +35,10 @@
 //     the epilogue happens in registers. h is converted to bf16 [hi, mid, lo] into LDS once per block (with its group
 //     sums); the chunk-major codes of a chunk's 16 rows are 256 (Q4) or 512 (Q8) contiguous bytes, read by the
 //     wave's lanes directly, four chunks ahead.
-// * Vector rows (down mix below 16 tokens, or d % 128 != 0): a block of 4 waves computes the group's inverse RMS into
-//   LDS, then each wave takes one weight row (T = 1: a row's chunks split over the 4 waves): per stream, lane l dots
-//   the stream's 32-code chunks l, l + 64, ... with the chunk of every token of the group (the codes converted to
-//   floats once for the group), a butterfly gives the stream's total, and a += inv_s * total.
+// * Vector rows (down mix below 256 tokens, or d % 128 != 0): a block of 4 waves computes the group's inverse RMS into
+//   LDS, then each wave takes one weight row (T = 1: a row's chunks split over the 4 waves): lane l dots the row's
+//   32-code chunks l, l + 64, ... with the chunk of every token of the group (the codes converted to floats once for
+//   the group) and adds each dot scaled by its stream's inverse RMS into one accumulator a token; a butterfly ends it.
 #include "common.hpp"
 
 #include <algorithm>
@@ -53,6 +53,10 @@ namespace {
 using namespace strix::dev;
 constexpr int kWave = 64, kStreams = 4, kChunk = 32;
 constexpr int64_t kMaxR = 1024, kMaxTokens = 65535, kMaxD = 1 << 20;
+// the down mix's matrix-core tiles from this many tokens: a 32-token tile block streams the whole weight, so with fewer
+// tiles than CUs the vector-row kernel, which spreads the rows over the CUs, is faster (measured at d 2560, r 320: tiles
+// ~100 us flat up to a few hundred tokens; rows 8 us at 1 token, ~60 at 64)
+constexpr int64_t kDownTileMinTokens = 256;
 
 __device__ __forceinline__ float ld_act(const float *p, int64_t i) { return p[i]; }
 __device__ __forceinline__ float ld_act(const uint16_t *p, int64_t i) { return bf16_to_f32(p[i]); }
@@ -427,15 +431,17 @@ __global__ void __launch_bounds__(dn::kThreads)
 template <int BITS, bool F32> constexpr size_t down_tile_lds() { return (size_t)2 * dn::Stage<BITS, F32>::SIZE * 4; }
 
 // ================================================================================================ down: vector rows
-// KS waves share a row (its chunks split over them, their per-stream totals meeting in LDS) or, KS = 1, a wave takes
-// one row; MT tokens a block
+// KS waves share a row (its chunks split over them, their totals meeting in LDS) or, KS = 1, a wave takes one row; MT
+// tokens a block. The streams' inverse RMS is known before the dot products (the block's first phase), so each
+// chunk's dot goes straight into one accumulator a token, scaled by its stream's inverse RMS:
+// a = sum over chunks of inv[stream(chunk)] (s dot + m sum(x)).
 template <typename T, int BITS, int MT, int KS>
 __global__ void __launch_bounds__(256)
     mix_down_rows_kernel(const T *x, const uint8_t *q, const uint16_t *scale, const uint16_t *minv, int64_t R,
                          int64_t d, int64_t G, int64_t r, float eps, int64_t Tn, float *h, float *w_in, float *inv) {
     constexpr int kWaves = 4;
     __shared__ float invs[MT][kStreams];
-    __shared__ float red[KS > 1 ? KS : 1][MT][kStreams];
+    __shared__ float red[KS > 1 ? KS : 1][MT];
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int64_t K = kStreams * d, t0 = (int64_t)blockIdx.y * MT;
     const int nt = (int)(Tn - t0 < MT ? Tn - t0 : MT);
@@ -460,68 +466,65 @@ __global__ void __launch_bounds__(256)
     if (KS == 1 && row >= R) return;  // after the block's only barrier (KS > 1: the grid holds whole rows)
     const int64_t grow = row < R ? row : R - 1;
     const uint8_t *qrow = q + grow * (K * BITS / 8);
-    const int64_t cpr = d / kChunk;  // chunks a stream
-    float tot[MT][kStreams];
+    const int64_t nc = K / kChunk, cps = d / kChunk;  // chunks of the row, chunks a stream
+    float iv[MT][kStreams];
 #pragma unroll
-    for (int s = 0; s < kStreams; ++s) {
-        float acc[MT];
+    for (int tt = 0; tt < MT; ++tt)
 #pragma unroll
-        for (int tt = 0; tt < MT; ++tt) acc[tt] = 0.f;
-        for (int64_t c = s * cpr + part * kWave + lane; c < (s + 1) * cpr; c += (int64_t)kWave * KS) {
-            uint32_t w[BITS];
+        for (int st = 0; st < kStreams; ++st) iv[tt][st] = tt < nt ? invs[tt][st] : 0.f;
+    float acc[MT];
 #pragma unroll
-            for (int i = 0; i < BITS / 4; ++i) {
-                const uint4 u = reinterpret_cast<const uint4 *>(qrow + c * (kChunk * BITS / 8))[i];
-                w[4 * i] = u.x, w[4 * i + 1] = u.y, w[4 * i + 2] = u.z, w[4 * i + 3] = u.w;
-            }
-            const int64_t gi = grow * (K / G) + c * kChunk / G;
-            const float sc = bf16_to_f32(scale[gi]), mn = bf16_to_f32(minv[gi]);
-            float cf[kChunk];
+    for (int tt = 0; tt < MT; ++tt) acc[tt] = 0.f;
+    for (int64_t c = (int64_t)part * kWave + lane; c < nc; c += (int64_t)kWave * KS) {
+        uint32_t w[BITS];
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k)
-                cf[k] = (float)((w[k * BITS / 32] >> ((k * BITS) % 32)) & ((1u << BITS) - 1u));
-#pragma unroll
-            for (int tt = 0; tt < MT; ++tt) {
-                if (tt >= nt) break;
-                const T *xc = x + (t0 + tt) * K + c * kChunk;
-                float dot = 0.f, xsum = 0.f;
-#pragma unroll
-                for (int p8 = 0; p8 < kChunk / 8; ++p8) {
-                    float v[8];
-                    ld8(xc, 8 * p8, v);
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) dot = fmaf(v[k], cf[8 * p8 + k], dot), xsum += v[k];
-                }
-                acc[tt] = fmaf(sc, dot, fmaf(mn, xsum, acc[tt]));
-            }
+        for (int i = 0; i < BITS / 4; ++i) {
+            const uint4 u = reinterpret_cast<const uint4 *>(qrow + c * (kChunk * BITS / 8))[i];
+            w[4 * i] = u.x, w[4 * i + 1] = u.y, w[4 * i + 2] = u.z, w[4 * i + 3] = u.w;
         }
+        const int64_t gi = grow * (K / G) + c * kChunk / G;
+        const float sc = bf16_to_f32(scale[gi]), mn = bf16_to_f32(minv[gi]);
+        const int sg = (int)(c / cps);  // the chunk's stream
+        float cf[kChunk];
 #pragma unroll
-        for (int tt = 0; tt < MT; ++tt) tot[tt][s] = wave_sum(acc[tt]);
+        for (int k = 0; k < kChunk; ++k)
+            cf[k] = (float)((w[k * BITS / 32] >> ((k * BITS) % 32)) & ((1u << BITS) - 1u));
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt) {
+            if (tt >= nt) break;
+            const T *xc = x + (t0 + tt) * K + c * kChunk;
+            float dot = 0.f, xsum = 0.f;
+#pragma unroll
+            for (int p8 = 0; p8 < kChunk / 8; ++p8) {
+                float v[8];
+                ld8(xc, 8 * p8, v);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) dot = fmaf(v[k], cf[8 * p8 + k], dot), xsum += v[k];
+            }
+            const float s_inv = sg == 0 ? iv[tt][0] : sg == 1 ? iv[tt][1] : sg == 2 ? iv[tt][2] : iv[tt][3];
+            acc[tt] = fmaf(s_inv, fmaf(sc, dot, mn * xsum), acc[tt]);
+        }
     }
+    float tot[MT];
+#pragma unroll
+    for (int tt = 0; tt < MT; ++tt) tot[tt] = wave_sum(acc[tt]);
     if constexpr (KS > 1) {
         if (lane == 0)
 #pragma unroll
-            for (int tt = 0; tt < MT; ++tt)
-#pragma unroll
-                for (int s = 0; s < kStreams; ++s) red[part][tt][s] = tot[tt][s];
+            for (int tt = 0; tt < MT; ++tt) red[part][tt] = tot[tt];
         __syncthreads();
         if (part != 0) return;
 #pragma unroll
-        for (int tt = 0; tt < MT; ++tt)
-#pragma unroll
-            for (int s = 0; s < kStreams; ++s) {
-                float v = 0.f;
-                for (int k = 0; k < KS; ++k) v += red[k][tt][s];
-                tot[tt][s] = v;
-            }
+        for (int tt = 0; tt < MT; ++tt) {
+            float v = 0.f;
+            for (int k = 0; k < KS; ++k) v += red[k][tt];
+            tot[tt] = v;
+        }
     }
     if (lane != 0 || row >= R) return;
     for (int tt = 0; tt < nt; ++tt) {
-        float a = 0.f;
-#pragma unroll
-        for (int s = 0; s < kStreams; ++s) a = fmaf(invs[tt][s], tot[tt][s], a);
         const int64_t t = t0 + tt;
-        const float z = a * 0.25f;
+        const float z = tot[tt] * 0.25f;
         if (row < r) h[t * r + row] = z / (1.0f + expf(-z));
         else w_in[t * kStreams + (row - r)] = 2.0f / (1.0f + expf(-z));
     }
@@ -557,9 +560,12 @@ __global__ void __launch_bounds__(WAVES * kWave)
         int t = 0, k8 = 0;
         if (uix < units) {
             t = uix / (int)(r / 8), k8 = uix % (int)(r / 8);
-            const int64_t tg = t0 + t < Tn ? t0 + t : Tn - 1;
-            const float4 a = *reinterpret_cast<const float4 *>(h + tg * r + 8 * k8),
-                         b = *reinterpret_cast<const float4 *>(h + tg * r + 8 * k8 + 4);
+            // rows past the tokens are zeros (their outputs are not stored), so a short batch loads only its rows
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            if (t0 + t < Tn) {
+                a = *reinterpret_cast<const float4 *>(h + (t0 + t) * r + 8 * k8);
+                b = *reinterpret_cast<const float4 *>(h + (t0 + t) * r + 8 * k8 + 4);
+            }
             const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
             const Split v = split8(f);
             *reinterpret_cast<uint4 *>(hh + t * rdw + 4 * k8) = uint4{v.hi.d[0], v.hi.d[1], v.hi.d[2], v.hi.d[3]};
@@ -597,8 +603,40 @@ __global__ void __launch_bounds__(WAVES * kWave)
             a.sc[s] = scale[g * N + s * d + j0 + n];
         }
     };
+    // the operands of the min terms and of the epilogue depend on nothing the loop computes: for a 16-token tile (a
+    // short, latency-bound kernel) they are loaded now, so their round trips overlap the loop instead of following it
+    // (all loads unconditional, indices clamped); a 32-token tile has no registers to spare and loads them after it
+    constexpr bool kHoist = MT == 1;
+    constexpr int kMinPre = kHoist ? 2 : 1;  // four-group steps of the min terms held here; more load after the loop
+    uint16_t pre_s[kMinPre][kStreams], pre_m[kMinPre][kStreams];
+#pragma unroll
+    for (int gs = 0; gs < kMinPre; ++gs) {
+        if (!kHoist) break;
+        const int g = 4 * gs + qd < ngr ? 4 * gs + qd : 0;
+#pragma unroll
+        for (int s = 0; s < kStreams; ++s) {
+            const int64_t gi = g * N + s * d + j0 + n;
+            pre_s[gs][s] = scale[gi], pre_m[gs][s] = minv[gi];
+        }
+    }
+    const int64_t j = j0 + n;  // < d: d is a multiple of 16
+    float nwv[kStreams], xe[MT][4][kStreams], ie[MT][4][kStreams];
+    auto load_epilogue = [&]() {
+#pragma unroll
+        for (int s = 0; s < kStreams; ++s) nwv[s] = 1.0f + norm_w[s * d + j];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t t = t0 + 16 * m + 4 * qd + i, tc = t < Tn ? t : Tn - 1;
+#pragma unroll
+            for (int s = 0; s < kStreams; ++s) xe[m][i][s] = ld_act(x, tc * N + s * d + j), ie[m][i][s] = inv[tc * kStreams + s];
+        }
+    };
+    if constexpr (kHoist) load_epilogue();
+
     // a ring of kAhead chunks in flight: chunk c computes from slot c % kAhead, then that slot loads chunk c + kAhead
-    constexpr int kAhead = 4;
+    constexpr int kAhead = 4;  // (8 for the 16-token tiles measured slower: 15.1 against 13.2 us at 1 token)
     Ahead ring[kAhead];
 #pragma unroll
     for (int p = 0; p < kAhead; ++p) ld_chunk(p, ring[p]);
@@ -646,8 +684,15 @@ __global__ void __launch_bounds__(WAVES * kWave)
         for (int s = 0; s < kStreams; ++s) {
             float mp = 0.f;
             if (g < ngr) {
-                const int64_t gi = g * N + s * d + j0 + n;
-                const float sc = bf16_to_f32(scale[gi]), mn = bf16_to_f32(minv[gi]);
+                float sc, mn;
+                if (kHoist && g4 / 4 < kMinPre) {
+                    const int gs = g4 / 4;
+                    sc = bf16_to_f32(gs == 0 ? pre_s[0][s] : pre_s[kMinPre - 1][s]);
+                    mn = bf16_to_f32(gs == 0 ? pre_m[0][s] : pre_m[kMinPre - 1][s]);
+                } else {
+                    const int64_t gi = g * N + s * d + j0 + n;
+                    sc = bf16_to_f32(scale[gi]), mn = bf16_to_f32(minv[gi]);
+                }
                 mp = min_prime<BITS>(sc, mn);
             }
 #pragma unroll
@@ -655,11 +700,7 @@ __global__ void __launch_bounds__(WAVES * kWave)
         }
     }
     // epilogue: gates and the stream combine, in registers
-    const int64_t j = j0 + n;
-    if (j >= d) return;
-    float nw[kStreams];
-#pragma unroll
-    for (int s = 0; s < kStreams; ++s) nw[s] = 1.0f + norm_w[s * d + j];
+    if constexpr (!kHoist) load_epilogue();
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -670,7 +711,7 @@ __global__ void __launch_bounds__(WAVES * kWave)
 #pragma unroll
             for (int s = 0; s < kStreams; ++s) {
                 const float gate = 1.0f / (1.0f + expf(-acc[s][m][i]));
-                sum += gate * (ld_act(x, t * N + s * d + j) * inv[t * kStreams + s] * nw[s]);
+                sum += gate * (xe[m][i][s] * ie[m][i][s] * nwv[s]);
             }
             st_act(u, t * d + j, sum * 0.25f);
         }
@@ -732,7 +773,7 @@ void run_mix_down(const void *x, const Weights &w, int64_t T, int64_t H, int64_t
                 " rows are needed");
     STRIX_CHECK(std::isfinite(eps) && eps > 0.f, what, ": eps = ", eps, " (a finite positive value is needed)");
     const bool f32 = act == Act::F32;
-    if (T >= 16 && d % dn::kK == 0) {  // matrix-core tiles
+    if (T >= kDownTileMinTokens && d % dn::kK == 0) {  // matrix-core tiles
         const int64_t nrb = (R + dn::kRows - 1) / dn::kRows, ntt = (T + dn::kTok - 1) / dn::kTok;
         const size_t lds = f32 ? down_tile_lds<BITS, true>() : down_tile_lds<BITS, false>();
         auto go = [&](auto tag, auto gtag) {
@@ -790,7 +831,9 @@ void run_mix_up(const float *h, const Weights &w, const void *x, const float *no
     STRIX_CHECK(reinterpret_cast<uintptr_t>(h) % 16 == 0, what, ": h must start on a 16-byte boundary");
     const int64_t es = act == Act::F32 ? 4 : 2;
     STRIX_CHECK(disjoint(u, T * d * es, x, T * H * d * es), what, ": u and the streams x overlap");
-    const bool small = T <= 16 || w.K > 768;  // 32-token tiles of h up to r = 768 fit the LDS
+    // 16-token tiles of 4 waves a block up to 16 tokens, 32-token tiles of 8 waves above (the h tile shared by more
+    // columns); 32-token tiles of h fit the LDS up to r = 768
+    const bool small = T <= 16 || w.K > 768;
     const int MT = small ? 1 : 2, WAVES = small ? 4 : 8;
     const size_t lds = up_tile_lds(MT, w.K, w.G);
     const int64_t njb = (d / 16 + WAVES - 1) / WAVES, ntt = (T + 16 * MT - 1) / (16 * MT);

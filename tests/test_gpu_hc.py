@@ -33,12 +33,13 @@ def _weight(bits, N, K, G, seed, chunk_major=False):
     return moe.QWeight.from_host(bits, q, s, m, N, K, G), w64
 
 
-# token counts below 16 (and d % 128 != 0) take the vector-row down kernel, the rest the matrix-core tiles; every up
+# token counts below 256 (and d % 128 != 0) take the vector-row down kernel, the rest the matrix-core tiles; every up
 # mix runs on the matrix cores (16-token tiles up to 16 tokens, 32-token tiles above)
 CASES = [(4, 64, "bf16", 1, 256, 64, True), (4, 128, "f32", 5, 256, 96, True), (8, 32, "bf16", 37, 128, 32, False),
          (8, 64, "f32", 8, 512, 320, True), (4, 64, "bf16", 3, 2560, 320, True), (4, 32, "f32", 40, 256, 320, True),
          (8, 128, "bf16", 100, 384, 64, True), (8, 32, "f32", 17, 128, 96, False), (4, 64, "bf16", 16, 160, 64, True),
-         (4, 64, "bf16", 4096, 2560, 320, True)]
+         (8, 128, "bf16", 300, 384, 64, True), (4, 32, "f32", 260, 256, 320, True), (8, 32, "f32", 256, 128, 96, False),
+         (4, 64, "bf16", 257, 160, 64, True), (4, 64, "bf16", 4096, 2560, 320, True)]
 
 
 @pytest.mark.parametrize("bits,G,act,T,d,r,inject", CASES)
