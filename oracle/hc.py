@@ -52,7 +52,8 @@ def hc_mix_up(h: np.ndarray, wup64: np.ndarray, x: np.ndarray, norm_w: np.ndarra
     """u [T, d] = (1/4) sum_s sigmoid(W_up[s d + j] . h[t]) * X[t, s d + j] inv[t, s] (1 + norm_w[s d + j]), W_up
     [4 d, r] (strixite kernels/hc.hpp:38-50)."""
     T = x.shape[0]
-    g = 1.0 / (1.0 + np.exp(-(np.asarray(h, np.float64) @ wup64.T)))
+    with np.errstate(over="ignore"):  # exp overflow to inf gives the gate's limit 0 exactly
+        g = 1.0 / (1.0 + np.exp(-(np.asarray(h, np.float64) @ wup64.T)))
     n = np.asarray(x, np.float64).reshape(T, STREAMS, d) * np.asarray(inv, np.float64)[:, :, None] * (
         1.0 + np.asarray(norm_w, np.float64).reshape(STREAMS, d))
     return (g.reshape(T, STREAMS, d) * n).sum(axis=1) / STREAMS
