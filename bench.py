@@ -287,9 +287,11 @@ def main():
     routes = [moe.moe_group_routes(outs[l]["ids"], E)[0] for l in range(nl)]
     hbuf = [torch.empty((Md * K_TOP, I), dtype=torch.bfloat16, device=dev) for _ in range(nl)]
     torch.cuda.synchronize()
-    # one graph of the kernel over the 8 layers' routing (its own launches only, no host gap between them)
+    # one graph of the kernel over the 8 layers' routing (its own launches only, no host gap between them); the
+    # exact-weight math the layer's decode runs
     ggu = capture(torch, lambda: [moe.experts_gather_grouped_swiglu(xs[l], dlayers[l].gate_up, E, routes[l], Md, K_TOP,
-                                                                    h=hbuf[l]) for l in range(nl)])
+                                                                    h=hbuf[l], math=moe.MOE_MATH_WMMA_BF16)
+                                  for l in range(nl)])
     gu_ms = timer(lambda i: ggu.replay(), steps=max(3, args.steps // nl)) / nl
     gu_bytes = statistics.mean(u * GU_BYTES_PER_EXPERT + Md * H * 2 + Md * K_TOP * I * 2 for u in un)
     gu_gbs = gu_bytes / (gu_ms / 1e3) / 1e9

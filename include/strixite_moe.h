@@ -9,7 +9,7 @@
  * STRIX_E_GPU when the HIP runtime reports an error; strix_moe_last_error() then holds the message (thread-local).
  * Device-detected data errors (non-finite logits, invalid expert ids) never trap: they set the caller-zeroed
  * uint32_t err[3] word ({1, token or id, expert or slot}, first flag wins) and make the affected rows NaN.
- * act / out_act: 0 = F32, 1 = BF16 (strixite kernels/norm.hpp:20 Act). math: strixite MoeMath (0..5; 2..5 = the F16 math for Q4 experts at prefill sizes).
+ * act / out_act: 0 = F32, 1 = BF16 (strixite kernels/norm.hpp:20 Act). math: strixite MoeMath (0..5; 2..5 = the F16 math for Q4 experts' grouped projections).
  */
 #ifndef STRIXITE_MOE_H
 #define STRIXITE_MOE_H

@@ -6,11 +6,12 @@
 // functions with the same types, and this library exports exactly those symbols - and include only
 // strixite_moe_extras.hpp with STRIXITE_MOE_DROPIN defined.
 //
-// Numerics shared by the expert kernels: activations BF16; at decode sizes (and for Q8 experts, the shared expert and
-// the exact MoeMath kinds) the weights enter the matrix cores as their exact integer codes in BF16 with the group's
-// scale and min applied to the FP32 accumulator (v_mfma_f32_16x16x32_bf16), so no weight is rounded; Q4 experts at
-// prefill sizes under the F16 MoeMath kinds use the reference's F16 math (v_mfma_f32_32x32x16_f16). Every stored
-// value is rounded once (RNE) to BF16. Router logits are FP32 in one fixed summation order (linear_bf16w below).
+// Numerics shared by the expert kernels: activations BF16; under the exact MoeMath kinds (and for Q8 experts and the
+// shared expert) the weights enter the matrix cores as their exact integer codes in BF16 with the group's scale and
+// min applied to the FP32 accumulator (v_mfma_f32_16x16x32_bf16), so no weight is rounded; the grouped Q4 entry points
+// under the F16 MoeMath kinds use the reference's F16 math (v_mfma_f32_32x32x16_f16) at every batch size, and the
+// sublayer call (moe_layer_forward) uses it at prefill sizes, exact weights at decode sizes. Every stored value is
+// rounded once (RNE) to BF16. Router logits are FP32 in one fixed summation order (linear_bf16w below).
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -282,6 +282,14 @@ def experts_gate_up_swiglu_f16math(x, bits, q, s, m, N_total, K, G, E, ids):
         return f32_to_bf16((g / (np.float32(1) + np.exp(-g))) * u)
 
 
+def experts_gather_f16math(x, bits, q, s, m, N_total, K, G, E, ids):
+    """FP32 per-slot gate_up (no SwiGLU) outputs [M * A, N] of the F16 math (x rows by slot // A; strixite
+    kernels/moe_grouped.hip:348-351, the plain gather under an F16 kind)."""
+    assert bits == 4, "F16 matrix-unit math: Q4 experts"
+    A = ids.shape[1]
+    return _f16_grouped(x, q4_weights_f16(q, s, m, N_total, K, G), E, ids, lambda sl: sl // A)
+
+
 def experts_down_f16math(h, bits, q, s, m, N_total, K, G, E, ids):
     """FP32 per-slot down outputs [M * A, N] of the F16 math (h BF16 bits, slot rows)."""
     assert bits == 4, "F16 matrix-unit math: Q4 experts"

@@ -1,4 +1,4 @@
-// Prefill-size grouped projections of the Q4 (g128) experts in the reference's F16 matrix-unit math: included by
+// Grouped projections of the Q4 (g32 / g64 / g128) experts in the reference's F16 matrix-unit math: included by
 // experts.hip after expert_gemm.hpp (it uses GemmArgs, the epilogues, the buffer-load helpers and the 64-slot tile
 // records).
 //
@@ -11,9 +11,10 @@
 //
 // Block: 4 waves, BM = 128 token slots (two consecutive 64-slot tile records of one expert's bucket) x BN = 256 weight
 // rows (SwiGLU: 128 gate rows and the matching 128 up rows, a wave 32 + 32; otherwise a wave 64 consecutive rows).
-// K runs in chunks of 64, two per quantization group. The block's activations (gathered by slot) reach LDS two
-// chunks ahead: X16 (x already F16 in the paired order below) straight from memory into one of three LDS buffers;
-// otherwise (BF16 x) through registers, converted there, into one of two. The 16-byte columns of an LDS row are
+// K runs in chunks of 64: two a quantization group at G 128, one at G 64; at G 32 each lane half's 32 k of a chunk
+// are one group. The block's activations (gathered by slot) reach LDS two chunks ahead: X_F16P (x already F16 in the
+// paired order below) straight from memory into one of three LDS buffers; otherwise (BF16 x, or F16 x in natural
+// order) through registers, converted or permuted there, into one of two. The 16-byte columns of an LDS row are
 // XOR-swizzled by the row, so the MFMA reads are conflict-free. Each lane loads its weight row's 32 codes of a chunk
 // (16 bytes) two chunks ahead. A block whose slots fill fewer than 4 of its 32-token sub-tiles runs a K loop for just
 // the live ones.
@@ -27,8 +28,10 @@
 
 namespace g2 {
 constexpr int BM = 128, BN = 256, BK = 64, kThreads = 256;
-// h forms of the SwiGLU epilogue: BF16, F16 (natural order), F16 in the paired order (an X16 input)
+// h forms of the SwiGLU epilogue: BF16, F16 (natural order), F16 in the paired order (an X_F16P input)
 enum HForm { H_BF16 = 0, H_F16 = 1, H_F16P = 2 };
+// activation forms: BF16, F16 in the paired order (loaded straight into LDS), F16 in natural order (an H_F16 h)
+enum XForm { X_BF16 = 0, X_F16P = 1, X_F16 = 2 };
 }  // namespace g2
 
 typedef float float16v __attribute__((ext_vector_type(16)));
@@ -81,6 +84,12 @@ __device__ __forceinline__ uint4 bf16x8_to_f16_paired(const uint4 &v) {
                       pk_f16_rtz(hi(v.y), hi(v.w)));
 }
 
+// 8 F16 activations in natural k order -> the paired order (k0 k4, k1 k5, k2 k6, k3 k7 a dword)
+__device__ __forceinline__ uint4 f16x8_to_paired(const uint4 &v) {
+    return make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                      __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+}
+
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14)
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -93,12 +102,14 @@ __global__ void __launch_bounds__(256) bf16_to_f16_paired_kernel(const uint4 *x,
         y[i] = bf16x8_to_f16_paired(x[i]);
 }
 
-template <int EPI, bool XROW_DIV, int HF, bool X16>
+template <int EPI, bool XROW_DIV, int HF, int XF, int GS>
 __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     expert_gemm2_kernel(GemmArgs a, int64_t tiles_bound, int64_t col_blocks, int64_t rec64, uint32_t q_bytes,
                         uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
     using namespace g2;
-    constexpr bool SWI = EPI == EPI_SWIGLU;
+    constexpr bool SWI = EPI == EPI_SWIGLU, X16 = XF == X_F16P;
+    static_assert(GS == 32 || GS == 64 || GS == 128, "group sizes 32, 64, 128");
+    constexpr int CPG = GS > BK ? GS / BK : 1;  // chunks that start with a new scale and min
     // the activation buffers [row * 8 + (col ^ (row & 7))], separate arrays picked at compile time: the compiler
     // then tells a read of one from the loads still landing in another and waits for those loads no longer than it
     // must
@@ -133,8 +144,8 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
 
     const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, x_bytes), rq = rsrc(a.q, q_bytes), rs = rsrc(a.scale, s_bytes),
                                  rm = rsrc(a.minv, s_bytes), ry = rsrc(a.y, y_bytes);
-    const uint32_t K = (uint32_t)a.K, groups = (uint32_t)(a.K / a.G);
-    const int chunks = (int)(a.K / BK);  // even: two a group
+    const uint32_t K = (uint32_t)a.K, groups = (uint32_t)(a.K / GS);
+    const int chunks = (int)(a.K / BK);
     // this thread's activation pieces: LDS slots tid + 256 v (v = 0..3) = row / 8, column ^ (row & 7)
     uint32_t xoff[4];
 #pragma unroll
@@ -165,8 +176,9 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     asm("v_mov_b32 %0, 0x54005400" : "=v"(b54));
 
     // Loads past the last chunk read in-bounds or zero data that is never used. X16: every chunk issues the same
-    // loads in the same order (scales at a group's first chunk, then codes and activations two chunks ahead), so the
-    // activations of chunk c are in LDS once at most 6 (c even) or 10 (c odd) later loads are outstanding.
+    // loads in the same order (4 scale and min loads at a chunk that starts a group, then codes and activations two
+    // chunks ahead), so the activations of chunk c are in LDS once at most 6 (chunk c - 1 loaded no scales: c odd at
+    // G 128, and chunk 0) or 10 later loads are outstanding.
     uint4 ar[2][4];  // !X16: activations in flight
     constexpr int QPF = 2;  // chunks of codes in flight
     uint4 qr[QPF][2];
@@ -184,15 +196,18 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     };
     auto store_a = [&](const uint4 (&src)[4], int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) abuf(buf)[tid + 256 * v] = bf16x8_to_f16_paired(src[v]);
+        for (int v = 0; v < 4; ++v)
+            abuf(buf)[tid + 256 * v] = XF == X_F16 ? f16x8_to_paired(src[v]) : bf16x8_to_f16_paired(src[v]);
     };
     // scale and min of the current group for the two tiles (F16 pairs); the next group's raw bf16 loaded a group ahead
+    // (chunk c: this lane half's k 64 c + 32 h lie in group (64 c + 32 h) / G)
     f16x2v sc[2], mn[2];
     uint16_t sraw[2], mraw[2];
-    auto load_sm = [&](int gi) __attribute__((always_inline)) {
+    auto load_sm = [&](int c) __attribute__((always_inline)) {
+        const uint32_t gi = ((uint32_t)c * BK + 32u * (uint32_t)h) / GS;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const uint32_t o = gi < (int)groups ? soff[t] + 2 * (uint32_t)gi : s_bytes;
+            const uint32_t o = c < chunks ? soff[t] + 2 * gi : s_bytes;
             sraw[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0);
             mraw[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rm, o, 0, 0);
         }
@@ -223,8 +238,9 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
         for (int i = 0; i < NT; ++i)
 #pragma unroll
             for (int t = 0; t < 2; ++t) acc[i][t] = float16v{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        // trips of TRIP chunks (X16: 6, so the three buffers' turns are known at compile time)
+        // trips of TRIP chunks (X16: 6, so the three buffers' turns are known at compile time; a multiple of CPG)
         constexpr int TRIP = X16 ? 6 : 2;
+        static_assert(TRIP % CPG == 0, "a trip starts a group");
         for (int c0 = 0; c0 < chunks; c0 += TRIP) {
 #pragma unroll
             for (int pt = 0; pt < TRIP; ++pt) {
@@ -232,13 +248,14 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                 if (c >= chunks) break;
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (X16) {
-                    if (p == 0) wait_vmcnt<6>();
+                    // chunk c - 1 loaded no scales (CPG 2: c even); CPG 1: at a trip's start, also right for chunk 0
+                    if ((CPG == 2 && p == 0) || (CPG == 1 && pt == 0)) wait_vmcnt<6>();
                     else wait_vmcnt<10>();
                 }
-                if (p == 0) {
+                if (pt % CPG == 0) {
 #pragma unroll
                     for (int t = 0; t < 2; ++t) sc[t] = bf16_to_f16x2(sraw[t]), mn[t] = bf16_to_f16x2(mraw[t]);
-                    load_sm(c / 2 + 1);
+                    load_sm(c + CPG);
                 }
                 // chunk c's activations are visible; every wave is done with chunk c - 1's buffer. X16: each wave has
                 // waited for its own loads into LDS above; a plain barrier (no fence) keeps the later loads in flight.
@@ -355,13 +372,14 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     else run(std::integral_constant<int, 1>{});
 }
 
-// Launch for Q4 g128 grouped projections (activations BF16, or F16 in the paired order when X16; SwiGLU h in the
-// form HF, or FP32 partials); false when the shape is outside what the kernel takes.
+// Launch for Q4 g32 / g64 / g128 grouped projections (activations in the form XF; SwiGLU h in the form HF, or BF16
+// outputs); false when the shape is outside what the kernel takes.
 template <int EPI> bool expert_gemm2_fits(const GemmArgs &a) {
-    return a.G == 2 * g2::BK && a.K % a.G == 0 && (EPI == EPI_SWIGLU ? (a.N / 2) % 32 : a.N % 32) == 0;
+    return (a.G == 32 || a.G == 64 || a.G == 128) && a.K % g2::BK == 0 && a.K % a.G == 0 &&
+           (EPI == EPI_SWIGLU ? (a.N / 2) % 32 : a.N % 32) == 0;
 }
 
-template <int EPI, bool XROW_DIV, int HF, bool X16>
+template <int EPI, bool XROW_DIV, int HF, int XF>
 bool launch_expert_gemm2(const GemmArgs &a, hipStream_t stream) {
     using namespace g2;
     if (!expert_gemm2_fits<EPI>(a)) return false;
@@ -373,9 +391,16 @@ bool launch_expert_gemm2(const GemmArgs &a, hipStream_t stream) {
     if (q_bytes >= (1ll << 31) || s_bytes >= (1ll << 31) || x_bytes >= (1ll << 31) || y_bytes >= (1ll << 31)) return false;
     const int64_t blocks = (tiles_bound + 7) / 8 * 8 * col_blocks;  // whole rounds of the 8 XCDs
     if (blocks >= (1ll << 31)) return false;
-    expert_gemm2_kernel<EPI, XROW_DIV, HF, X16><<<(unsigned)blocks, g2::kThreads, 0, stream>>>(
-        a, tiles_bound, col_blocks, t64_rec_at(a.S, a.E), (uint32_t)q_bytes, (uint32_t)s_bytes, (uint32_t)x_bytes,
-        (uint32_t)y_bytes);
+    auto go = [&](auto gs) {
+        expert_gemm2_kernel<EPI, XROW_DIV, HF, XF, decltype(gs)::value><<<(unsigned)blocks, g2::kThreads, 0, stream>>>(
+            a, tiles_bound, col_blocks, t64_rec_at(a.S, a.E), (uint32_t)q_bytes, (uint32_t)s_bytes, (uint32_t)x_bytes,
+            (uint32_t)y_bytes);
+    };
+    switch (a.G) {
+        case 32: go(std::integral_constant<int, 32>{}); break;
+        case 64: go(std::integral_constant<int, 64>{}); break;
+        default: go(std::integral_constant<int, 128>{}); break;
+    }
     return true;
 }
 

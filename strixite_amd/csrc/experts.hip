@@ -1322,11 +1322,12 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
     GemmArgs a = make_args(w, E, x, h, I);
     a.A = A, a.ws = static_cast<const int32_t *>(ws), a.S = M * A;
     const int64_t tiles = grouped_tiles(M, A, E);
-    if (use_expert_gemm(M * A, E, w.K, w.G)) {
+    // the F16 kinds on Q4 experts: the F16 math at every batch size, as the reference's F16 kernels
+    if (f16 && w.bits == 4 && (h_f16 ? launch_expert_gemm2<EPI_SWIGLU, true, g2::H_F16, g2::X_BF16>(a, stream)
+                                     : launch_expert_gemm2<EPI_SWIGLU, true, g2::H_BF16, g2::X_BF16>(a, stream))) {
+    } else if (use_expert_gemm(M * A, E, w.K, w.G)) {
         if (w.bits == 4) {
-            if (f16 && (h_f16 ? launch_expert_gemm2<EPI_SWIGLU, true, g2::H_F16, false>(a, stream)
-                              : launch_expert_gemm2<EPI_SWIGLU, true, g2::H_BF16, false>(a, stream))) {
-            } else if (h_f16) launch_expert_gemm<4, GROUPED, EPI_SWIGLU, true, true>(a, stream);
+            if (h_f16) launch_expert_gemm<4, GROUPED, EPI_SWIGLU, true, true>(a, stream);
             else launch_expert_gemm<4, GROUPED, EPI_SWIGLU, true, false>(a, stream);
         } else {
             if (h_f16) launch_expert_gemm<8, GROUPED, EPI_SWIGLU, true, true>(a, stream);
@@ -1431,12 +1432,13 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
     const int64_t tiles = grouped_tiles(M, A, E);
     // the F16 math keeps its per-slot partials in BF16 in the first half of partial, as the reference's F16 kinds do
     // (strixite kernels/moe_grouped.hpp:84); every other form keeps them FP32
-    bool pb = false;
-    if (!h_f16 && use_expert_gemm(M * A, E, w.K, w.G)) {  // (the GEMM reads bf16 activations only)
-        if (w.bits == 4) {
-            pb = f16 && launch_expert_gemm2<EPI_BF16, false, g2::H_BF16, false>(a, stream);
-            if (!pb) launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
-        } else launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
+    bool pb = f16 && w.bits == 4 &&
+              (h_f16 ? launch_expert_gemm2<EPI_BF16, false, g2::H_BF16, g2::X_F16>(a, stream)
+                     : launch_expert_gemm2<EPI_BF16, false, g2::H_BF16, g2::X_BF16>(a, stream));
+    if (pb) {
+    } else if (!h_f16 && use_expert_gemm(M * A, E, w.K, w.G)) {  // (the GEMM reads bf16 activations only)
+        if (w.bits == 4) launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
+        else launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
     } else if (!h_f16 && w.bits == 4 && M <= dec::kMaxTokens && decode_fits(a, M, false)) {
         launch_decode_down(a, M, nullptr, stream);
     } else if (h_f16) launch_bits<GROUPED, EPI_F32, true, false, false>(w.bits, a, tiles, stream);
@@ -1460,7 +1462,8 @@ void check_perslot(const char *fn, const void *x, const QV &w, int64_t E, const 
 
 // ---- grouped -------------------------------------------------------------------------------------------------------
 void linear_q4_experts_gather_grouped(const void *x, const Q4DeviceView &w, int64_t E, const void *ws,
-                                      size_t ws_bytes, int64_t M, int64_t A, void *y, Act act, MoeMath, hipStream_t stream) {
+                                      size_t ws_bytes, int64_t M, int64_t A, void *y, Act act, MoeMath math,
+                                      hipStream_t stream) {
     const char *fn = "linear_q4_experts_gather_grouped";
     const QV v = qv(w);
     const int64_t N = v.N / E;
@@ -1472,7 +1475,9 @@ void linear_q4_experts_gather_grouped(const void *x, const Q4DeviceView &w, int6
     STRIX_CHECK(reinterpret_cast<uintptr_t>(y) % 8 == 0, fn, ": y must be 8-byte aligned");
     GemmArgs a = make_args(v, E, x, y, N);
     a.A = A, a.ws = static_cast<const int32_t *>(ws), a.S = M * A;
-    launch_gemm<4, GROUPED, EPI_BF16, false, true, false>(a, grouped_tiles(M, A, E), stream);
+    // the F16 kinds: the F16 math (outputs rounded once to BF16); else exact weights
+    if (!(f16_math(math) && launch_expert_gemm2<EPI_BF16, true, g2::H_BF16, g2::X_BF16>(a, stream)))
+        launch_gemm<4, GROUPED, EPI_BF16, false, true, false>(a, grouped_tiles(M, A, E), stream);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E);
 }
 
@@ -2032,7 +2037,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     if (f16p) {
         check_grouped(fn, x, qv(w.gate_up), Es, route, L.route_bytes, M, A, h, Act::BF16, M * A * I * 2, M);
         if (!x16_done) bf16_to_f16_paired(x, base + L.x16, M, H, stream);
-        STRIX_CHECK((launch_expert_gemm2<EPI_SWIGLU, true, g2::H_F16P, true>(gu2, stream)), fn, ": F16 gate_up");
+        STRIX_CHECK((launch_expert_gemm2<EPI_SWIGLU, true, g2::H_F16P, g2::X_F16P>(gu2, stream)), fn, ": F16 gate_up");
     } else if (fold) {
         const QV gv = q8 ? qv(gu8) : qv(w.gate_up);
         check_grouped(fn, x, gv, Es, route, L.route_bytes, M, A, h, Act::BF16, M * A * I * 2, M);
@@ -2052,7 +2057,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         GemmArgs a = make_args(dv, Es, h, partial, H);
         a.A = A, a.ws = static_cast<const int32_t *>(route), a.S = M * A;
         if (f16p) {
-            STRIX_CHECK((launch_expert_gemm2<EPI_BF16, false, g2::H_BF16, true>(dn2, stream)), fn, ": F16 down");
+            STRIX_CHECK((launch_expert_gemm2<EPI_BF16, false, g2::H_BF16, g2::X_F16P>(dn2, stream)), fn, ": F16 down");
         } else if (use_expert_gemm(M * A, Es, dv.K, dv.G)) {
             if (q8) launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
             else launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);

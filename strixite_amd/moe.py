@@ -18,8 +18,9 @@ from . import _lib as L
 from ._lib import GpuError, StrixError  # noqa: F401  (re-exported)
 
 F32, BF16 = 0, 1
-# strixite MoeMath (kernels/moe_grouped.hpp:39): the F16 kinds (2..5) run Q4 experts' prefill-size grouped GEMMs in
-# the reference's F16 math (x and the dequantized weights in F16); F32 and WmmaBf16 keep the weights exact
+# strixite MoeMath (kernels/moe_grouped.hpp:39): the F16 kinds (2..5) run Q4 experts' grouped projections in the
+# reference's F16 math (x and the dequantized weights in F16) at every batch size; F32 and WmmaBf16 keep the weights
+# exact (and take the decode-size stream kernels)
 MOE_MATH_F32, MOE_MATH_WMMA_BF16, MOE_MATH_WMMA_F16 = 0, 1, 2
 
 TENSOR = {  # tensor ids of the seeded generator (oracle/moe_oracle.c uses the same ids)
@@ -215,7 +216,7 @@ def experts_gather_grouped_swiglu(x, w: QWeight, E, ws, M, A, h_f16=False, h=Non
     return h
 
 
-def experts_gather_grouped(x, w: QWeight, E, ws, M, A, y=None):
+def experts_gather_grouped(x, w: QWeight, E, ws, M, A, y=None, math=MOE_MATH_WMMA_F16):
     """strixite kernels/moe_grouped.hpp:56-58: y [M * A, N] = x[slot / A] W[id]^T (Q4)."""
     N = w.N // E
     if y is None:
@@ -223,7 +224,7 @@ def experts_gather_grouped(x, w: QWeight, E, ws, M, A, y=None):
     v = w.view()
     L.check(getattr(L.lib(), f"strix_linear_{_fam(w.bits)}_experts_gather_grouped")(
         _p(x), C.byref(v), E, _p(ws), ws.numel() * 4, M, A, _p(y),
-                                                           _act(x), MOE_MATH_WMMA_F16, _stream()))
+                                                           _act(x), math, _stream()))
     return y
 
 

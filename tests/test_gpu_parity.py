@@ -197,9 +197,9 @@ def test_grouped_gate_up_swiglu_and_down(bits, M, A, E, H, I):
     b, q, s, m, G = qspec(gu)
     href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G), E, ids)
     assert rel_err(to_np(h), href) < 1e-2
-    # Q4 at prefill sizes runs the reference's F16 math (x and the weights rounded to F16): equal to its model up to
-    # FP32 summation order and the bf16 rounding of h
-    f16 = bits == 4 and _expert_gemm_size(M * A, E)
+    # Q4 under the F16 kinds (the default) runs the reference's F16 math at every batch size (x and the weights
+    # rounded to F16): equal to its model up to FP32 summation order and the bf16 rounding of h
+    f16 = bits == 4
     if f16:
         h16 = orc.experts_gate_up_swiglu_f16math(x, b, q, s, m, gu.N, H, G, E, ids)
         assert rel_err(to_np(h), h16) < 2.0 ** -8
@@ -232,11 +232,13 @@ def test_grouped_gate_up_swiglu_and_down(bits, M, A, E, H, I):
         assert rel_err(pt.cpu().numpy(), part) < 1e-4
     yref, _ = orc.combine(part, ids, coef, E, H)
     assert rel_err(to_np(y), yref) < 1e-2
-    # the f16-h form sums in another order: an output may round to the neighbouring bf16 (2^-8 of its magnitude); at
-    # prefill sizes it takes the exact weights with FP32 partials, y the F16 math with BF16 partials (one more rounding
-    # and the F16 weights' own)
+    # the f16-h form: under the F16 math its h holds the F16 operands the BF16 h converts to, so y is the same bits;
+    # Q8 (exact weights) sums in another order, so an output may round to the neighbouring bf16
     y2 = moe.experts_combine_grouped(hf, dn, E, tid, torch.from_numpy(coef).to(DEV), ws, M, A, h_f16=True)
-    assert rel_err(to_np(y2), to_np(y)) < (2.0 ** -6 if f16 else 2.0 ** -8)
+    if f16:
+        assert torch.equal(y2, y)
+    else:
+        assert rel_err(to_np(y2), to_np(y)) < 2.0 ** -8
 
 
 def test_grouped_gather_plain_q4():
@@ -246,11 +248,18 @@ def test_grouped_gather_plain_q4():
     x = orc.gen_bf16_normal(orc.tensor_key(3, "x"), 1.0, (M, H))
     ids = np.random.default_rng(1).integers(0, E, (M, A)).astype(np.int32)
     ws, _ = moe.moe_group_routes(torch.from_numpy(ids).to(DEV), E)
-    y = to_np(moe.experts_gather_grouped(bf16(x), gu, E, ws, M, A))
     w = orc.dequantize(4, *qspec(gu)[1:4], gu.N, H, gu.G).astype(np.float64)
     xf = orc.bf16_to_f32(x).astype(np.float64)
     N = 2 * I
     ref = np.stack([w[ids.ravel()[s] * N:(ids.ravel()[s] + 1) * N] @ xf[s // A] for s in range(M * A)])
+    # exact weights: FP32 sums rounded once to bf16
+    yx = to_np(moe.experts_gather_grouped(bf16(x), gu, E, ws, M, A, math=moe.MOE_MATH_WMMA_BF16))
+    assert rel_err(yx, ref) < 2.0 ** -8
+    # the F16 kinds: the F16 math's outputs rounded once to bf16, against its model up to FP32 summation order
+    y = to_np(moe.experts_gather_grouped(bf16(x), gu, E, ws, M, A))
+    b, q, s, m, G = qspec(gu)
+    y16 = orc.f32_to_bf16(orc.experts_gather_f16math(x, b, q, s, m, gu.N, H, G, E, ids))
+    assert rel_err(y, y16) <= 2.0 ** -8 and np.mean(y == y16) > 0.99
     assert rel_err(y, ref) < 1e-2
 
 
@@ -329,14 +338,16 @@ def test_perslot_kernels_match_grouped():
     href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G), E, ids)
     assert rel_err(to_np(h), href) < 1e-2
     ws, _ = moe.moe_group_routes(tid, E)
-    hg = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)
-    assert torch.equal(h, hg)  # same per-slot MFMA sequence, so the same bits
+    # the exact-weight kinds: the same per-slot MFMA sequence as the per-slot kernels, so the same bits
+    ex = moe.MOE_MATH_WMMA_BF16
+    hg = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A, math=ex)
+    assert torch.equal(h, hg)
     g = moe.experts_gather(bf16(x), gu, E, tid, err)
-    gg = moe.experts_gather_grouped(bf16(x), gu, E, ws, M, A)
+    gg = moe.experts_gather_grouped(bf16(x), gu, E, ws, M, A, math=ex)
     assert torch.equal(g, gg)
     coef = torch.from_numpy(np.random.default_rng(3).random((M, A)).astype(np.float32)).to(DEV)
     y = moe.experts_combine(h, dn, E, tid, coef, err)
-    yg = moe.experts_combine_grouped(h, dn, E, tid, coef, ws, M, A)
+    yg = moe.experts_combine_grouped(h, dn, E, tid, coef, ws, M, A, math=ex)
     assert torch.equal(y, yg)  # per-slot dots summed over a in order: the same arithmetic
     assert to_np(err)[0] == 0
     bad = tid.clone()
@@ -359,7 +370,8 @@ def test_decode_kernels_match_perslot(M, A, E):
     tid = torch.from_numpy(ids).to(DEV)
     err = moe.zero_err()
     ws, _ = moe.moe_group_routes(tid, E)
-    hg = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)
+    ex = moe.MOE_MATH_WMMA_BF16  # the exact-weight kinds take the decode kernels
+    hg = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A, math=ex)
     hp = moe.experts_gather(bf16(x), gu, E, tid, err, swiglu=True)
     # the decode gate_up splits K over a block's waves and adds their FP32 parts in K order; the per-slot kernel sums
     # over all of K in one wave: an h may round to the neighbouring bf16
@@ -370,7 +382,7 @@ def test_decode_kernels_match_perslot(M, A, E):
     assert rel_err(to_np(hg), href) < 1e-2
     coef = torch.from_numpy(np.random.default_rng(7).random((M, A)).astype(np.float32)).to(DEV)
     pt = torch.empty((M * A, H), dtype=torch.float32, device=DEV)
-    yg = moe.experts_combine_grouped(hg, dn, E, tid, coef, ws, M, A, partial=pt)
+    yg = moe.experts_combine_grouped(hg, dn, E, tid, coef, ws, M, A, partial=pt, math=ex)
     b, q, s, m, G = qspec(dn)
     part = orc.experts_down(to_np(hg), orc.qview(b, q, s, m, dn.N, I, G), E, ids)
     assert rel_err(pt.cpu().numpy(), part) < 1e-4
@@ -809,7 +821,9 @@ def test_layer_stacked_shared_nonfinite_gate():
 def test_grouped_small_groups(bits, G, M, A, E, H, I):
     """G = 64 is the converter's default Q4 layout (strixite formats/convert_qwen4exp.hpp:37, default=q4g64). With G
     below the load's span the K step is one group; decode (M 16: the stream kernels) and prefill sizes (M 300: the
-    exact-weight GEMM at G 64, the stream kernels at G 32): h and the FP32 down partials against the oracle."""
+    exact-weight GEMM at G 64, the stream kernels at G 32) under the exact kinds: h and the FP32 down partials against
+    the oracle; Q4 under the F16 kinds (a group a chunk at G 64, a group a lane half at G 32): h and the BF16 partials
+    against the F16 math's model."""
     say("small groups", bits, G, M, A, E, H, I)
     gu = moe.QWeight.synth(bits, 17, "gu_q", "gu_s", 0, E * 2 * I, H, G)
     dn = moe.QWeight.synth(bits, 17, "dn_q", "dn_s", 0, E * H, I, G)
@@ -817,13 +831,25 @@ def test_grouped_small_groups(bits, G, M, A, E, H, I):
     ids = np.stack([np.random.default_rng(300 + m).permutation(E)[:A] for m in range(M)]).astype(np.int32)
     tid = torch.from_numpy(ids).to(DEV)
     ws, _ = moe.moe_group_routes(tid, E)
-    h = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)
+    ex = moe.MOE_MATH_WMMA_BF16
+    h = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A, math=ex)
     b, q, s, m, G_ = qspec(gu)
     href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G_), E, ids)
     assert G_ == G and rel_err(to_np(h), href) < 1e-2
+    if bits == 4:
+        h16 = moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A)
+        m16 = orc.experts_gate_up_swiglu_f16math(x, b, q, s, m, gu.N, H, G, E, ids)
+        assert rel_err(to_np(h16), m16) < 2.0 ** -8
     coef = torch.from_numpy(np.random.default_rng(6).random((M, A)).astype(np.float32)).to(DEV)
+    if bits == 4:
+        p16 = torch.empty((M * A, H), dtype=torch.float32, device=DEV)
+        moe.experts_combine_grouped(h, dn, E, tid, coef, ws, M, A, partial=p16)
+        bd, qd, sd, md, _ = qspec(dn)
+        pm = orc.f32_to_bf16(orc.experts_down_f16math(to_np(h), bd, qd, sd, md, dn.N, I, G, E, ids))
+        pb = _bf16_partials(p16)
+        assert rel_err(pb, pm) <= 2.0 ** -8 and np.mean(pb == pm) > 0.99
     pt = torch.empty((M * A, H), dtype=torch.float32, device=DEV)
-    y = moe.experts_combine_grouped(h, dn, E, tid, coef, ws, M, A, partial=pt)
+    y = moe.experts_combine_grouped(h, dn, E, tid, coef, ws, M, A, partial=pt, math=ex)
     b, q, s, m, _ = qspec(dn)
     part = orc.experts_down(to_np(h), orc.qview(b, q, s, m, dn.N, I, G), E, ids)
     assert rel_err(pt.cpu().numpy(), part) < 1e-4

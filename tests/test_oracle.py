@@ -376,3 +376,28 @@ def test_experts_f16math_against_exact_weights(orc):
     xs = orc.bf16_to_f16_rtz(h[sl]).astype(np.float64)
     w16 = orc.q4_weights_f16(q, s, m, E * H, I, G)[e * H:(e + 1) * H].astype(np.float64)
     assert np.allclose(p16[sl], [sum(xs[kk] * w16[n, kk] for kk in range(I)) for n in range(H)], rtol=1e-6, atol=1e-6)
+
+
+def test_experts_gather_f16math_brute_force(orc):
+    """The plain gather's F16 model at G 32 (a group every 32 k): each output the float64 sum of F16 x (toward zero)
+    times the F16 weight code * f16(s) + f16(m) of that k's group, built here from the nibbles by hand; a weight
+    taken from a neighbouring group, the wrong x row (slot instead of slot // A) or the high/low nibble swapped fails."""
+    N, K, G, E, A = 8, 64, 32, 2, 2
+    q, s, m = orc.gen_q(4, 71, 72, E * N, K, G)
+    x = orc.gen_bf16_normal(73, 1.0, (3, K))
+    ids = np.array([[1, 0], [0, 0], [1, 1]], np.int32)
+    got = orc.experts_gather_f16math(x, 4, q, s, m, E * N, K, G, E, ids)
+    xf = orc.bf16_to_f16_rtz(x).astype(np.float64)
+    sf = orc.bf16_to_f32(s).astype(np.float16).astype(np.float64).reshape(E * N, K // G)
+    mf = orc.bf16_to_f32(m).astype(np.float16).astype(np.float64).reshape(E * N, K // G)
+    qb = np.asarray(q, np.uint8).reshape(E * N, K // 2)
+    for slot in range(ids.size):
+        e, row = ids.ravel()[slot], slot // A
+        for n in range(N):
+            r = e * N + n
+            acc = 0.0
+            for k in range(K):
+                code = (qb[r, k // 2] >> (4 * (k % 2))) & 0xF
+                w = np.float64(np.float16(code * sf[r, k // G] + mf[r, k // G]))
+                acc += xf[row, k] * w
+            assert abs(got[slot, n] - acc) <= 1e-6 * max(1.0, abs(acc)), (slot, n)
