@@ -241,6 +241,9 @@ int strix_strixw_moe_layer(void *dev, const char *prefix, int64_t top_k, strix_m
  * Asynchronous on stream; out: one float of device scratch. */
 int64_t strix_calib_mfma_peak(int64_t blocks, int iters, float *out, void *stream);
 int strix_calib_read_peak(const void *p, int64_t bytes, int64_t blocks, float *out, void *stream);
+/* The FP32 -> BF16 rounding every kernel of this library stores with (no reference counterpart; the tests pin it
+ * against the reference's integer RNE, strixite common/bf16.hpp:19-26): y[i] = bf16(x[i]), n elements. */
+int strix_calib_bf16_round(const float *x, uint16_t *y, int64_t n, void *stream);
 
 /* Seeded synthetic tensors on the device (no reference counterpart: the bench's input generator). Element i of a
  * tensor is a function of (key, i) only; key = strix_synth_tensor_key(seed, tensor id, layer). */

@@ -93,6 +93,7 @@ _SIGS = {
     "strix_moe_layer_context_destroy": (_int, [_p]),
     "strix_calib_mfma_peak": (_i64, [_i64, _int, _p, _p]),
     "strix_calib_read_peak": (_int, [_p, _i64, _i64, _p, _p]),
+    "strix_calib_bf16_round": (_int, [_p, _p, _i64, _p]),
     "strix_moe_layer_noalloc_max_bytes": (_i64, []),
     "strix_moe_layer_forward_noalloc": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "strix_moe_layer_forward": (_int, [C.POINTER(LayerWeights), _p, _i64, _p, _p, _p, _p, _p, _p, _sz, _p, _p, _p,

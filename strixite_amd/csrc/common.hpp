@@ -80,12 +80,15 @@ namespace dev {
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-// RNE, NaN kept quiet (strixite common/bf16.hpp:19-26).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0x007fffffu) ? 0x0040u : 0u));
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+// RNE, NaN kept quiet (strixite common/bf16.hpp:19-26): gfx950's v_cvt_pk_bf16_f32, which gives the bits of the
+// integer form (u + 0x7fff + lsb) >> 16 for every finite or infinite input and the quieted top half of a NaN (checked
+// on the device against that form through strix_calib_bf16_round), in one instruction for two values.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+// two values in one dword (a low, b high)
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2v{a, b}), bf16x2v));
 }
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 __device__ __forceinline__ float qnan() { return __uint_as_float(0x7fc00000u); }

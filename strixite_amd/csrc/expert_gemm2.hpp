@@ -104,8 +104,8 @@ __global__ void __launch_bounds__(256) bf16_to_f16_paired_kernel(const uint4 *x,
 
 template <int EPI, bool XROW_DIV, int HF, int XF, int GS>
 __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-    expert_gemm2_kernel(GemmArgs a, int64_t tiles_bound, int64_t col_blocks, int64_t rec64, uint32_t q_bytes,
-                        uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
+    expert_gemm2_kernel(GemmArgs a, int64_t pairs_bound, int64_t col_blocks, int64_t pair_at, int64_t npairs_at,
+                        uint32_t q_bytes, uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
     using namespace g2;
     constexpr bool SWI = EPI == EPI_SWIGLU, X16 = XF == X_F16P;
     static_assert(GS == 32 || GS == 64 || GS == 128, "group sizes 32, 64, 128");
@@ -119,25 +119,18 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     const int tid = threadIdx.x, lane = tid % kWave, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int h = lane / 32, l32 = lane % 32;
 
-    // the item: blocks are dealt to the 8 XCDs round-robin (block b to XCD b % 8). XCD x takes records x, x + 8, ..
-    // in turn and the column blocks of each consecutively, so the column blocks of one token tile run together on
-    // one XCD and read its activations through the same L2, while consecutive records (one expert's tiles) spread
-    // over the XCDs. A block takes two 64-slot records of one bucket (the even-indexed one).
-    const int64_t j = blockIdx.x / 8, rec = 8 * (j / col_blocks) + blockIdx.x % 8, cb = j % col_blocks;
-    if (rec >= tiles_bound) return;
-    const int64_t n64 = a.ws[3] < tiles_bound ? a.ws[3] : tiles_bound;
-    if (rec >= n64) return;  // uniform per block, before any barrier
-    const int4 r0 = *reinterpret_cast<const int4 *>(a.ws + rec64 + 4 * rec);
-    const int32_t bucket = __builtin_amdgcn_readfirstlane(r0.x), start = __builtin_amdgcn_readfirstlane(r0.y);
+    // the item: blocks are dealt to the 8 XCDs round-robin (block b to XCD b % 8). XCD x takes pairs x, x + 8, .. in
+    // turn and the column blocks of each consecutively, so the column blocks of one token tile run together on one
+    // XCD and read its activations through the same L2. The pairs (up to 128 slots of one bucket) come in the order
+    // the packing wrote: most 32-slot sub-tiles first, so the longest blocks start first and the short ones fill the
+    // end of the launch.
+    const int64_t j = blockIdx.x / 8, pi = 8 * (j / col_blocks) + blockIdx.x % 8, cb = j % col_blocks;
+    if (pi >= pairs_bound) return;
+    if (pi >= a.ws[npairs_at]) return;  // uniform per block, before any barrier
+    const int4 pr = *reinterpret_cast<const int4 *>(a.ws + pair_at + 4 * pi);
+    const int32_t bucket = __builtin_amdgcn_readfirstlane(pr.x), start = __builtin_amdgcn_readfirstlane(pr.y);
+    const int32_t rows = __builtin_amdgcn_readfirstlane(pr.z);
     const bool nan = bucket < 0 || bucket >= a.E;
-    const int32_t first = a.ws[4 + (bucket < 0 ? 0 : bucket > a.E ? a.E : bucket)];  // offsets[bucket] (header: 4)
-    if (((start - first) / 64) % 2 != 0) return;  // the previous record's block covers this one
-    int32_t rows = r0.z;
-    if (rec + 1 < n64) {
-        const int4 r1 = *reinterpret_cast<const int4 *>(a.ws + rec64 + 4 * (rec + 1));
-        if (r1.x == bucket) rows += r1.z;
-    }
-    rows = __builtin_amdgcn_readfirstlane(rows);
     const uint32_t expert = nan ? 0u : (uint32_t)bucket;
     const int32_t *slots = a.ws + route::slots_at(a.E) + start;
     if (tid < BM) orow[tid] = tid < rows ? slots[tid] : -1;
@@ -306,13 +299,23 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
             // 256 v + 64 w, v = 0..3, one a group of 8 rows), then stores 16 bytes a lane, 8 lanes a row
             uint16_t *st = reinterpret_cast<uint16_t *>(abuf(X16 ? chunks % 3 : chunks & 1));
             auto sidx = [&](int r, int c) { return ((r >> 3) * 256 + 64 * wave) * 8 + (r & 7) * 64 + c; };
+            // column pairs as dwords: lanes 2 j and 2 j + 1 (columns c, c + 1) swap one of the two token rows they
+            // hold, so the even lane packs row r's (c, c + 1) and the odd lane row r + 1's
+            const bool odd = l32 & 1;
 #pragma unroll
             for (int i = 0; i < NT; ++i) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
+                for (int r = 0; r < 16; r += 2)
 #pragma unroll
-                    for (int t = 0; t < 2; ++t)
-                        st[sidx(8 * (r / 4) + 4 * h + r % 4, 32 * t + l32)] = f32_to_bf16(nan ? qnan() : acc[i][t][r]);
+                    for (int t = 0; t < 2; ++t) {
+                        const float v0 = nan ? qnan() : acc[i][t][r], v1 = nan ? qnan() : acc[i][t][r + 1];
+                        const float give = odd ? v0 : v1;
+                        const float got = __int_as_float(
+                            __builtin_amdgcn_mov_dpp(__float_as_int(give), 0xB1, 0xF, 0xF, true));  // lane ^ 1
+                        const uint32_t pk = odd ? f32x2_to_bf16x2(got, v1) : f32x2_to_bf16x2(v0, got);
+                        const int row = 8 * (r / 4) + 4 * h + r % 4 + (odd ? 1 : 0);
+                        *reinterpret_cast<uint32_t *>(st + sidx(row, 32 * t + (l32 & ~1))) = pk;
+                    }
                 __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -383,18 +386,19 @@ template <int EPI, bool XROW_DIV, int HF, int XF>
 bool launch_expert_gemm2(const GemmArgs &a, hipStream_t stream) {
     using namespace g2;
     if (!expert_gemm2_fits<EPI>(a)) return false;
-    const int64_t tiles_bound = std::min(a.S, a.S / 64 + a.E + 2);
+    const route::Layout L = route::layout(a.S, 1, a.E);
+    const int64_t pairs_bound = std::min(L.T64, a.S / route::kPairRows + a.E + 2);
     const int64_t col_blocks = EPI == EPI_SWIGLU ? (a.N / 2 + BN / 2 - 1) / (BN / 2) : (a.N + BN - 1) / BN;
     const int64_t q_bytes = a.N * a.E * a.K / 2, s_bytes = a.N * a.E * (a.K / a.G) * 2;
     const int64_t x_bytes = (XROW_DIV ? a.S / a.A : a.S) * a.K * 2;
     const int64_t y_bytes = a.S * a.ldy * (EPI == EPI_F32 ? 4 : 2);
     if (q_bytes >= (1ll << 31) || s_bytes >= (1ll << 31) || x_bytes >= (1ll << 31) || y_bytes >= (1ll << 31)) return false;
-    const int64_t blocks = (tiles_bound + 7) / 8 * 8 * col_blocks;  // whole rounds of the 8 XCDs
+    const int64_t blocks = (pairs_bound + 7) / 8 * 8 * col_blocks;  // whole rounds of the 8 XCDs
     if (blocks >= (1ll << 31)) return false;
     auto go = [&](auto gs) {
         expert_gemm2_kernel<EPI, XROW_DIV, HF, XF, decltype(gs)::value><<<(unsigned)blocks, g2::kThreads, 0, stream>>>(
-            a, tiles_bound, col_blocks, t64_rec_at(a.S, a.E), (uint32_t)q_bytes, (uint32_t)s_bytes, (uint32_t)x_bytes,
-            (uint32_t)y_bytes);
+            a, pairs_bound, col_blocks, L.pair_rec(), L.npairs(), (uint32_t)q_bytes, (uint32_t)s_bytes,
+            (uint32_t)x_bytes, (uint32_t)y_bytes);
     };
     switch (a.G) {
         case 32: go(std::integral_constant<int, 32>{}); break;

@@ -59,7 +59,7 @@ __global__ void __launch_bounds__(kRangeChunks * kWave) route_hist_kernel(const 
 }
 
 __global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, Layout L, int32_t *ws, uint32_t *err) {
-    __shared__ int wsum[99];
+    __shared__ int wsum[scan_lds_ints(7)];
     __shared__ int bad_lds;
     const int E = (int)L.E, t = threadIdx.x;
     const int64_t R = L.nrange();
@@ -79,12 +79,17 @@ __global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, La
 #pragma unroll
             for (int b = 0; b < B; ++b) cnt += h[b];
         }
-    int v[3] = {cnt, (cnt + kTileRows - 1) / kTileRows, (cnt + kWideRows - 1) / kWideRows}, tot[3];
-    block_scan3(v, wsum, tot);
+    int v[7], tot[7];
+    bucket_scan_values(cnt, v);
+    block_scan<7>(v, wsum, tot);
     if (t <= E) {
+        int pos_full, pos_part;
+        pair_starts(v, tot, pos_full, pos_part, cnt);
         ws[L.offsets() + t] = v[0];
         ws[L.tstart() + t] = v[1];
         ws[L.tstart() + (E + 2) + t] = v[2];
+        ws[L.pstart() + t] = pos_full;
+        ws[L.pstart() + (E + 2) + t] = pos_part;
         int run = v[0];
         for (int64_t r0 = 0; r0 < R; r0 += B) {
             int h[B];
@@ -102,6 +107,7 @@ __global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, La
         write_header(ws, L, tot);
         ws[L.tstart() + E + 1] = tot[1];
         ws[L.tstart() + (E + 2) + E + 1] = tot[2];
+        ws[L.npairs()] = tot[3] + tot[4] + tot[5] + tot[6];
         report_bad(ids, bad_lds, err);
     }
 }
@@ -123,7 +129,8 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave) route_place_kernel(con
 
 // The tile records, after placement, a thread per (16-slot tile, entry) and per 64-slot tile: a tile's bucket is the
 // last whose first tile is at or before it (binary search over the buckets' first tiles, staged in LDS; empty buckets
-// share their successor's first tile and are passed over).
+// share their successor's first tile and are passed over). The thread of a bucket's even 64-slot tile 2 q also writes
+// pair q's record at its place in the pair order.
 __global__ void __launch_bounds__(256) route_tiles_kernel(Layout L, int32_t *ws) {
     extern __shared__ int tl[];  // [3][E + 2]: first 16-slot tiles, first 64-slot tiles, bucket offsets
     const int nb = (int)L.E + 2;
@@ -155,9 +162,15 @@ __global__ void __launch_bounds__(256) route_tiles_kernel(Layout L, int32_t *ws)
     }
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n64; i += stride) {
         const int ti = (int)i, b = bucket_of_tile(tl + nb, ti), r = ti - tl[nb + b];
-        const int first = tl[2 * nb + b] + r * kWideRows;
+        const int first = tl[2 * nb + b] + r * kWideRows, c = tl[2 * nb + b + 1] - tl[2 * nb + b];
         *reinterpret_cast<int4 *>(ws + L.t64_rec() + 4 * ti) =
             make_int4(b, first, min(kWideRows, tl[2 * nb + b + 1] - first), 0);
+        if (r % 2 == 0) {
+            const int q = r / 2;
+            const int pos = pair_pos(q, c, ws[L.pstart() + b], ws[L.pstart() + nb + b]);
+            *reinterpret_cast<int4 *>(ws + L.pair_rec() + 4 * pos) =
+                make_int4(b, first, min(kPairRows, c - q * kPairRows), 0);
+        }
     }
 }
 

@@ -26,14 +26,21 @@ struct Layout {
     // expert kernel needs about a tile in independent loads; 64-slot tiles {bucket, first index, rows, 0}
     __host__ __device__ int64_t t16_rec() const { return (slots() + S + 3) / 4 * 4; }
     __host__ __device__ int64_t t64_rec() const { return t16_rec() + kRec16 * T16; }
+    // 128-slot pairs (a bucket's 64-slot tiles 2 q and 2 q + 1) {bucket, first index, rows, 0}, the F16 GEMM's blocks,
+    // ordered by their 32-slot sub-tiles, most first (full pairs, then the buckets' last pairs by size): the longest
+    // blocks start first. At most one pair a 64-slot tile; then the pair count.
+    __host__ __device__ int64_t pair_rec() const { return t64_rec() + 4 * T64; }
+    __host__ __device__ int64_t npairs() const { return pair_rec() + 4 * T64; }
     // the large-S path: chunk positions within their range of kRangeChunks chunks [nch][E + 1], the ranges' bucket
     // counts and then their first positions [nrange][E + 1], each chunk's first invalid slot [nch]
-    __host__ __device__ int64_t hist() const { return t64_rec() + 4 * T64; }
+    __host__ __device__ int64_t hist() const { return npairs() + 1; }
     __host__ __device__ int64_t rsum() const { return hist() + nch * (E + 1); }
     __host__ __device__ int64_t bad() const { return rsum() + nrange() * (E + 1); }
     // each bucket's first 16-slot and 64-slot tile, with the totals at E + 1: [2][E + 2]
     __host__ __device__ int64_t tstart() const { return bad() + nch; }
-    __host__ __device__ int64_t ints() const { return tstart() + 2 * (E + 2); }
+    // each bucket's first full pair's position and its last (partial) pair's position in the pair order: [2][E + 2]
+    __host__ __device__ int64_t pstart() const { return tstart() + 2 * (E + 2); }
+    __host__ __device__ int64_t ints() const { return pstart() + 2 * (E + 2); }
     __host__ __device__ int64_t nrange() const { return (nch + kRangeChunks - 1) / kRangeChunks; }
     static constexpr int kRangeChunks = 16;  // chunks a histogram block (a wave each)
 };
@@ -47,6 +54,19 @@ inline Layout layout(int64_t M, int64_t A, int64_t E) {
 
 
 __device__ __forceinline__ int bucket_of(int32_t id, int E) { return (id < 0 || id >= E) ? E : id; }
+
+constexpr int kPairRows = 2 * kWideRows;  // slots a pair
+// a bucket of c slots: its pairs' counts by 32-slot sub-tiles, n[0] = 4 (the full ones and a last of > 96 slots),
+// n[1] = 3, n[2] = 2, n[3] = 1
+__host__ __device__ inline void pair_classes(int c, int (&n)[4]) {
+    const int rem = c % kPairRows, cls = (rem + 31) / 32;  // the last pair's sub-tiles (0: none)
+    n[0] = c / kPairRows + (cls == 4);
+    n[1] = cls == 3, n[2] = cls == 2, n[3] = cls == 1;
+}
+// pair q of a bucket of c slots whose full pairs start at pos_full and whose partial pair sits at pos_part
+__host__ __device__ inline int pair_pos(int q, int c, int pos_full, int pos_part) {
+    return (q < c / kPairRows || c % kPairRows > 96) ? pos_full + q : pos_part;
+}
 
 // Lanes of the wave whose (valid) bucket equals this lane's: a ballot per bucket bit.
 __device__ __forceinline__ uint64_t match_bucket(int b, bool valid, int nbits) {
@@ -110,35 +130,54 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
     return v;
 }
 
-// Exclusive scan of three ints over the threads of a block (at most 16 waves); totals returned through tot[3]. Each
-// wave scans in registers; wave 0 scans the waves' totals; two barriers.
-__device__ inline void block_scan3(int (&v)[3], int *wsum /* [2][16][3] LDS */, int (&tot)[3]) {
+// Exclusive scan of N ints over the threads of a block (at most 16 waves); totals returned through tot[N]. Each wave
+// scans in registers; wave 0 scans the waves' totals; two barriers. wsum: scan_lds_ints(N) ints of LDS.
+__host__ __device__ constexpr int scan_lds_ints(int N) { return 33 * N; }
+template <int N>
+__device__ inline void block_scan(int (&v)[N], int *wsum /* [16][N] totals, [16][N] prefixes, [N] */, int (&tot)[N]) {
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, nw = (int)(blockDim.x / kWave);
-    int inc[3];
+    int inc[N];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) inc[j] = wave_incl_scan(v[j]);
+    for (int j = 0; j < N; ++j) inc[j] = wave_incl_scan(v[j]);
     if (lane == kWave - 1)
 #pragma unroll
-        for (int j = 0; j < 3; ++j) wsum[wave * 3 + j] = inc[j];
+        for (int j = 0; j < N; ++j) wsum[wave * N + j] = inc[j];
     __syncthreads();
-    if (wave == 0) {  // lanes 0..nw-1: the waves' totals, scanned; exclusive prefixes and the totals to wsum[16..]
+    if (wave == 0) {  // lanes 0..nw-1: the waves' totals, scanned; exclusive prefixes and the totals after them
 #pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int t = lane < nw ? wsum[lane * 3 + j] : 0;
+        for (int j = 0; j < N; ++j) {
+            const int t = lane < nw ? wsum[lane * N + j] : 0;
             const int p = wave_incl_scan(t);
-            if (lane < nw) wsum[48 + lane * 3 + j] = p - t;
-            if (lane == kWave - 1) wsum[96 + j] = p;
+            if (lane < nw) wsum[16 * N + lane * N + j] = p - t;
+            if (lane == kWave - 1) wsum[32 * N + j] = p;
         }
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        v[j] = wsum[48 + wave * 3 + j] + inc[j] - v[j];
-        tot[j] = wsum[96 + j];
+    for (int j = 0; j < N; ++j) {
+        v[j] = wsum[16 * N + wave * N + j] + inc[j] - v[j];
+        tot[j] = wsum[32 * N + j];
     }
 }
 
-__device__ inline void write_header(int32_t *ws, const Layout &L, const int (&tot)[3]) {
+// The scan's 7 ints of a bucket of c slots (t <= E, else 0): slots, 16-slot tiles, 64-slot tiles, pairs by class
+__device__ inline void bucket_scan_values(int c, int (&v)[7]) {
+    int n[4];
+    pair_classes(c, n);
+    v[0] = c, v[1] = (c + kTileRows - 1) / kTileRows, v[2] = (c + kWideRows - 1) / kWideRows;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[3 + j] = n[j];
+}
+// After the scan: this bucket's full-pair and partial-pair positions (the classes one after another, 4 first)
+__device__ inline void pair_starts(const int (&v)[7], const int (&tot)[7], int &pos_full, int &pos_part, int c) {
+    int base[4] = {0, tot[3], tot[3] + tot[4], tot[3] + tot[4] + tot[5]};
+    int n[4];
+    pair_classes(c, n);
+    pos_full = base[0] + v[3];
+    pos_part = n[1] ? base[1] + v[4] : n[2] ? base[2] + v[5] : n[3] ? base[3] + v[6] : 0;
+}
+
+template <int N> __device__ inline void write_header(int32_t *ws, const Layout &L, const int (&tot)[N]) {
     ws[0] = tot[1];
     ws[1] = (int32_t)L.S;
     ws[2] = (int32_t)L.E;
@@ -181,10 +220,11 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
     int *bcount = btile + nb;                 // [E + 1]
     int *b64 = bcount + nb;                   // [E + 1] bucket's first 64-slot tile
     int *tile_b = b64 + nb;                   // [T16] bucket of a tile
-    int *wsum = tile_b + L.T16;               // [99]
-    int *bad = wsum + 99;                     // [1]
+    int *wsum = tile_b + L.T16;               // [scan_lds_ints(7)]
+    int *bad = wsum + scan_lds_ints(7);       // [1]
     // [16][kCandScratch] the waves' top-k candidates (8-byte aligned)
-    uint2 *cand = reinterpret_cast<uint2 *>(lds + ((3 * kFusedSlots + kSmallWaves * nb + 4 * nb + L.T16 + 100 + 1) & ~1));
+    uint2 *cand = reinterpret_cast<uint2 *>(
+        lds + ((3 * kFusedSlots + kSmallWaves * nb + 4 * nb + L.T16 + scan_lds_ints(7) + 1 + 1) & ~1));
     // only the waves that hold slots (chunks of 64) count: their counters are the only ones cleared and summed
     const int nw = (S + kWave - 1) / kWave;
     for (int i = t; i < nw * nb; i += nthr) cnt[i] = 0;
@@ -226,8 +266,11 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
     int c = 0;
     if (t <= E)
         for (int w = 0; w < nw; ++w) c += cnt[w * nb + t];
-    int v[3] = {c, (c + kTileRows - 1) / kTileRows, (c + kWideRows - 1) / kWideRows}, tot[3];
-    block_scan3(v, wsum, tot);
+    int v[7], tot[7];
+    bucket_scan_values(c, v);
+    block_scan<7>(v, wsum, tot);
+    int pos_full, pos_part;
+    pair_starts(v, tot, pos_full, pos_part, c);
     if (t <= E) {
         bstart[t] = v[0], btile[t] = v[1], bcount[t] = c, b64[t] = v[2];
         for (int i = 0; i < (c + kTileRows - 1) / kTileRows; ++i) tile_b[v[1] + i] = t;
@@ -252,6 +295,9 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
         for (int i = 0; i < n64; ++i)
             *reinterpret_cast<int4 *>(ws + L.t64_rec() + 4 * (b64[t] + i)) =
                 make_int4(t, bstart[t] + i * kWideRows, min(kWideRows, bcount[t] - i * kWideRows), 0);
+        for (int q = 0; q < (bcount[t] + kPairRows - 1) / kPairRows; ++q)
+            *reinterpret_cast<int4 *>(ws + L.pair_rec() + 4 * pair_pos(q, bcount[t], pos_full, pos_part)) =
+                make_int4(t, bstart[t] + q * kPairRows, min(kPairRows, bcount[t] - q * kPairRows), 0);
     }
     // 16-slot tile records {bucket, first, rows, 0, slot[16]}: a thread per (tile, slot entry)
     for (int i = t; i < tot[1] * kTileRows; i += nthr) {
@@ -263,6 +309,7 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
     }
     if (t == 0) {
         write_header(ws, L, tot);
+        ws[L.npairs()] = tot[3] + tot[4] + tot[5] + tot[6];
         report_bad(sids, *bad, err_route);  // the ids live in LDS here: report_bad reads them through this pointer
     }
 }
@@ -278,7 +325,7 @@ __device__ inline void topk_route_small_body(const float *logits, int64_t ld, in
 // LDS bytes pack_small_body needs
 inline size_t topk_route_small_lds(const Layout &L) {
     const size_t ints = ((size_t)3 * kFusedSlots + (size_t)kSmallWaves * (L.E + 1) + 4 * (size_t)(L.E + 1) +
-                         (size_t)L.T16 + 100 + 1) & ~(size_t)1;
+                         (size_t)L.T16 + scan_lds_ints(7) + 1 + 1) & ~(size_t)1;
     return ints * 4 + (size_t)kSmallWaves * topk::kCandScratch * 8;  // + the top-k candidates
 }
 // ballot bits a bucket index 0..E takes

@@ -147,6 +147,27 @@ def test_group_routes_bit_exact(M, A, E):
     assert int(t["S"]) == M * A and int(t["E"]) == E
     assert int(t["n_tiles"]) == int(sum((c + 15) // 16 for c in np.diff(off)))
     assert to_np(err)[0] == 0
+    _check_pairs(to_np(ws), M * A, E, off)
+
+
+def _check_pairs(w, S, E, off):
+    """The F16 GEMM's 128-slot pairs: every bucket's slots cut into pairs {bucket, first, rows} exactly once, listed
+    with their 32-slot sub-tile counts non-increasing. Offsets of the workspace layout (route_small.hpp Layout):
+    header 4, offsets E + 2, slots S, 16-slot records of 20 ints, 64-slot records of 4, then the pairs and their
+    count."""
+    t16 = min(S, S // 16 + E + 2)
+    t64 = min(S, S // 64 + E + 2)
+    t16_rec = (4 + E + 2 + S + 3) // 4 * 4
+    pair_rec = t16_rec + 20 * t16 + 4 * t64
+    n = int(w[pair_rec + 4 * t64])
+    cnt = np.diff(off)
+    want = {(b, int(off[b]) + 128 * q, int(min(128, cnt[b] - 128 * q))) for b in range(E + 1)
+            for q in range((int(cnt[b]) + 127) // 128)}
+    assert n == len(want)
+    recs = w[pair_rec:pair_rec + 4 * n].reshape(n, 4)
+    assert {tuple(int(v) for v in r[:3]) for r in recs} == want
+    subtiles = (recs[:, 2] + 31) // 32
+    assert np.all(np.diff(subtiles) <= 0)
 
 
 def test_group_routes_invalid_ids():
@@ -160,6 +181,7 @@ def test_group_routes_invalid_ids():
         t = moe.route_tables(ws, M, A, E)
         assert np.array_equal(to_np(t["offsets"]), off) and np.array_equal(to_np(t["slots"]), slots)
         assert np.array_equal(to_np(err).view(np.uint32), rerr)  # the first invalid slot in slot order
+        _check_pairs(to_np(ws), M * A, E, off)
         with pytest.raises(moe.StrixError, match="out of range"):
             moe.check_expert_error(err)
 
