@@ -69,16 +69,14 @@ __device__ __forceinline__ float lane_chain(const uint4 (&xr)[NCH], const uint4 
     return acc;
 }
 
-// The approximate logits as pass 1 left them: `parts` K parts (summed here), part p of token m at a[p part_stride +
-// m ld]; the squared router-row norms likewise in parts of N floats.
+// The approximate logits as pass 1 left them: token m's at a[m ld + e].
 struct ApproxIn {
     const float *a;
-    int64_t ld, part_stride;
-    int parts;
+    int64_t ld;
 };
 
 // One wave per token. The exact values are written into the layer's logits row (ld); nw2: the squared norms of the
-// router rows in the approximate pass's parts.
+// router rows.
 template <int NV, int NCH>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     router_select_kernel(const uint16_t *x, const uint16_t *w, const float *bias, float *logits, int64_t ld,
@@ -90,7 +88,6 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     const int64_t m = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
     if (m >= M) return;  // whole wave; no barrier in this kernel
     constexpr int64_t K = (int64_t)NCH * 512;
-    const int64_t N = E;  // rows of the approximate pass (the routed ones)
     const uint16_t *xm = x + m * K;
     float *row = logits + m * ld;
     uint4 xr[NCH];
@@ -115,16 +112,19 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
     for (int s = 1; s < kWave; s *= 2) q += __shfl_xor(q, s, kWave);
     constexpr float up = 1.0f + 1.0f / 256;  // the FP32 sums of squares are within 2^-10 of the exact ones
     const float nxm = sqrtf(q) * up;
-    float va[NV], dl[NV];
+    float va[NV], dl[NV], av[NV], n2v[NV], bv[NV];
     bool fin = isfinite(nxm);
+    // every lane's approximate values, norms and biases loaded together (clamped indices: one round trip)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int e = lane + j * kWave, ec = e < E ? e : E - 1;
+        av[j] = ap.a[m * ap.ld + ec], n2v[j] = nw2[ec], bv[j] = bias ? bias[ec] : 0.f;
+    }
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int e = lane + j * kWave;
-        float a = 0.f, n2 = 0.f;
-        if (e < E)
-#pragma unroll
-            for (int p = 0; p < ap.parts; ++p) a += ap.a[p * ap.part_stride + m * ap.ld + e], n2 += nw2[p * N + e];
-        const float b = e < E && bias ? bias[e] : 0.f, n = sqrtf(n2) * up;
+        const float a = e < E ? av[j] : 0.f, n2 = e < E ? n2v[j] : 0.f;
+        const float b = e < E ? bv[j] : 0.f, n = sqrtf(n2) * up;
         va[j] = bias ? a + b : a;
         fin = fin && isfinite(va[j]) && isfinite(n);
         // delta' = (4K + 64) u |x| |w| + K 2^-124 + 2^-22 (|a| + |b|), rounded up by the 1 + 2^-10 factor
@@ -242,7 +242,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 // The approximate logits are a plain bf16 GEMM (any FP32 summation order is within the bound above), so at prefill
 // sizes they come from the library GEMM: C [M, N] (ld N) = x [M, K] w [N, K]^T, FP32 accumulation. Column-major in
 // hipBLASLt's terms: C^T (N x M) = op_T(w as K x N) * (x as K x M). The handle lives per device and the chosen
-// algorithm per shape (no workspace); a shape the library declines returns false and pass 1 runs on the kernel above.
+// algorithm per shape (no workspace); a shape the library declines returns false (the caller then routes through the
+// canonical-order projection and top-k).
 struct BltShape {
     int device;
     int64_t M, N, K;
@@ -365,7 +366,7 @@ void moe_router_prefill_select(const void *x, const uint16_t *w, const float *bi
                                int64_t k, bool shared, float *logits, float *norms, int32_t *ids, float *coef,
                                uint32_t *err, hipStream_t stream, bool shared_slot, void *x16) {
     const int64_t nch = H / 512, ld = E + (shared ? 1 : 0);
-    const ApproxIn ap{logits + M * ld, E, 0, 1};
+    const ApproxIn ap{logits + M * ld, E};
     const float *nw = norms + M;  // (the first M floats: unused)
     const unsigned g2 = (unsigned)((M + 3) / 4);
     const int nv = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
