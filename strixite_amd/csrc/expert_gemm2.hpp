@@ -108,6 +108,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                         uint32_t q_bytes, uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
     using namespace g2;
     constexpr bool SWI = EPI == EPI_SWIGLU, X16 = XF == X_F16P;
+    static_assert(SWI || EPI == EPI_BF16, "SwiGLU h or BF16 outputs");
     static_assert(GS == 32 || GS == 64 || GS == 128, "group sizes 32, 64, 128");
     constexpr int CPG = GS > BK ? GS / BK : 1;  // chunks that start with a new scale and min
     // the activation buffers [row * 8 + (col ^ (row & 7))], separate arrays picked at compile time: the compiler
@@ -334,38 +335,42 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
             }
             return;
         }
+        if constexpr (SWI) {
+            // h column pairs as dwords: the lane of the pair's lower column packs token row r, its partner (column
+            // + PX, lane l32 ^ PX) row r + 1. PX 1 in natural order; 4 in the paired order, where columns c and c + 4
+            // of an 8-column block sit side by side. (N / 2 is a multiple of 32, so a pair is live or dead whole.)
+            constexpr int PX = HF == H_F16P ? 4 : 1;
+            const bool upper = (l32 & PX) != 0;
+            const uint32_t pc = (uint32_t)(col0[0] + (l32 & ~PX));  // the pair's lower column
+            const uint32_t dpos = HF == H_F16P ? (pc & ~7u) + 2 * (pc & 3u) : pc;
+            const bool live_col = pc < (uint32_t)nrows;
+            auto swap = [&](float v) __attribute__((always_inline)) {
+                if constexpr (PX == 1)
+                    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+                else
+                    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));  // lane ^ 4
+            };
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
+            for (int i = 0; i < NT; ++i) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int tok = 32 * i + 8 * (r / 4) + 4 * h + r % 4;
-                const int32_t orw = orow[tok];
-                if constexpr (SWI) {
-                    const int64_t col = col0[0] + l32;
-                    const bool live = orw >= 0 && col < nrows;
+                for (int r = 0; r < 16; r += 2) {
                     // silu with the hardware exp and reciprocal (a few FP32 ulps; h is rounded to 16 bits)
-                    const float g = acc[i][0][r];
-                    const float v = nan ? qnan() : g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * acc[i][1][r];
-                    // F16 forms: the BF16-rounded h toward zero (what a BF16 h converts to on the way into the down)
-                    const uint16_t bits = HF == H_BF16 ? f32_to_bf16(v) : (uint16_t)pk_f16_rtz(bf16_round(v), 0.0f);
-                    const uint32_t cs =
-                        HF == H_F16P ? (uint32_t)((col & ~7) + paired_pos((int)(col & 7))) : (uint32_t)col;
-                    __builtin_amdgcn_raw_buffer_store_b16(
-                        bits, ry, live ? ((uint32_t)orw * (uint32_t)a.ldy + cs) * 2 : y_bytes, 0, 0);
-                } else {
+                    float v[2];
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const int64_t col = col0[t] + l32;
-                        const bool live = orw >= 0 && col < nrows;
-                        const float v = nan ? qnan() : acc[i][t][r];
-                        const uint32_t e = (uint32_t)orw * (uint32_t)a.ldy + (uint32_t)col;
-                        if constexpr (EPI == EPI_F32)
-                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, live ? e * 4 : y_bytes, 0, 0);
-                        else
-                            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), ry, live ? e * 2 : y_bytes, 0, 0);
+                    for (int e = 0; e < 2; ++e) {
+                        const float g = acc[i][0][r + e];
+                        v[e] = nan ? qnan() : g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * acc[i][1][r + e];
                     }
+                    const float got = swap(upper ? v[0] : v[1]);
+                    const float lo = upper ? got : v[0], hi = upper ? v[1] : got;
+                    // F16 forms: the BF16-rounded h toward zero (what a BF16 h converts to on the way into the down)
+                    const uint32_t bits = HF == H_BF16 ? f32x2_to_bf16x2(lo, hi) : pk_f16_rtz(bf16_round(lo), bf16_round(hi));
+                    const int32_t orw = orow[32 * i + 8 * (r / 4) + 4 * h + r % 4 + (upper ? 1 : 0)];
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        bits, ry, orw >= 0 && live_col ? ((uint32_t)orw * (uint32_t)a.ldy + dpos) * 2 : y_bytes, 0, 0);
                 }
             }
+            return;
         }
     };
     const int live_tiles = (rows + 31) / 32;
