@@ -2046,10 +2046,14 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         if (!q8 && decode_fits(a, M, true)) launch_decode_gate_up(a, M, &sh_jobs[0], stream);
         else if (q8) launch_gemm<8, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, A, Es), stream, &sh_jobs[0]);
         else launch_gemm<4, GROUPED, EPI_SWIGLU, false, true, false>(a, grouped_tiles(M, A, Es), stream, &sh_jobs[0]);
-    } else if (q8) {
-        linear_q8_experts_gather_grouped_swiglu(x, gu8, Es, route, L.route_bytes, M, A, h, Act::BF16, MoeMath::WmmaF16, stream, false);
     } else {
-        linear_q4_experts_gather_grouped_swiglu(x, w.gate_up, Es, route, L.route_bytes, M, A, h, Act::BF16, MoeMath::WmmaF16, stream, false);
+        // outside the F16 GEMM's sizes the layer keeps exact weights (the exact-weight kinds' kernels)
+        if (q8)
+            linear_q8_experts_gather_grouped_swiglu(x, gu8, Es, route, L.route_bytes, M, A, h, Act::BF16,
+                                                    MoeMath::WmmaBf16, stream, false);
+        else
+            linear_q4_experts_gather_grouped_swiglu(x, w.gate_up, Es, route, L.route_bytes, M, A, h, Act::BF16,
+                                                    MoeMath::WmmaBf16, stream, false);
     }
     {
         const QV dv = q8 ? qv(dn8) : qv(w.down);
