@@ -765,7 +765,7 @@ __global__ void __launch_bounds__(1024)
                              GemmArgs sa, int spp, int parts, float *part, int64_t units) {
     extern __shared__ int lds[];
     if (blockIdx.x == 0) {
-        route::topk_route_small_body<NV>(logits, ld, M, E, k, ids, coef, L, nbits, ws, err_router, err_route, lds);
+        route::topk_route_small_body<NV, false>(logits, ld, M, E, k, ids, coef, L, nbits, ws, err_router, err_route, lds);
         return;
     }
     // 4 units a block (its other waves exit): the units spread over many CUs
@@ -830,7 +830,7 @@ __global__ void __launch_bounds__(1024)
     if (!last) return;
     // the other blocks' logits after their tickets: the L2 invalidated (no stale line of them read back)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    route::topk_route_small_body<NV>(logits, ld, M, E, k, ids, coef, L, nbits, ws, err_router, err_route, lds);
+    route::topk_route_small_body<NV, false>(logits, ld, M, E, k, ids, coef, L, nbits, ws, err_router, err_route, lds);
 }
 
 // y[m, n] = sum_a coef[m, a] * partial[m * A + a, n] in slot order (fmaf), rounded once; NaN for a token with an

@@ -204,7 +204,9 @@ constexpr int kFusedSlots = 1024;
 // TOPK with shared_slot: each token's slot k is the shared expert (id E_top, coefficient sigmoid(its gate logit at
 // column E_top of the logits); a non-finite one is bad index E_top, strixite kernels/moe_router.hip:108-111), and the
 // packing runs over L.E = E_top + 1 experts. E: the packing's expert count (L.E).
-template <int NV, bool TOPK>
+// PAIRS: also the F16 GEMM's 128-slot pair table (the layer's own decode launches, whose routes no GEMM reads, skip it
+// and leave a pair count of 0).
+template <int NV, bool TOPK, bool PAIRS = true>
 __device__ inline void pack_small_body(const float *logits, int64_t ld, const int32_t *ids_in, int M, int E, int k,
                                        int32_t *ids_out, float *coef_out, Layout L, int nbits, int32_t *ws,
                                        uint32_t *err_router, uint32_t *err_route, int *lds, bool shared_slot = false) {
@@ -266,11 +268,14 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
     int c = 0;
     if (t <= E)
         for (int w = 0; w < nw; ++w) c += cnt[w * nb + t];
-    int v[7], tot[7];
-    bucket_scan_values(c, v);
-    block_scan<7>(v, wsum, tot);
-    int pos_full, pos_part;
-    pair_starts(v, tot, pos_full, pos_part, c);
+    constexpr int NSC = PAIRS ? 7 : 3;
+    int v7[7], v[NSC], tot[NSC];
+    bucket_scan_values(c, v7);
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) v[i] = v7[i];
+    block_scan<NSC>(v, wsum, tot);
+    int pos_full = 0, pos_part = 0;
+    if constexpr (PAIRS) pair_starts(v, tot, pos_full, pos_part, c);
     if (t <= E) {
         bstart[t] = v[0], btile[t] = v[1], bcount[t] = c, b64[t] = v[2];
         for (int i = 0; i < (c + kTileRows - 1) / kTileRows; ++i) tile_b[v[1] + i] = t;
@@ -295,9 +300,10 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
         for (int i = 0; i < n64; ++i)
             *reinterpret_cast<int4 *>(ws + L.t64_rec() + 4 * (b64[t] + i)) =
                 make_int4(t, bstart[t] + i * kWideRows, min(kWideRows, bcount[t] - i * kWideRows), 0);
-        for (int q = 0; q < (bcount[t] + kPairRows - 1) / kPairRows; ++q)
-            *reinterpret_cast<int4 *>(ws + L.pair_rec() + 4 * pair_pos(q, bcount[t], pos_full, pos_part)) =
-                make_int4(t, bstart[t] + q * kPairRows, min(kPairRows, bcount[t] - q * kPairRows), 0);
+        if constexpr (PAIRS)
+            for (int q = 0; q < (bcount[t] + kPairRows - 1) / kPairRows; ++q)
+                *reinterpret_cast<int4 *>(ws + L.pair_rec() + 4 * pair_pos(q, bcount[t], pos_full, pos_part)) =
+                    make_int4(t, bstart[t] + q * kPairRows, min(kPairRows, bcount[t] - q * kPairRows), 0);
     }
     // 16-slot tile records {bucket, first, rows, 0, slot[16]}: a thread per (tile, slot entry)
     for (int i = t; i < tot[1] * kTileRows; i += nthr) {
@@ -309,16 +315,17 @@ __device__ inline void pack_small_body(const float *logits, int64_t ld, const in
     }
     if (t == 0) {
         write_header(ws, L, tot);
-        ws[L.npairs()] = tot[3] + tot[4] + tot[5] + tot[6];
+        if constexpr (PAIRS) ws[L.npairs()] = tot[3] + tot[4] + tot[5] + tot[6];
+        else ws[L.npairs()] = 0;
         report_bad(sids, *bad, err_route);  // the ids live in LDS here: report_bad reads them through this pointer
     }
 }
 
-template <int NV>
+template <int NV, bool PAIRS = true>
 __device__ inline void topk_route_small_body(const float *logits, int64_t ld, int M, int E, int k, int32_t *ids_out,
                                              float *coef_out, Layout L, int nbits, int32_t *ws, uint32_t *err_router,
                                              uint32_t *err_route, int *lds, bool shared_slot = false) {
-    pack_small_body<NV, true>(logits, ld, nullptr, M, E, k, ids_out, coef_out, L, nbits, ws, err_router, err_route,
+    pack_small_body<NV, true, PAIRS>(logits, ld, nullptr, M, E, k, ids_out, coef_out, L, nbits, ws, err_router, err_route,
                               lds, shared_slot);
 }
 
