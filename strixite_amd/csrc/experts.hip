@@ -1937,21 +1937,23 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
     const bool approx_done = !logits_in && M >= 256 &&
                              moe_router_prefill_approx(x, w.router, M, H, E, k, w.has_shared || stacked, logits,
                                                        reinterpret_cast<float *>(base + L.norms), stream);
-    // with a context the shared expert runs on its helper stream; without one, on the caller's stream first
+    // with a context the shared expert runs on its helper stream, forked here; its launches are issued after the
+    // routed projections' (so a captured graph keeps the main chain on the caller's queue and its first-created
+    // branch, and only the shared expert's branch crosses queues); without a context, on the caller's stream first
     hipStream_t sh_stream = stream;
-    if (w.has_shared && !fold) {
+    if (w.has_shared && !fold && ctx != nullptr) {
+        int dev = 0;
+        STRIX_HIP_CHECK(hipGetDevice(&dev), fn, ": hipGetDevice");
+        STRIX_CHECK(dev == ctx->device, fn, ": the layer context belongs to device ", ctx->device,
+                    ", the current device is ", dev);
+        STRIX_HIP_CHECK(hipEventRecord(ctx->fork, stream), fn, ": fork");
+        sh_stream = ctx->s;
+    }
+    auto launch_shared = [&]() {
         const QV gv = qv(w.sh_gate_up), dv = qv(w.sh_down);
         check_view(fn, gv, 1);
         check_view(fn, dv, 1);
-        if (ctx != nullptr) {
-            int dev = 0;
-            STRIX_HIP_CHECK(hipGetDevice(&dev), fn, ": hipGetDevice");
-            STRIX_CHECK(dev == ctx->device, fn, ": the layer context belongs to device ", ctx->device,
-                        ", the current device is ", dev);
-            STRIX_HIP_CHECK(hipEventRecord(ctx->fork, stream), fn, ": fork");
-            STRIX_HIP_CHECK(hipStreamWaitEvent(ctx->s, ctx->fork, 0), fn, ": fork wait");
-            sh_stream = ctx->s;
-        }
+        if (ctx != nullptr) STRIX_HIP_CHECK(hipStreamWaitEvent(ctx->s, ctx->fork, 0), fn, ": fork wait");
         GemmArgs a = make_args(gv, 1, x, sh_h, I);
         a.M = M;
         GemmArgs b = make_args(dv, 1, sh_h, sh_s, H);
@@ -1965,7 +1967,8 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         }
         STRIX_HIP_CHECK_LAUNCH(fn, " shared expert M=", M);
         if (ctx != nullptr) STRIX_HIP_CHECK(hipEventRecord(ctx->join, ctx->s), fn, ": join");
-    }
+    };
+    if (w.has_shared && !fold && ctx == nullptr) launch_shared();
 
     const bool q8 = w.gate_up_bits == 8;
     // Q4 experts at prefill sizes run the reference's F16 math (MoeMath::WmmaF16): x converted to F16 once, h kept
@@ -2073,7 +2076,10 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
             launch_gemm<4, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, A, Es), stream, fold ? &sh_jobs[1] : nullptr);
         }
     }
-    if (ctx != nullptr && w.has_shared && !fold) STRIX_HIP_CHECK(hipStreamWaitEvent(stream, ctx->join, 0), fn, ": join wait");
+    if (ctx != nullptr && w.has_shared && !fold) {
+        launch_shared();
+        STRIX_HIP_CHECK(hipStreamWaitEvent(stream, ctx->join, 0), fn, ": join wait");
+    }
     const MoeSharedAdd sh{sh_s, lg + E, ld, (uint32_t)E, err_router};
     const InjectArgs inj = inject ? InjectArgs{static_cast<uint16_t *>(inject->xs), inject->w_in, inject->streams}
                                   : InjectArgs{};
