@@ -937,6 +937,16 @@ inline void launch_decode_gate_up(const GemmArgs &ga, int64_t M, const SharedJob
     }
 }
 
+// The LDS-ring down kernel at any token count (it reads h by slot and writes partials by slot; every tile needs one of
+// its waves): Q4 g128, K = 512
+inline bool down_stream_fits(const GemmArgs &ga) {
+    constexpr int kDnBlocksPerCu = 163840 / (gdn::kDnWaves * gdn::kDnStages * gdn::kPosU4 * 16);
+    return ga.G == dec::kSpan && ga.K == dec::kSpan * kDecDownSteps && ga.N % 32 == 0 &&
+           std::min(ga.S, ga.S / 16 + ga.E + 2) <= (int64_t)kDnBlocksPerCu * device_cus() * gdn::kDnWaves &&
+           ga.S * ga.K * 2 < (1ll << 31) && ga.S * ga.N * 4 < (1ll << 31) && ga.N * ga.E * ga.K / 2 < (1ll << 31) &&
+           ga.N * ga.E * (ga.K / ga.G) * 2 < (1ll << 31);
+}
+
 // down into FP32 partials; sh (optional): the shared expert's down parts riding along in leading blocks
 inline void launch_decode_down(const GemmArgs &ga, int64_t M, const SharedJob *sh, hipStream_t stream) {
     const DecodeArgs d = decode_args(ga, M, false);

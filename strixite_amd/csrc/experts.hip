@@ -1439,7 +1439,7 @@ void combine_grouped(const char *fn, const void *h, const V &wv, int64_t E, cons
     } else if (!h_f16 && use_expert_gemm(M * A, E, w.K, w.G)) {  // (the GEMM reads bf16 activations only)
         if (w.bits == 4) launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
         else launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
-    } else if (!h_f16 && w.bits == 4 && M <= dec::kMaxTokens && decode_fits(a, M, false)) {
+    } else if (!h_f16 && w.bits == 4 && ((M <= dec::kMaxTokens && decode_fits(a, M, false)) || down_stream_fits(a))) {
         launch_decode_down(a, M, nullptr, stream);
     } else if (h_f16) launch_bits<GROUPED, EPI_F32, true, false, false>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_F32, false, false, false>(w.bits, a, tiles, stream);
@@ -2068,7 +2068,7 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         } else if (use_expert_gemm(M * A, Es, dv.K, dv.G)) {
             if (q8) launch_expert_gemm<8, GROUPED, EPI_F32, false, false>(a, stream);
             else launch_expert_gemm<4, GROUPED, EPI_F32, false, false>(a, stream);
-        } else if (!q8 && M <= dec::kMaxTokens && decode_fits(a, M, false)) {
+        } else if (!q8 && ((M <= dec::kMaxTokens && decode_fits(a, M, false)) || (!fold && down_stream_fits(a)))) {
             launch_decode_down(a, M, fold ? &sh_jobs[1] : nullptr, stream);
         } else if (q8) {
             launch_gemm<8, GROUPED, EPI_F32, false, false, false>(a, grouped_tiles(M, A, Es), stream, fold ? &sh_jobs[1] : nullptr);
