@@ -407,7 +407,10 @@ constexpr int kGuMaxWaves = 12;  // K <= 3072 (LDS: rings, two unit reductions, 
 constexpr int kGuMaxBlockTiles = 32;  // tiles a block's unit range may touch (their slots live in LDS)
 }  // namespace gul
 
-template <int W, int SH>
+// GA (gathered activations, any token count): the MFMA's 16 A rows are the current tile's slots (x row slot / A, zeros
+// past the tile's rows) instead of the M <= 16 tokens, reloaded when a wave's unit moves to the next tile (a drain of
+// the wave's ring, once a tile: a tile's 32 units stream ~1.6 MB of weights against 8 KB of activations a wave).
+template <int W, int SH, bool GA = false>
 __global__ void __launch_bounds__((W + 1) * kWave) decode_gate_up_lds_kernel(DecodeArgs a, SharedJob sh) {
     constexpr int NS = gul::kGuStages, G = 2 * W;
     static_assert(W >= 1 && W <= gul::kGuMaxWaves, "K = 256 W");
@@ -459,15 +462,16 @@ __global__ void __launch_bounds__((W + 1) * kWave) decode_gate_up_lds_kernel(Dec
     const int32_t U0 = (int32_t)u0, U1 = (int32_t)u1;
     const int32_t T0 = U0 / upt;  // the block's first tile (the launcher checks that its tiles fit tslot)
 
-    // this wave's activations: groups 2 w, 2 w + 1 of all M <= 16 tokens (rows past M read zeros)
+    // this wave's activations: groups 2 w, 2 w + 1 of all M <= 16 tokens (rows past M read zeros); GA: of the slots
+    // of the current tile (loaded after the tile tables below)
     uint4 xr[2][4];
-    {
-        const uint32_t xo = j < a.M ? ((uint32_t)j * (uint32_t)a.K + 32u * g) * 2 : a.x_bytes;
+    auto load_x = [&](uint32_t xo) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < 2; ++k)
 #pragma unroll
             for (int v = 0; v < 4; ++v) xr[k][v] = bld16(rx, xo, (uint32_t)((2 * wave + k) * dec::kSpan + 8 * v) * 2);
-    }
+    };
+    if constexpr (!GA) load_x(j < a.M ? ((uint32_t)j * (uint32_t)a.K + 32u * g) * 2 : a.x_bytes);
     for (int64_t t = tid; t < n_tiles; t += nthr) tb[t] = a.ws[rec0 + route::kRec16 * t];
     const int32_t nbt = (U1 - 1) / upt - T0 + 1;  // tiles the block's units touch
     for (int i = tid; i < nbt * 16; i += nthr) tslot[i / 16][i % 16] = a.ws[rec0 + route::kRec16 * (T0 + i / 16) + 4 + i % 16];
@@ -489,7 +493,8 @@ __global__ void __launch_bounds__((W + 1) * kWave) decode_gate_up_lds_kernel(Dec
                 const int32_t sl = tslot[t - T0][k0 + g];
                 if (__builtin_amdgcn_readfirstlane(tslot[t - T0][k0]) < 0) break;
                 if (sl < 0) continue;
-                const uint32_t tok = (uint32_t)sl / A32, i = tok % 4;
+                // the MFMA row of the slot: its token (decode) or its place in the tile (GA)
+                const uint32_t tok = GA ? (uint32_t)(k0 + g) : (uint32_t)sl / A32, i = tok % 4;
                 const int src = (int)(tok / 4) * 16 + j;
                 float gv = 0.f, uv = 0.f;
 #pragma unroll
@@ -540,7 +545,7 @@ __global__ void __launch_bounds__((W + 1) * kWave) decode_gate_up_lds_kernel(Dec
     // against ones
     Frag xf[2][4];
     float xs[2][4];
-    {
+    auto prep_x = [&]() __attribute__((always_inline)) {
         const Frag ones{{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}};
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -553,7 +558,18 @@ __global__ void __launch_bounds__((W + 1) * kWave) decode_gate_up_lds_kernel(Dec
 #pragma unroll
             for (int i = 0; i < 4; ++i) xs[k][i] = d[i];
         }
-    }
+    };
+    // GA: lane (g, j) loads the row of the tile's slot j (its token slot / A), zeros past the tile's rows
+    int32_t xtile = -1;
+    auto gather_x = [&](int32_t t) __attribute__((always_inline)) {
+        const int32_t sl = tslot[t - T0][j];
+        load_x(sl >= 0 ? ((uint32_t)sl / A32 * (uint32_t)a.K + 32u * g) * 2 : a.x_bytes);
+        wait_vmcnt<0>();  // (every load of the wave: the ring's loads in flight land too)
+        prep_x();
+        xtile = t;
+    };
+    if constexpr (GA) gather_x(U0 / upt);
+    else prep_x();
 
     float4v acc[2] = {float4v{0, 0, 0, 0}, float4v{0, 0, 0, 0}};
     uint32_t smd[4] = {0, 0, 0, 0};  // the current unit's scale / min dwords of row j: gate s, gate m, up s, up m
@@ -562,6 +578,10 @@ __global__ void __launch_bounds__((W + 1) * kWave) decode_gate_up_lds_kernel(Dec
     // and meets the block (and the finisher)
     auto step = [&](int32_t q, auto P) __attribute__((always_inline)) {
         constexpr int p = decltype(P)::value, half = p % 2;
+        if constexpr (GA && half == 0) {  // a unit on another tile: that tile's slots' activations
+            const int32_t u = U0 + q / 2;
+            if (u < U1 && u / upt != xtile) gather_x(u / upt);
+        }
         // loads issued after stage q's (at step q - 3): those of stages q + 1 and q + 2 (a gate stage: 4, an up: 2)
         wait_vmcnt<6>();
         __builtin_amdgcn_sched_barrier(0);
@@ -888,11 +908,34 @@ inline DecodeArgs decode_args(const GemmArgs &ga, int64_t M, bool swiglu) {
 }
 
 template <int W>
-void launch_decode_gate_up_lds(const DecodeArgs &d, SharedJob s, hipStream_t stream) {
+void launch_decode_gate_up_lds(const DecodeArgs &d, SharedJob s, hipStream_t stream, bool gather = false) {
     s.blocks = s.units > 0 ? (int)((s.units + (W + 1) * kWave - 1) / ((W + 1) * kWave)) : 0;
     const unsigned blocks = (unsigned)(device_cus() + s.blocks);
-    if (s.blocks > 0) decode_gate_up_lds_kernel<W, 1><<<blocks, (W + 1) * kWave, 0, stream>>>(d, s);
+    if (gather) decode_gate_up_lds_kernel<W, 0, true><<<blocks, (W + 1) * kWave, 0, stream>>>(d, s);
+    else if (s.blocks > 0) decode_gate_up_lds_kernel<W, 1><<<blocks, (W + 1) * kWave, 0, stream>>>(d, s);
     else decode_gate_up_lds_kernel<W, 0><<<blocks, (W + 1) * kWave, 0, stream>>>(d, s);
+}
+
+// the LDS-ring gate_up's shapes: K = 256 W (W 8 or 12), Q4 g128; a block's unit range (at most ceil(units / CUs)
+// units) must touch at most kGuMaxBlockTiles tiles, and the tile count fit the block's table
+inline bool gate_up_lds_fits(const GemmArgs &ga) {
+    const int64_t tiles_bound = std::min(ga.S, ga.S / 16 + ga.E + 2);
+    const int64_t upt = ga.N / 32, most_units = (tiles_bound * upt + device_cus() - 1) / device_cus();
+    return ga.G == dec::kSpan && ga.K % 256 == 0 && (ga.K / 256 == 8 || ga.K / 256 == 12) && (ga.N / 2) % 16 == 0 &&
+           (most_units + upt - 1) / upt + 1 <= gul::kGuMaxBlockTiles && tiles_bound <= kDecMaxTilesL;
+}
+
+// gate_up + SwiGLU at any token count through the LDS-ring kernel, activations gathered by the tiles' slots
+inline bool gate_up_stream_fits(const GemmArgs &ga, int64_t M) {
+    return gate_up_lds_fits(ga) && M * ga.K * 2 < (1ll << 31) && ga.S * (ga.N / 2) * 2 < (1ll << 31) &&
+           ga.N * ga.E * ga.K / 2 < (1ll << 31) && ga.N * ga.E * (ga.K / ga.G) * 2 < (1ll << 31);
+}
+inline void launch_gate_up_stream(const GemmArgs &ga, int64_t M, hipStream_t stream) {
+    const DecodeArgs d = decode_args(ga, M, true);
+    switch (ga.K / 256) {
+        case 8: return launch_decode_gate_up_lds<8>(d, SharedJob{}, stream, true);
+        default: return launch_decode_gate_up_lds<12>(d, SharedJob{}, stream, true);
+    }
 }
 
 template <int SPW>
@@ -917,11 +960,8 @@ inline void launch_decode_gate_up(const GemmArgs &ga, int64_t M, const SharedJob
     const DecodeArgs d = decode_args(ga, M, true);
     SharedJob s = sh ? *sh : SharedJob{};
     s.blocks = sh ? (int)((s.units + kDecGuWaves * kWave - 1) / (kDecGuWaves * kWave)) : 0;
-    // the LDS-ring kernel: W = K / 256 waves; a block's unit range (at most ceil(units / CUs) units) must touch at most
-    // kGuMaxBlockTiles tiles
-    const int64_t upt = ga.N / 32, most_units = (d.tiles_bound * upt + device_cus() - 1) / device_cus();
-    if (ga.K % 256 == 0 && (ga.K / 256 == 8 || ga.K / 256 == 12) &&
-        (most_units + upt - 1) / upt + 1 <= gul::kGuMaxBlockTiles && !getenv("STRIX_OLD_GU")) {
+    // the LDS-ring kernel: W = K / 256 waves
+    if (gate_up_lds_fits(ga)) {
         SharedJob t = s;
         t.units = sh ? s.units : 0;
         switch (ga.K / 256) {
@@ -955,8 +995,7 @@ inline void launch_decode_down(const GemmArgs &ga, int64_t M, const SharedJob *s
     // the LDS-ring kernel deals its waves to tiles: every tile needs a wave
     constexpr int kDnBlocksPerCu = 163840 / (gdn::kDnWaves * gdn::kDnStages * gdn::kPosU4 * 16);
     if (ga.K == dec::kSpan * kDecDownSteps && ga.N % 16 == 0 &&
-        d.tiles_bound <= (int64_t)kDnBlocksPerCu * device_cus() * gdn::kDnWaves &&
-        !getenv("STRIX_OLD_DN")) {
+        d.tiles_bound <= (int64_t)kDnBlocksPerCu * device_cus() * gdn::kDnWaves) {
         // 4 waves x 3 ring positions a block, three blocks a CU (12 waves): measured on MI355X at 16 tokens, H 3072,
         // I 512, 512 experts top-10 (layer us): 4 x 4 two blocks 104.2, 4 x 3 102.7, 3 x 4 104.1, 3 x 6 109.9,
         // 2 x 8 109.3, 1 x 8 110.4 - more waves beat more units in flight (the LDS reads and the dequantisation

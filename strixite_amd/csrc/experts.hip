@@ -1335,6 +1335,8 @@ void gather_grouped_swiglu(const char *fn, const void *x, const V &wv, int64_t E
         }
     } else if (!h_f16 && w.bits == 4 && decode_fits(a, M, true)) {
         launch_decode_gate_up(a, M, nullptr, stream);
+    } else if (!h_f16 && w.bits == 4 && gate_up_stream_fits(a, M)) {
+        launch_gate_up_stream(a, M, stream);
     } else if (h_f16) launch_bits<GROUPED, EPI_SWIGLU, false, true, true>(w.bits, a, tiles, stream);
     else launch_bits<GROUPED, EPI_SWIGLU, false, true, false>(w.bits, a, tiles, stream);
     STRIX_HIP_CHECK_LAUNCH(fn, " M=", M, " A=", A, " E=", E, " N=", N, " K=", w.K, " G=", w.G, h_f16 ? " (F16 h)" : "");

@@ -285,6 +285,40 @@ def test_grouped_gather_plain_q4():
     assert rel_err(y, ref) < 1e-2
 
 
+def test_stream_kernels_invalid_ids_make_nan_rows():
+    """The gathered LDS-ring gate_up and the stream down at M above 16 (exact-weight kinds): a slot with an invalid id
+    (-1, E, beyond) gets a NaN h row and NaN partials; the other slots match the oracle."""
+    say("stream kernels invalid ids")
+    M, A, E, H, I = 48, 4, 32, 3072, 512
+    gu, dn = _experts(4, E, H, I, seed=19)
+    x = orc.gen_bf16_normal(orc.tensor_key(8, "x"), 1.0, (M, H))
+    ids = np.stack([np.random.default_rng(500 + m).permutation(E)[:A] for m in range(M)]).astype(np.int32)
+    ids[5, 1], ids[20, 3], ids[47, 0] = -1, E, E + 7
+    tid = torch.from_numpy(ids).to(DEV)
+    ws, _ = moe.moe_group_routes(tid, E)
+    ex = moe.MOE_MATH_WMMA_BF16
+    h = to_np(moe.experts_gather_grouped_swiglu(bf16(x), gu, E, ws, M, A, math=ex))
+    bad = np.array([5 * A + 1, 20 * A + 3, 47 * A + 0])
+    good = np.setdiff1d(np.arange(M * A), bad)
+    assert np.all(np.isnan(orc.bf16_to_f32(h[bad]))) and not np.isnan(orc.bf16_to_f32(h[good])).any()
+    ok_ids = ids.copy()
+    ok_ids[ids < 0], ok_ids[ids >= E] = 0, 0
+    b, q, s, m, G = qspec(gu)
+    href = orc.experts_gate_up_swiglu(x, orc.qview(b, q, s, m, gu.N, H, G), E, ok_ids)
+    assert rel_err(h[good], href[good]) < 1e-2
+    hz = h.copy()
+    hz[bad] = 0
+    pt = torch.empty((M * A, H), dtype=torch.float32, device=DEV)
+    coef = torch.full((M, A), 0.25, device=DEV)
+    moe.experts_combine_grouped(torch.from_numpy(hz.view(np.int16)).to(DEV).view(torch.bfloat16), dn, E, tid, coef,
+                                ws, M, A, partial=pt, math=ex)
+    p = pt.cpu().numpy()
+    assert np.all(np.isnan(p[bad]))
+    b, q, s, m, G = qspec(dn)
+    pref = orc.experts_down(hz, orc.qview(b, q, s, m, dn.N, I, G), E, ok_ids)
+    assert rel_err(p[good], pref[good]) < 1e-4
+
+
 def test_invalid_ids_make_nan_rows():
     say("experts invalid ids")
     M, A, E, H, I = 4, 2, 8, 256, 128
@@ -379,11 +413,12 @@ def test_perslot_kernels_match_grouped():
     assert to_np(err).view(np.uint32).tolist() == [1, E + 5, 6]
 
 
-@pytest.mark.parametrize("M,A,E", [(4, 6, 24), (40, 3, 6)])
+@pytest.mark.parametrize("M,A,E", [(4, 6, 24), (40, 3, 6), (100, 10, 128)])
 def test_decode_kernels_match_perslot(M, A, E):
-    """The decode-size grouped kernels at the served shape (H 3072, I 512, Q4 g128): h bit for bit that of the per-slot
-    kernel, h and the down partials against the oracle; (40, 3, 6) puts 20 slots
-    on each expert, so each expert has two token tiles."""
+    """The LDS-ring stream kernels at the served shape (H 3072, I 512, Q4 g128, the exact-weight kinds): h against the
+    per-slot kernel, h and the down partials against the oracle. (4, 6, 24): the decode form (all M <= 16 tokens in the
+    MFMA's rows); (40, 3, 6) puts 20 slots on each expert, so each expert has two token tiles, and (100, 10, 128)
+    ~8: both take the gathered form (a tile's slots' rows), M above 16."""
     say("decode kernels vs per-slot", M, A, E)
     H, I = 3072, 512
     gu, dn = _experts(4, E, H, I, seed=13)
