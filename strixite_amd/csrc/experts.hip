@@ -1302,6 +1302,10 @@ int64_t grouped_tiles(int64_t M, int64_t A, int64_t E) { return std::min(M * A, 
 // the reference's F16 matrix-unit kinds (x and the dequantized Q4 weights in F16) against the exact-weight ones
 bool f16_math(MoeMath m) { return m >= MoeMath::WmmaF16; }
 
+// the shared expert's dense projections take the LDS-tiled GEMM from this many tokens (measured on MI355X, cfg3's 512
+// tokens: 367 us a layer against 385 with the stream kernels; cfg4: 0.81 against 1.09 ms)
+constexpr int64_t kSharedGemmMinTokens = 128;
+
 bool use_expert_gemm(int64_t S, int64_t E, int64_t K, int64_t G) {
     return S >= 1024 && S >= 16 * E && K % gemm::BK == 0 && G % gemm::BK == 0 && K / G <= gemm::kMaxGroups;
 }
@@ -1960,7 +1964,8 @@ void moe_layer_forward(const MoeLayerWeights &w, const void *x, int64_t M, const
         a.M = M;
         GemmArgs b = make_args(dv, 1, sh_h, sh_s, H);
         b.M = M;
-        if (M >= 128 && H % gemm::BK == 0 && I % gemm::BK == 0 && gv.G % gemm::BK == 0 && dv.G % gemm::BK == 0) {
+        if (M >= kSharedGemmMinTokens && H % gemm::BK == 0 && I % gemm::BK == 0 && gv.G % gemm::BK == 0 &&
+            dv.G % gemm::BK == 0) {
             launch_expert_gemm<8, DENSE, EPI_SWIGLU, false, false>(a, sh_stream);
             launch_expert_gemm<8, DENSE, EPI_BF16, false, false>(b, sh_stream);
         } else {
