@@ -15,9 +15,11 @@
 // are one group. The block's activations (gathered by slot) reach LDS two chunks ahead: X_F16P (x already F16 in the
 // paired order below) straight from memory into one of three LDS buffers; otherwise (BF16 x, or F16 x in natural
 // order) through registers, converted or permuted there, into one of two. The 16-byte columns of an LDS row are
-// XOR-swizzled by the row, so the MFMA reads are conflict-free. Each lane loads its weight row's 32 codes of a chunk
-// (16 bytes) two chunks ahead. A block whose slots fill fewer than 4 of its 32-token sub-tiles runs a K loop for just
-// the live ones.
+// XOR-swizzled by half the row index, so the MFMA reads are conflict-free. Codes: with X_F16P, a wave's 64 weight
+// rows' codes of a 4-chunk span (128 bytes a row: whole lines, 8 rows an instruction) go straight into 8 KB of LDS a
+// span ahead and into registers a span at a time (the 32 rows x 32 bytes a lane's own chunk load would touch cost the
+// vector memory path ~4x as much per instruction); otherwise each lane loads its row's 32 codes of a chunk two chunks
+// ahead. A block whose slots fill fewer than 4 of its 32-token sub-tiles runs a K loop for just the live ones.
 //
 // The k order of an MFMA operand: lane half h takes k 32 h .. 32 h + 31 of a chunk and K step ks the 8 at
 // 32 h + 8 ks, whose 8 halves hold k = 0, 4, 1, 5, 2, 6, 3, 7 of that block (the paired order), for the activations
@@ -96,13 +98,32 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// the LDS byte address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// wait_vmcnt<n> for n known after unrolling (the values the prefill GEMM's chunk order produces)
+__device__ __forceinline__ void wait_vmcnt_n(int n) {
+    switch (n) {
+        case 4: wait_vmcnt<4>(); break;
+        case 8: wait_vmcnt<8>(); break;
+        case 12: wait_vmcnt<12>(); break;
+        case 16: wait_vmcnt<16>(); break;
+        case 20: wait_vmcnt<20>(); break;
+        case 24: wait_vmcnt<24>(); break;
+        case 32: wait_vmcnt<32>(); break;
+        default: wait_vmcnt<0>(); break;
+    }
+}
+
 // [rows, K] BF16 -> F16 toward zero in the paired order (the X16 input of the gate_up projection); n8 = rows * K / 8
 __global__ void __launch_bounds__(256) bf16_to_f16_paired_kernel(const uint4 *x, uint4 *y, int64_t n8) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x)
         y[i] = bf16x8_to_f16_paired(x[i]);
 }
 
-template <int EPI, bool XROW_DIV, int HF, int XF, int GS>
+template <int EPI, bool XROW_DIV, int HF, int XF, int GS, bool SE>
 __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
     expert_gemm2_kernel(GemmArgs a, int64_t pairs_bound, int64_t col_blocks, int64_t pair_at, int64_t npairs_at,
                         uint32_t q_bytes, uint32_t s_bytes, uint32_t x_bytes, uint32_t y_bytes) {
@@ -111,12 +132,21 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     static_assert(SWI || EPI == EPI_BF16, "SwiGLU h or BF16 outputs");
     static_assert(GS == 32 || GS == 64 || GS == 128, "group sizes 32, 64, 128");
     constexpr int CPG = GS > BK ? GS / BK : 1;  // chunks that start with a new scale and min
-    // the activation buffers [row * 8 + (col ^ (row & 7))], separate arrays picked at compile time: the compiler
+    // X16 at G 128 with an even number of groups a row: a span's two groups' scales (and mins) come as one aligned
+    // dword a row, loaded a span ahead (4 instead of 8 loads a span, each over the 12 lines of 32 rows)
+    constexpr bool SPAN_SM = X16 && CPG == 2 && SE;
+    static_assert(!SE || SPAN_SM, "SE: X16 at G 128 only");
+    // the activation buffers [row * 8 + (col ^ ((row >> 1) & 7))], separate arrays picked at compile time: the
+    // compiler
     // then tells a read of one from the loads still landing in another and waits for those loads no longer than it
     // must
     __shared__ __attribute__((aligned(16))) uint4 As0[BM * BK / 8], As1[BM * BK / 8], As2[X16 ? BM * BK / 8 : 1];
     auto abuf = [&](int i) __attribute__((always_inline)) -> uint4 * { return i == 0 ? As0 : i == 1 ? As1 : As2; };
-    __shared__ int32_t orow[BM];
+    // X16: the codes of a 4-chunk span (256 k: 128 bytes of each of a wave's 64 weight rows, whole lines) reach LDS
+    // directly, 8 KB a wave; otherwise each lane loads its own 32 codes of a chunk (32 rows x 32 bytes an
+    // instruction: gfx950's vector memory path takes ~4x as long for those 32 lines as for 8 whole ones)
+    constexpr bool QLDS = X16;
+    __shared__ __attribute__((aligned(16))) uint4 Qs[QLDS ? 4 * 512 : 1];
     const int tid = threadIdx.x, lane = tid % kWave, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int h = lane / 32, l32 = lane % 32;
 
@@ -134,17 +164,17 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     const bool nan = bucket < 0 || bucket >= a.E;
     const uint32_t expert = nan ? 0u : (uint32_t)bucket;
     const int32_t *slots = a.ws + route::slots_at(a.E) + start;
-    if (tid < BM) orow[tid] = tid < rows ? slots[tid] : -1;
+    auto orow = [&](int r) __attribute__((always_inline)) { return r < rows ? slots[r] : -1; };
 
     const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, x_bytes), rq = rsrc(a.q, q_bytes), rs = rsrc(a.scale, s_bytes),
                                  rm = rsrc(a.minv, s_bytes), ry = rsrc(a.y, y_bytes);
     const uint32_t K = (uint32_t)a.K, groups = (uint32_t)(a.K / GS);
     const int chunks = (int)(a.K / BK);
-    // this thread's activation pieces: LDS slots tid + 256 v (v = 0..3) = row / 8, column ^ (row & 7)
+    // this thread's activation pieces: LDS slots tid + 256 v (v = 0..3) = row / 8, column ^ ((row >> 1) & 7)
     uint32_t xoff[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-        const int slot = tid + 256 * v, row = slot / 8, col = (slot % 8) ^ (row & 7);
+        const int slot = tid + 256 * v, row = slot / 8, col = (slot % 8) ^ ((row >> 1) & 7);
         const int32_t s = row < rows ? slots[row] : -1;
         xoff[v] = s >= 0 ? ((XROW_DIV ? (uint32_t)s / (uint32_t)a.A : (uint32_t)s) * K + col * 8) * 2 : x_bytes;
     }
@@ -154,17 +184,33 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     int64_t col0[2];
     uint32_t wrow[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        col0[t] = SWI ? cb * (BN / 2) + 32 * wave : cb * BN + 64 * wave + 32 * t;
-        const int64_t c = col0[t] + l32, cl = c < nrows ? c : nrows - 1;
-        wrow[t] = expert * (uint32_t)a.N + (uint32_t)(SWI && t == 1 ? a.N / 2 + cl : cl);
-    }
+    for (int t = 0; t < 2; ++t) col0[t] = SWI ? cb * (BN / 2) + 32 * wave : cb * BN + 64 * wave + 32 * t;
+    auto wrow_of = [&](int t, int l) __attribute__((always_inline)) {
+        const int64_t c = col0[t] + l, cl = c < nrows ? c : nrows - 1;
+        return expert * (uint32_t)a.N + (uint32_t)(SWI && t == 1 ? a.N / 2 + cl : cl);
+    };
+#pragma unroll
+    for (int t = 0; t < 2; ++t) wrow[t] = wrow_of(t, l32);
     const uint32_t qoff[2] = {wrow[0] * (K / 2) + 16 * h, wrow[1] * (K / 2) + 16 * h};
+    // QLDS: instruction i of a span's load brings rows 8 i .. 8 i + 7 of the wave's 64 (tile i / 4), 8 lanes a row;
+    // lane p lands in LDS slot 64 i + p = row * 8 + 16-byte column p % 8, which holds the row's column (p % 8) ^
+    // ((row >> 1) & 7) (the activations' swizzle: a lane group's 16 rows then read 16 distinct bank groups)
+    uint32_t qdoff[QLDS ? 8 : 1];
+    if constexpr (QLDS) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int rr = 8 * i + lane / 8, seg = (lane % 8) ^ ((rr >> 1) & 7);
+            qdoff[i] = wrow_of(rr / 32, rr % 32) * (K / 2) + 16 * seg;
+        }
+    }
     const uint32_t soff[2] = {wrow[0] * groups * 2, wrow[1] * groups * 2};
-    // this lane's LDS fragment of K step ks in a buffer: row 32 i + l32 (row & 7 = l32 & 7), 16-byte column 4 h + ks
+    // this lane's LDS fragment of K step ks in a buffer: row 32 i + l32 ((row >> 1) & 7 = (l32 >> 1) & 7), 16-byte
+    // column 4 h + ks. gfx950 serves a 16-byte read 16 lanes at a time from 64 banks (256 bytes): lanes of rows r and
+    // r + 8 would share banks under col ^ (row & 7) (2-way conflicts, reads at 2/3 of the rate); under the swizzle by
+    // row / 2 the 16 rows of a lane group cover every bank once.
     int aofs[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) aofs[ks] = l32 * 8 + ((4 * h + ks) ^ (l32 & 7));
+    for (int ks = 0; ks < 4; ++ks) aofs[ks] = l32 * 8 + ((4 * h + ks) ^ ((l32 >> 1) & 7));
     uint32_t b64, b54;  // in VGPRs, so the and-or takes the mask as its one scalar operand
     asm("v_mov_b32 %0, 0x64006400" : "=v"(b64));
     asm("v_mov_b32 %0, 0x54005400" : "=v"(b54));
@@ -174,8 +220,8 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     // chunks ahead), so the activations of chunk c are in LDS once at most 6 (chunk c - 1 loaded no scales: c odd at
     // G 128, and chunk 0) or 10 later loads are outstanding.
     uint4 ar[2][4];  // !X16: activations in flight
-    constexpr int QPF = 2;  // chunks of codes in flight
-    uint4 qr[QPF][2];
+    constexpr int QPF = 2;  // !QLDS: chunks of codes in flight
+    uint4 qr[QLDS ? 4 : QPF][2];  // QLDS: the span's codes, chunk c % 4
     auto load_a = [&](int c, uint4 (&dst)[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) dst[v] = bld16(rx, xoff[v], (uint32_t)c * BK * 2);
@@ -183,6 +229,23 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     auto dma_a = [&](int c, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) lds_load16(rx, abuf(buf) + 256 * v + 64 * wave, xoff[v], (uint32_t)c * BK * 2);
+    };
+    auto dma_q = [&](int span) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lds_load16(rq, Qs + 512 * wave + 64 * i, qdoff[i], (uint32_t)span * 128);
+    };
+    // the span's 8 reads: issued as inline asm, so the compiler does not wait for every load into LDS still in flight
+    // before them (it cannot tell the span's buffer from the activations'); the caller waits for the span's load
+    auto read_q = [&]() __attribute__((always_inline)) {
+        const int fx = (l32 >> 1) & 7;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const uint32_t ad = lds_addr(Qs + 512 * wave + l32 * 8 + ((2 * cc + h) ^ fx));
+            v4u32_t v0, v1;
+            asm volatile("ds_read_b128 %0, %1" : "=v"(v0) : "v"(ad));
+            asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(v1) : "v"(ad));  // tile 1: rows 32 .. 63
+            qr[cc][0] = __builtin_bit_cast(uint4, v0), qr[cc][1] = __builtin_bit_cast(uint4, v1);
+        }
     };
     auto load_q = [&](int c, uint4 (&dst)[2]) __attribute__((always_inline)) {
 #pragma unroll
@@ -197,6 +260,15 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     // (chunk c: this lane half's k 64 c + 32 h lie in group (64 c + 32 h) / G)
     f16x2v sc[2], mn[2];
     uint16_t sraw[2], mraw[2];
+    uint32_t sraw2[2], mraw2[2], shi[2], mhi[2];  // SPAN_SM: the span's two groups; the second group's halves
+    auto load_sm_span = [&](int span) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t o = 4 * span < chunks ? soff[t] + 4 * (uint32_t)span : s_bytes;
+            sraw2[t] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0);
+            mraw2[t] = __builtin_amdgcn_raw_buffer_load_b32(rm, o, 0, 0);
+        }
+    };
     auto load_sm = [&](int c) __attribute__((always_inline)) {
         const uint32_t gi = ((uint32_t)c * BK + 32u * (uint32_t)h) / GS;
 #pragma unroll
@@ -206,13 +278,17 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
             mraw[t] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rm, o, 0, 0);
         }
     };
-    load_sm(0);
+    if constexpr (SPAN_SM) load_sm_span(0);
+    else load_sm(0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (X16) {
-        load_q(0, qr[0]);
+        // span 0's codes straight into registers (the 32-line form, once); then the same order as the chunks' ends:
+        // activations two chunks ahead, then the next span's codes into LDS
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) load_q(cc, qr[cc]);
         dma_a(0, 0);
-        load_q(1, qr[1]);
         dma_a(1, 1);
+        dma_q(1);
     } else {
         load_a(0, ar[0]);
         load_a(1, ar[1]);
@@ -232,8 +308,9 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
         for (int i = 0; i < NT; ++i)
 #pragma unroll
             for (int t = 0; t < 2; ++t) acc[i][t] = float16v{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        // trips of TRIP chunks (X16: 6, so the three buffers' turns are known at compile time; a multiple of CPG)
-        constexpr int TRIP = X16 ? 6 : 2;
+        // trips of TRIP chunks (X16: 12, so the three buffers' and the four span positions' turns are known at
+        // compile time; a multiple of CPG)
+        constexpr int TRIP = X16 ? 12 : 2;
         static_assert(TRIP % CPG == 0, "a trip starts a group");
         for (int c0 = 0; c0 < chunks; c0 += TRIP) {
 #pragma unroll
@@ -242,11 +319,27 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                 if (c >= chunks) break;
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (X16) {
-                    // chunk c - 1 loaded no scales (CPG 2: c even); CPG 1: at a trip's start, also right for chunk 0
-                    if ((CPG == 2 && p == 0) || (CPG == 1 && pt == 0)) wait_vmcnt<6>();
-                    else wait_vmcnt<10>();
+                    // chunk c's activations (issued at the end of chunk c - 2) have landed: the loads issued after
+                    // them are chunk c - 2's span load (if it ended a span), chunk c - 1's scales (at a group start),
+                    // activations and span load; the prologue stands for chunk -1 (activations 1 and span 1)
+                    const int spn2 = (pt + TRIP - 2) % 4 == 3 ? 8 : 0, spn1 = (pt + TRIP - 1) % 4 == 3 ? 8 : 0;
+                    const int sm1 = (pt + TRIP - 1) % (SPAN_SM ? 4 : CPG) == 0 ? 4 : 0;
+                    wait_vmcnt_n(pt == 0 && c == 0 ? 12 : 4 + sm1 + spn2 + spn1);
                 }
-                if (pt % CPG == 0) {
+                if constexpr (SPAN_SM) {
+                    if (pt % 4 == 0) {
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) {
+                            sc[t] = bf16_to_f16x2((uint16_t)sraw2[t]), mn[t] = bf16_to_f16x2((uint16_t)mraw2[t]);
+                            shi[t] = sraw2[t] >> 16, mhi[t] = mraw2[t] >> 16;
+                        }
+                        load_sm_span(c / 4 + 1);
+                    } else if (pt % 4 == 2) {
+#pragma unroll
+                        for (int t = 0; t < 2; ++t)
+                            sc[t] = bf16_to_f16x2((uint16_t)shi[t]), mn[t] = bf16_to_f16x2((uint16_t)mhi[t]);
+                    }
+                } else if (pt % CPG == 0) {
 #pragma unroll
                     for (int t = 0; t < 2; ++t) sc[t] = bf16_to_f16x2(sraw[t]), mn[t] = bf16_to_f16x2(mraw[t]);
                     load_sm(c + CPG);
@@ -257,7 +350,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                 else __syncthreads();
                 __builtin_amdgcn_sched_barrier(0);
                 const uint4 *as = abuf(X16 ? pt % 3 : p);
-                const uint4(&q)[2] = qr[pt % QPF];
+                const uint4(&q)[2] = qr[QLDS ? pt % 4 : pt % QPF];
                 Frag af[2][NT];
                 auto read_a = [&](int ks, Frag (&dst)[NT]) __attribute__((always_inline)) {
 #pragma unroll
@@ -281,9 +374,18 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                load_q(c + QPF, qr[pt % QPF]);
+                if constexpr (!QLDS) load_q(c + QPF, qr[pt % QPF]);
                 if constexpr (X16) {
                     dma_a(c + 2, (pt + 2) % 3);  // buffer (c + 2) % 3, last read at chunk c - 1
+                    if (pt % 4 == 3) {
+                        // the next span's codes to registers, then, once read, the span after it into the same LDS.
+                        // The span's load (issued at the end of chunk c - 4) has landed once the loads of chunks
+                        // c - 3 .. c are all that remain: their activations and, at group starts, scales
+                        wait_vmcnt_n(16 + 4 * (SPAN_SM ? 1 : 4 / CPG));
+                        read_q();
+                        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                        dma_q((c + 1) / 4 + 1);
+                    }
                 } else {
                     // the next chunk's activations to the other buffer, then the load of the one after next
                     store_a(ar[p ^ 1], p ^ 1);
@@ -323,7 +425,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                 for (int q = 0; q < 4; ++q) {
                     const int row = 8 * q + lane / 8, seg = lane % 8;
                     const uint4 v = *reinterpret_cast<const uint4 *>(st + sidx(row, 8 * seg));
-                    const int32_t orw = orow[32 * i + row];
+                    const int32_t orw = orow(32 * i + row);
                     const int64_t col = col0[0] + 8 * seg;  // the wave's 64 columns from col0[0]
                     const bool live = orw >= 0 && col < nrows;
                     __builtin_amdgcn_raw_buffer_store_b128(
@@ -365,7 +467,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                     const float lo = upper ? got : v[0], hi = upper ? v[1] : got;
                     // F16 forms: the BF16-rounded h toward zero (what a BF16 h converts to on the way into the down)
                     const uint32_t bits = HF == H_BF16 ? f32x2_to_bf16x2(lo, hi) : pk_f16_rtz(bf16_round(lo), bf16_round(hi));
-                    const int32_t orw = orow[32 * i + 8 * (r / 4) + 4 * h + r % 4 + (upper ? 1 : 0)];
+                    const int32_t orw = orow(32 * i + 8 * (r / 4) + 4 * h + r % 4 + (upper ? 1 : 0));
                     __builtin_amdgcn_raw_buffer_store_b32(
                         bits, ry, orw >= 0 && live_col ? ((uint32_t)orw * (uint32_t)a.ldy + dpos) * 2 : y_bytes, 0, 0);
                 }
@@ -400,15 +502,25 @@ bool launch_expert_gemm2(const GemmArgs &a, hipStream_t stream) {
     if (q_bytes >= (1ll << 31) || s_bytes >= (1ll << 31) || x_bytes >= (1ll << 31) || y_bytes >= (1ll << 31)) return false;
     const int64_t blocks = (pairs_bound + 7) / 8 * 8 * col_blocks;  // whole rounds of the 8 XCDs
     if (blocks >= (1ll << 31)) return false;
-    auto go = [&](auto gs) {
-        expert_gemm2_kernel<EPI, XROW_DIV, HF, XF, decltype(gs)::value><<<(unsigned)blocks, g2::kThreads, 0, stream>>>(
-            a, pairs_bound, col_blocks, L.pair_rec(), L.npairs(), (uint32_t)q_bytes, (uint32_t)s_bytes,
-            (uint32_t)x_bytes, (uint32_t)y_bytes);
+    auto go = [&](auto gs, auto se) {
+        expert_gemm2_kernel<EPI, XROW_DIV, HF, XF, decltype(gs)::value, decltype(se)::value>
+            <<<(unsigned)blocks, g2::kThreads, 0, stream>>>(a, pairs_bound, col_blocks, L.pair_rec(), L.npairs(),
+                                                            (uint32_t)q_bytes, (uint32_t)s_bytes, (uint32_t)x_bytes,
+                                                            (uint32_t)y_bytes);
     };
+    using F = std::false_type;
     switch (a.G) {
-        case 32: go(std::integral_constant<int, 32>{}); break;
-        case 64: go(std::integral_constant<int, 64>{}); break;
-        default: go(std::integral_constant<int, 128>{}); break;
+        case 32: go(std::integral_constant<int, 32>{}, F{}); break;
+        case 64: go(std::integral_constant<int, 64>{}, F{}); break;
+        default:
+            if constexpr (XF == X_F16P) {
+                if ((a.K / a.G) % 2 == 0) {
+                    go(std::integral_constant<int, 128>{}, std::true_type{});
+                    break;
+                }
+            }
+            go(std::integral_constant<int, 128>{}, F{});
+            break;
     }
     return true;
 }
