@@ -106,13 +106,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // wait_vmcnt<n> for n known after unrolling (the values the prefill GEMM's chunk order produces)
 __device__ __forceinline__ void wait_vmcnt_n(int n) {
     switch (n) {
-        case 4: wait_vmcnt<4>(); break;
-        case 8: wait_vmcnt<8>(); break;
-        case 12: wait_vmcnt<12>(); break;
-        case 16: wait_vmcnt<16>(); break;
-        case 20: wait_vmcnt<20>(); break;
-        case 24: wait_vmcnt<24>(); break;
-        case 32: wait_vmcnt<32>(); break;
+#define STRIX_VMCNT_CASE(k) \
+    case k: wait_vmcnt<k>(); break;
+        STRIX_VMCNT_CASE(2) STRIX_VMCNT_CASE(4) STRIX_VMCNT_CASE(6) STRIX_VMCNT_CASE(8) STRIX_VMCNT_CASE(10)
+        STRIX_VMCNT_CASE(12) STRIX_VMCNT_CASE(14) STRIX_VMCNT_CASE(16) STRIX_VMCNT_CASE(18) STRIX_VMCNT_CASE(20)
+        STRIX_VMCNT_CASE(22) STRIX_VMCNT_CASE(24) STRIX_VMCNT_CASE(26) STRIX_VMCNT_CASE(28) STRIX_VMCNT_CASE(30)
+        STRIX_VMCNT_CASE(32)
+#undef STRIX_VMCNT_CASE
         default: wait_vmcnt<0>(); break;
     }
 }
@@ -137,9 +137,8 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     constexpr bool SPAN_SM = X16 && CPG == 2 && SE;
     static_assert(!SE || SPAN_SM, "SE: X16 at G 128 only");
     // the activation buffers [row * 8 + (col ^ ((row >> 1) & 7))], separate arrays picked at compile time: the
-    // compiler
-    // then tells a read of one from the loads still landing in another and waits for those loads no longer than it
-    // must
+    // compiler then tells a read of one from the loads still landing in another and waits for those loads no longer
+    // than it must
     __shared__ __attribute__((aligned(16))) uint4 As0[BM * BK / 8], As1[BM * BK / 8], As2[X16 ? BM * BK / 8 : 1];
     auto abuf = [&](int i) __attribute__((always_inline)) -> uint4 * { return i == 0 ? As0 : i == 1 ? As1 : As2; };
     // X16: the codes of a 4-chunk span (256 k: 128 bytes of each of a wave's 64 weight rows, whole lines) reach LDS
@@ -195,13 +194,17 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     // QLDS: instruction i of a span's load brings rows 8 i .. 8 i + 7 of the wave's 64 (tile i / 4), 8 lanes a row;
     // lane p lands in LDS slot 64 i + p = row * 8 + 16-byte column p % 8, which holds the row's column (p % 8) ^
     // ((row >> 1) & 7) (the activations' swizzle: a lane group's 16 rows then read 16 distinct bank groups)
-    uint32_t qdoff[QLDS ? 8 : 1];
+    // (rr >> 1) & 7 = (4 (i & 1) + lane / 16) & 7, so a lane's byte offsets of the 8 instructions are two bases plus
+    // wave-uniform steps: 8 rows an instruction pair, and tile 1's distance from tile 0 (the up rows at N / 2, or 32
+    // rows). A tile past the projection's rows (whole: N / 2 and N are multiples of 32) reads rows that are never
+    // stored, in bounds or (past the last expert) as zeros.
+    uint32_t qd[2] = {0, 0}, qtile = 0;
     if constexpr (QLDS) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int rr = 8 * i + lane / 8, seg = (lane % 8) ^ ((rr >> 1) & 7);
-            qdoff[i] = wrow_of(rr / 32, rr % 32) * (K / 2) + 16 * seg;
-        }
+        for (int e = 0; e < 2; ++e)
+            qd[e] = ((uint32_t)(expert * a.N + col0[0]) + lane / 8) * (K / 2) +
+                    16 * ((lane % 8) ^ ((4 * e + lane / 16) & 7));
+        qtile = (uint32_t)(SWI ? a.N / 2 : 32) * (K / 2);
     }
     const uint32_t soff[2] = {wrow[0] * groups * 2, wrow[1] * groups * 2};
     // this lane's LDS fragment of K step ks in a buffer: row 32 i + l32 ((row >> 1) & 7 = (l32 >> 1) & 7), 16-byte
@@ -230,9 +233,9 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int v = 0; v < 4; ++v) lds_load16(rx, abuf(buf) + 256 * v + 64 * wave, xoff[v], (uint32_t)c * BK * 2);
     };
-    auto dma_q = [&](int span) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) lds_load16(rq, Qs + 512 * wave + 64 * i, qdoff[i], (uint32_t)span * 128);
+    auto dma_q_piece = [&](int span, int i) __attribute__((always_inline)) {
+        lds_load16(rq, Qs + 512 * wave + 64 * i, qd[i & 1],
+                   (uint32_t)span * 128 + (i / 4) * qtile + (uint32_t)(i % 4) * 8 * (K / 2));
     };
     // the span's 8 reads: issued as inline asm, so the compiler does not wait for every load into LDS still in flight
     // before them (it cannot tell the span's buffer from the activations'); the caller waits for the span's load
@@ -282,13 +285,11 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     else load_sm(0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (X16) {
-        // span 0's codes straight into registers (the 32-line form, once); then the same order as the chunks' ends:
-        // activations two chunks ahead, then the next span's codes into LDS
+        // span 0's codes straight into registers (the 32-line form, once), then the activations of chunks 0 and 1
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) load_q(cc, qr[cc]);
         dma_a(0, 0);
         dma_a(1, 1);
-        dma_q(1);
     } else {
         load_a(0, ar[0]);
         load_a(1, ar[1]);
@@ -319,12 +320,13 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                 if (c >= chunks) break;
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (X16) {
-                    // chunk c's activations (issued at the end of chunk c - 2) have landed: the loads issued after
-                    // them are chunk c - 2's span load (if it ended a span), chunk c - 1's scales (at a group start),
-                    // activations and span load; the prologue stands for chunk -1 (activations 1 and span 1)
-                    const int spn2 = (pt + TRIP - 2) % 4 == 3 ? 8 : 0, spn1 = (pt + TRIP - 1) % 4 == 3 ? 8 : 0;
+                    // chunk c's activations (issued in chunk c - 2's K steps) have landed: the loads issued after
+                    // their last piece are the last two pieces of chunk c - 2's span load (if it started a span),
+                    // chunk c - 1's scales (at a group start), its 4 activation pieces and its 8 span pieces (if it
+                    // started a span); before chunk 0, only chunk 1's activations
+                    const int spn2 = (pt + TRIP - 2) % 4 == 0 ? 2 : 0, spn1 = (pt + TRIP - 1) % 4 == 0 ? 8 : 0;
                     const int sm1 = (pt + TRIP - 1) % (SPAN_SM ? 4 : CPG) == 0 ? 4 : 0;
-                    wait_vmcnt_n(pt == 0 && c == 0 ? 12 : 4 + sm1 + spn2 + spn1);
+                    wait_vmcnt_n(pt == 0 && c == 0 ? 4 : 4 + sm1 + spn2 + spn1);
                 }
                 if constexpr (SPAN_SM) {
                     if (pt % 4 == 0) {
@@ -363,6 +365,10 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     if (ks + 1 < 4) read_a(ks + 1, af[(ks + 1) & 1]);
+                    // the next K step's reads stay ahead of this step's MFMAs (the scheduler would otherwise pull
+                    // them down to just before their use, where each pair's LDS latency stalls the wave); the
+                    // register-staged forms have no VGPRs to spare for it
+                    if constexpr (X16) __builtin_amdgcn_sched_barrier(0);
                     const uint32_t cw0 = ks == 0 ? q[0].x : ks == 1 ? q[0].y : ks == 2 ? q[0].z : q[0].w;
                     const uint32_t cw1 = ks == 0 ? q[1].x : ks == 1 ? q[1].y : ks == 2 ? q[1].z : q[1].w;
                     const Frag b0 = q4_dequant_f16(cw0, sc[0], mn[0], b64, b54),
@@ -372,19 +378,30 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                         acc[i][0] = mfma32_f16(af[ks & 1][i], b0, acc[i][0]);
                         acc[i][1] = mfma32_f16(af[ks & 1][i], b1, acc[i][1]);
                     }
+                    if constexpr (X16) {
+                        // the loads ahead, spread over the K steps (a burst of them fills the vector memory
+                        // path's queues and stalls the issuing wave): activation piece ks of chunk c + 2 into buffer
+                        // (c + 2) % 3 (last read at chunk c - 1); at a span's first chunk, two of the 8 pieces of
+                        // the next span's codes into the wave's LDS (read into registers at the end of chunk c - 1)
+                        __builtin_amdgcn_sched_barrier(0);
+                        lds_load16(rx, abuf((pt + 2) % 3) + 256 * ks + 64 * wave, xoff[ks], (uint32_t)(c + 2) * BK * 2);
+                        if (pt % 4 == 0) {
+                            dma_q_piece(c / 4 + 1, 2 * ks);
+                            dma_q_piece(c / 4 + 1, 2 * ks + 1);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (!QLDS) load_q(c + QPF, qr[pt % QPF]);
                 if constexpr (X16) {
-                    dma_a(c + 2, (pt + 2) % 3);  // buffer (c + 2) % 3, last read at chunk c - 1
                     if (pt % 4 == 3) {
-                        // the next span's codes to registers, then, once read, the span after it into the same LDS.
-                        // The span's load (issued at the end of chunk c - 4) has landed once the loads of chunks
-                        // c - 3 .. c are all that remain: their activations and, at group starts, scales
-                        wait_vmcnt_n(16 + 4 * (SPAN_SM ? 1 : 4 / CPG));
+                        // the next span's codes to registers (the LDS is then free for the span after it). The
+                        // span's load (issued in chunk c - 3's K steps) has landed once the loads of chunks c - 2 ..
+                        // c are all that remain: 12 activation pieces and the scales of their group starts
+                        wait_vmcnt_n(12 + 4 * (SPAN_SM ? 0 : CPG == 2 ? 1 : 3));
                         read_q();
                         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-                        dma_q((c + 1) / 4 + 1);
                     }
                 } else {
                     // the next chunk's activations to the other buffer, then the load of the one after next
