@@ -285,11 +285,15 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     else load_sm(0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (X16) {
-        // span 0's codes straight into registers (the 32-line form, once), then the activations of chunks 0 and 1
+        // span 0's codes into LDS and then registers (they land with chunk 0's activations, which the K loop waits
+        // for anyway), then the activations of chunks 0 and 1
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) load_q(cc, qr[cc]);
+        for (int i = 0; i < 8; ++i) dma_q_piece(0, i);
         dma_a(0, 0);
         dma_a(1, 1);
+        wait_vmcnt<8>();
+        read_q();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): read before chunk 0 loads the next span
     } else {
         load_a(0, ar[0]);
         load_a(1, ar[1]);
