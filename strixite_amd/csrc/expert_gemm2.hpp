@@ -108,10 +108,10 @@ __device__ __forceinline__ void wait_vmcnt_n(int n) {
     switch (n) {
 #define STRIX_VMCNT_CASE(k) \
     case k: wait_vmcnt<k>(); break;
-        STRIX_VMCNT_CASE(2) STRIX_VMCNT_CASE(4) STRIX_VMCNT_CASE(6) STRIX_VMCNT_CASE(8) STRIX_VMCNT_CASE(10)
-        STRIX_VMCNT_CASE(12) STRIX_VMCNT_CASE(14) STRIX_VMCNT_CASE(16) STRIX_VMCNT_CASE(18) STRIX_VMCNT_CASE(20)
-        STRIX_VMCNT_CASE(22) STRIX_VMCNT_CASE(24) STRIX_VMCNT_CASE(26) STRIX_VMCNT_CASE(28) STRIX_VMCNT_CASE(30)
-        STRIX_VMCNT_CASE(32)
+#define STRIX_VMCNT_CASE8(k) STRIX_VMCNT_CASE(k) STRIX_VMCNT_CASE(k + 1) STRIX_VMCNT_CASE(k + 2) STRIX_VMCNT_CASE(k + 3) \
+    STRIX_VMCNT_CASE(k + 4) STRIX_VMCNT_CASE(k + 5) STRIX_VMCNT_CASE(k + 6) STRIX_VMCNT_CASE(k + 7)
+        STRIX_VMCNT_CASE8(1) STRIX_VMCNT_CASE8(9) STRIX_VMCNT_CASE8(17) STRIX_VMCNT_CASE8(25) STRIX_VMCNT_CASE8(33)
+#undef STRIX_VMCNT_CASE8
 #undef STRIX_VMCNT_CASE
         default: wait_vmcnt<0>(); break;
     }
@@ -229,9 +229,9 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int v = 0; v < 4; ++v) dst[v] = bld16(rx, xoff[v], (uint32_t)c * BK * 2);
     };
-    auto dma_a = [&](int c, int buf) __attribute__((always_inline)) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) lds_load16(rx, abuf(buf) + 256 * v + 64 * wave, xoff[v], (uint32_t)c * BK * 2);
+    // piece v of chunk c's activations: rows 32 v .. 32 v + 31 (sub-tile v; a block loads only its live ones)
+    auto dma_a_piece = [&](int c, int buf, int v) __attribute__((always_inline)) {
+        lds_load16(rx, abuf(buf) + 256 * v + 64 * wave, xoff[v], (uint32_t)c * BK * 2);
     };
     auto dma_q_piece = [&](int span, int i) __attribute__((always_inline)) {
         lds_load16(rq, Qs + 512 * wave + 64 * i, qd[i & 1],
@@ -284,17 +284,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     if constexpr (SPAN_SM) load_sm_span(0);
     else load_sm(0);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (X16) {
-        // span 0's codes into LDS and then registers (they land with chunk 0's activations, which the K loop waits
-        // for anyway), then the activations of chunks 0 and 1
-#pragma unroll
-        for (int i = 0; i < 8; ++i) dma_q_piece(0, i);
-        dma_a(0, 0);
-        dma_a(1, 1);
-        wait_vmcnt<8>();
-        read_q();
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): read before chunk 0 loads the next span
-    } else {
+    if constexpr (!X16) {
         load_a(0, ar[0]);
         load_a(1, ar[1]);
         load_q(0, qr[0]);
@@ -308,6 +298,20 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     // two chunks of a group
     auto run = [&](auto nt_c) __attribute__((always_inline)) {
         constexpr int NT = decltype(nt_c)::value;
+        if constexpr (X16) {
+            // span 0's codes into LDS and then registers (they land with chunk 0's activations, which the K loop
+            // waits for anyway), then the live activation pieces of chunks 0 and 1
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dma_q_piece(0, i);
+#pragma unroll
+            for (int v = 0; v < NT; ++v) dma_a_piece(0, 0, v);
+#pragma unroll
+            for (int v = 0; v < NT; ++v) dma_a_piece(1, 1, v);
+            wait_vmcnt_n(2 * NT);
+            read_q();
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): read before chunk 0 loads the next span
+            __builtin_amdgcn_sched_barrier(0);
+        }
         float16v acc[NT][2];
 #pragma unroll
         for (int i = 0; i < NT; ++i)
@@ -325,12 +329,13 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (X16) {
                     // chunk c's activations (issued in chunk c - 2's K steps) have landed: the loads issued after
-                    // their last piece are the last two pieces of chunk c - 2's span load (if it started a span),
-                    // chunk c - 1's scales (at a group start), its 4 activation pieces and its 8 span pieces (if it
-                    // started a span); before chunk 0, only chunk 1's activations
-                    const int spn2 = (pt + TRIP - 2) % 4 == 0 ? 2 : 0, spn1 = (pt + TRIP - 1) % 4 == 0 ? 8 : 0;
+                    // their last piece (K step NT - 1) are the span pieces of chunk c - 2's later K steps (if it
+                    // started a span), chunk c - 1's scales (at a group start), its NT activation pieces and its 8
+                    // span pieces (if it started a span); before chunk 0, only chunk 1's activations
+                    const int spn2 = (pt + TRIP - 2) % 4 == 0 ? 2 * (5 - NT) : 0;
+                    const int spn1 = (pt + TRIP - 1) % 4 == 0 ? 8 : 0;
                     const int sm1 = (pt + TRIP - 1) % (SPAN_SM ? 4 : CPG) == 0 ? 4 : 0;
-                    wait_vmcnt_n(pt == 0 && c == 0 ? 4 : 4 + sm1 + spn2 + spn1);
+                    wait_vmcnt_n(pt == 0 && c == 0 ? NT : NT + sm1 + spn2 + spn1);
                 }
                 if constexpr (SPAN_SM) {
                     if (pt % 4 == 0) {
@@ -388,7 +393,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                         // (c + 2) % 3 (last read at chunk c - 1); at a span's first chunk, two of the 8 pieces of
                         // the next span's codes into the wave's LDS (read into registers at the end of chunk c - 1)
                         __builtin_amdgcn_sched_barrier(0);
-                        lds_load16(rx, abuf((pt + 2) % 3) + 256 * ks + 64 * wave, xoff[ks], (uint32_t)(c + 2) * BK * 2);
+                        if (ks < NT) dma_a_piece(c + 2, (pt + 2) % 3, ks);
                         if (pt % 4 == 0) {
                             dma_q_piece(c / 4 + 1, 2 * ks);
                             dma_q_piece(c / 4 + 1, 2 * ks + 1);
@@ -402,8 +407,8 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                     if (pt % 4 == 3) {
                         // the next span's codes to registers (the LDS is then free for the span after it). The
                         // span's load (issued in chunk c - 3's K steps) has landed once the loads of chunks c - 2 ..
-                        // c are all that remain: 12 activation pieces and the scales of their group starts
-                        wait_vmcnt_n(12 + 4 * (SPAN_SM ? 0 : CPG == 2 ? 1 : 3));
+                        // c are all that remain: 3 NT activation pieces and the scales of their group starts
+                        wait_vmcnt_n(3 * NT + 4 * (SPAN_SM ? 0 : CPG == 2 ? 1 : 3));
                         read_q();
                         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
                     }
