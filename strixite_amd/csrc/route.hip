@@ -38,22 +38,25 @@ __global__ void __launch_bounds__(kRangeChunks * kWave) route_hist_kernel(const 
     extern __shared__ int lds[];  // [kRangeChunks][E + 1]
     const int E = (int)L.E, nb = E + 1, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int64_t r = blockIdx.x, ch0 = r * kRangeChunks;
+    const int64_t ch = ch0 + wave, s0 = ch * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
+    ChunkIds ci{};
+    if (ch < L.nch) ci = chunk_ids(ids, s0, s1);  // in flight while the counters are cleared
     for (int i = threadIdx.x; i < kRangeChunks * nb; i += blockDim.x) lds[i] = 0;
     __syncthreads();
-    const int64_t ch = ch0 + wave;
     if (ch < L.nch) {
-        const int64_t s0 = ch * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
-        const int fb = chunk_hist(ids, s0, s1, E, nbits, lds + wave * nb);
+        const int fb = chunk_hist(ci, s0, s1, E, nbits, lds + wave * nb);
         if (lane == 0) ws[L.bad() + ch] = fb;
     }
     __syncthreads();
     const int nc = (int)(L.nch - ch0 < kRangeChunks ? L.nch - ch0 : kRangeChunks);
     for (int t = threadIdx.x; t < nb; t += blockDim.x) {
         int run = 0;
-        for (int w = 0; w < nc; ++w) {
-            ws[L.hist() + (ch0 + w) * nb + t] = run;
-            run += lds[w * nb + t];
-        }
+#pragma unroll
+        for (int w = 0; w < kRangeChunks; ++w)
+            if (w < nc) {
+                ws[L.hist() + (ch0 + w) * nb + t] = run;
+                run += lds[w * nb + t];
+            }
         ws[L.rsum() + r * nb + t] = run;
     }
 }
@@ -70,7 +73,7 @@ __global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, La
     if (fb != INT_MAX) atomicMin(&bad_lds, fb);
     // the ranges' counts are read 16 at a time (independent loads in flight together)
     constexpr int B = 16;
-    int cnt = 0;
+    int cnt = 0, h0[B];  // h0: the first B ranges' counts, kept for the second pass
     if (t <= E)
         for (int64_t r0 = 0; r0 < R; r0 += B) {
             int h[B];
@@ -78,6 +81,9 @@ __global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, La
             for (int b = 0; b < B; ++b) h[b] = r0 + b < R ? ws[L.rsum() + (r0 + b) * (E + 1) + t] : 0;
 #pragma unroll
             for (int b = 0; b < B; ++b) cnt += h[b];
+            if (r0 == 0)
+#pragma unroll
+                for (int b = 0; b < B; ++b) h0[b] = h[b];
         }
     int v[7], tot[7];
     bucket_scan_values(cnt, v);
@@ -94,7 +100,8 @@ __global__ void __launch_bounds__(1024) route_scan_kernel(const int32_t *ids, La
         for (int64_t r0 = 0; r0 < R; r0 += B) {
             int h[B];
 #pragma unroll
-            for (int b = 0; b < B; ++b) h[b] = r0 + b < R ? ws[L.rsum() + (r0 + b) * (E + 1) + t] : 0;
+            for (int b = 0; b < B; ++b)
+                h[b] = r0 == 0 ? h0[b] : r0 + b < R ? ws[L.rsum() + (r0 + b) * (E + 1) + t] : 0;
 #pragma unroll
             for (int b = 0; b < B; ++b)
                 if (r0 + b < R) {
@@ -121,10 +128,22 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave) route_place_kernel(con
     const int64_t ch = (int64_t)blockIdx.x * kWavesPerBlock + wave;
     if (ch >= L.nch) return;
     int *c = lds + wave * (E + 1);
-    const int32_t *gh = ws + L.hist() + ch * (E + 1), *rs = ws + L.rsum() + (ch / kRangeChunks) * (E + 1);
-    for (int b = lane; b <= E; b += kWave) c[b] = gh[b] + rs[b];
     const int64_t s0 = ch * kChunk, s1 = s0 + kChunk < L.S ? s0 + kChunk : L.S;
-    chunk_place(ids, s0, s1, E, nbits, c, ws + L.slots());
+    const ChunkIds ci = chunk_ids(ids, s0, s1);  // in flight with the cursors' loads
+    const int32_t *gh = ws + L.hist() + ch * (E + 1), *rs = ws + L.rsum() + (ch / kRangeChunks) * (E + 1);
+    // the cursors 8 a lane at a time (their loads in flight together)
+    for (int b0 = 0; b0 <= E; b0 += 8 * kWave) {
+        int g[8], q[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int b = b0 + u * kWave + lane;
+            g[u] = b <= E ? gh[b] : 0, q[u] = b <= E ? rs[b] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (b0 + u * kWave + lane <= E) c[b0 + u * kWave + lane] = g[u] + q[u];
+    }
+    chunk_place(ci, s0, s1, E, nbits, c, ws + L.slots());
 }
 
 // The tile records, after placement, a thread per (16-slot tile, entry) and per 64-slot tile: a tile's bucket is the

@@ -81,15 +81,31 @@ __device__ __forceinline__ uint64_t match_bucket(int b, bool valid, int nbits) {
 
 __device__ __forceinline__ uint64_t lanes_below() { return (1ull << (threadIdx.x % kWave)) - 1ull; }
 
+// A chunk's ids, all loaded before any is used (one round trip instead of one a 64-slot step).
+struct ChunkIds {
+    int32_t v[kChunk / kWave];
+};
+__device__ __forceinline__ ChunkIds chunk_ids(const int32_t *ids, int64_t s0, int64_t s1) {
+    const int lane = threadIdx.x % kWave;
+    ChunkIds c;
+#pragma unroll
+    for (int u = 0; u < kChunk / kWave; ++u) {
+        const int64_t s = s0 + u * kWave + lane;
+        c.v[u] = s < s1 ? ids[s] : 0;
+    }
+    return c;
+}
+
 // Histogram of chunk [s0, s1) into the wave-private counters h[E + 1] (zeroed by the caller); returns the chunk's
 // smallest invalid slot (INT_MAX if none) on every lane.
-__device__ inline int chunk_hist(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *h) {
+__device__ inline int chunk_hist(const ChunkIds &ci, int64_t s0, int64_t s1, int E, int nbits, int *h) {
     const int lane = threadIdx.x % kWave;
     int first_bad = INT_MAX;
-    for (int64_t base = s0; base < s1; base += kWave) {
-        const int64_t s = base + lane;
+#pragma unroll
+    for (int u = 0; u < kChunk / kWave; ++u) {
+        const int64_t s = s0 + u * kWave + lane;
         const bool valid = s < s1;
-        const int32_t id = valid ? ids[s] : 0;
+        const int32_t id = ci.v[u];
         const int b = bucket_of(id, E);
         const uint64_t same = match_bucket(b, valid, nbits);
         if (valid && (same & lanes_below()) == 0) h[b] += __popcll(same);
@@ -99,15 +115,20 @@ __device__ inline int chunk_hist(const int32_t *ids, int64_t s0, int64_t s1, int
     for (int off = kWave / 2; off > 0; off >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, off, kWave));
     return first_bad;
 }
+__device__ inline int chunk_hist(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *h) {
+    return chunk_hist(chunk_ids(ids, s0, s1), s0, s1, E, nbits, h);
+}
 
 // Stable placement of chunk [s0, s1) through the wave-private cursors c[E + 1] (each at the bucket's first free
 // position for this chunk).
-__device__ inline void chunk_place(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *c, int32_t *slots) {
+__device__ inline void chunk_place(const ChunkIds &ci, int64_t s0, int64_t s1, int E, int nbits, int *c,
+                                   int32_t *slots) {
     const int lane = threadIdx.x % kWave;
-    for (int64_t base = s0; base < s1; base += kWave) {
-        const int64_t s = base + lane;
+#pragma unroll
+    for (int u = 0; u < kChunk / kWave; ++u) {
+        const int64_t s = s0 + u * kWave + lane;
         const bool valid = s < s1;
-        const int32_t id = valid ? ids[s] : 0;
+        const int32_t id = ci.v[u];
         const int b = bucket_of(id, E);
         const uint64_t same = match_bucket(b, valid, nbits);
         const int rank = __popcll(same & lanes_below());
@@ -116,6 +137,9 @@ __device__ inline void chunk_place(const int32_t *ids, int64_t s0, int64_t s1, i
         if (valid) slots[cur + rank] = (int32_t)s;
         if (valid && rank == 0) c[b] = cur + __popcll(same);
     }
+}
+__device__ inline void chunk_place(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *c, int32_t *slots) {
+    chunk_place(chunk_ids(ids, s0, s1), s0, s1, E, nbits, c, slots);
 }
 
 // Inclusive sum over the wave's lanes in lane order: Kogge-Stone inside each 16-lane row (DPP row shifts), then the
