@@ -81,7 +81,7 @@ __device__ __forceinline__ uint64_t match_bucket(int b, bool valid, int nbits) {
 
 __device__ __forceinline__ uint64_t lanes_below() { return (1ull << (threadIdx.x % kWave)) - 1ull; }
 
-// A chunk's ids, all loaded before any is used (one round trip instead of one a 64-slot step).
+// A chunk's ids from global memory, all loaded before any is used (one round trip instead of one a 64-slot step).
 struct ChunkIds {
     int32_t v[kChunk / kWave];
 };
@@ -115,8 +115,22 @@ __device__ inline int chunk_hist(const ChunkIds &ci, int64_t s0, int64_t s1, int
     for (int off = kWave / 2; off > 0; off >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, off, kWave));
     return first_bad;
 }
+// (ids in LDS: a 64-slot step at a time, only the steps the chunk has)
 __device__ inline int chunk_hist(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *h) {
-    return chunk_hist(chunk_ids(ids, s0, s1), s0, s1, E, nbits, h);
+    const int lane = threadIdx.x % kWave;
+    int first_bad = INT_MAX;
+    for (int64_t base = s0; base < s1; base += kWave) {
+        const int64_t s = base + lane;
+        const bool valid = s < s1;
+        const int32_t id = valid ? ids[s] : 0;
+        const int b = bucket_of(id, E);
+        const uint64_t same = match_bucket(b, valid, nbits);
+        if (valid && (same & lanes_below()) == 0) h[b] += __popcll(same);
+        if (valid && b == E && (int)s < first_bad) first_bad = (int)s;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) first_bad = min(first_bad, __shfl_xor(first_bad, off, kWave));
+    return first_bad;
 }
 
 // Stable placement of chunk [s0, s1) through the wave-private cursors c[E + 1] (each at the bucket's first free
@@ -139,7 +153,19 @@ __device__ inline void chunk_place(const ChunkIds &ci, int64_t s0, int64_t s1, i
     }
 }
 __device__ inline void chunk_place(const int32_t *ids, int64_t s0, int64_t s1, int E, int nbits, int *c, int32_t *slots) {
-    chunk_place(chunk_ids(ids, s0, s1), s0, s1, E, nbits, c, slots);
+    const int lane = threadIdx.x % kWave;
+    for (int64_t base = s0; base < s1; base += kWave) {
+        const int64_t s = base + lane;
+        const bool valid = s < s1;
+        const int32_t id = valid ? ids[s] : 0;
+        const int b = bucket_of(id, E);
+        const uint64_t same = match_bucket(b, valid, nbits);
+        const int rank = __popcll(same & lanes_below());
+        int cur = 0;
+        if (valid) cur = c[b];
+        if (valid) slots[cur + rank] = (int32_t)s;
+        if (valid && rank == 0) c[b] = cur + __popcll(same);
+    }
 }
 
 // Inclusive sum over the wave's lanes in lane order: Kogge-Stone inside each 16-lane row (DPP row shifts), then the
