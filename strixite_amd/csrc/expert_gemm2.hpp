@@ -12,14 +12,14 @@
 // Block: 4 waves, BM = 128 token slots (two consecutive 64-slot tile records of one expert's bucket) x BN = 256 weight
 // rows (SwiGLU: 128 gate rows and the matching 128 up rows, a wave 32 + 32; otherwise a wave 64 consecutive rows).
 // K runs in chunks of 64: two a quantization group at G 128, one at G 64; at G 32 each lane half's 32 k of a chunk
-// are one group. The block's activations (gathered by slot) reach LDS two chunks ahead: X_F16P (x already F16 in the
-// paired order below) straight from memory into one of three LDS buffers; otherwise (BF16 x, or F16 x in natural
-// order) through registers, converted or permuted there, into one of two. The 16-byte columns of an LDS row are
-// XOR-swizzled by half the row index, so the MFMA reads are conflict-free. Codes: with X_F16P, a wave's 64 weight
-// rows' codes of a 4-chunk span (128 bytes a row: whole lines, 8 rows an instruction) go straight into 8 KB of LDS a
-// span ahead and into registers a span at a time (the 32 rows x 32 bytes a lane's own chunk load would touch cost the
-// vector memory path ~4x as much per instruction); otherwise each lane loads its row's 32 codes of a chunk two chunks
-// ahead. A block whose slots fill fewer than 4 of its 32-token sub-tiles runs a K loop for just the live ones.
+// are one group. The block's activations (gathered by slot) reach LDS two chunks ahead, straight from memory into one
+// of three buffers; X_F16P (x already F16 in the paired order below) as they are, the other forms (BF16 x, or F16 h
+// in natural order) converted in place by the wave that loaded them, a chunk ahead. The 16-byte columns of an LDS row
+// are XOR-swizzled by half the row index, so the MFMA reads are conflict-free. Codes: a wave's 64 weight rows' codes
+// of a 4-chunk span (128 bytes a row: whole lines, 8 rows an instruction) go straight into 8 KB of LDS a span ahead
+// and into registers a span at a time (the 32 rows x 32 bytes a lane's own chunk load would touch cost the vector
+// memory path ~4x as much per instruction). A block whose slots fill fewer than 4 of its 32-token sub-tiles runs a K
+// loop for just the live ones.
 //
 // The k order of an MFMA operand: lane half h takes k 32 h .. 32 h + 31 of a chunk and K step ks the 8 at
 // 32 h + 8 ks, whose 8 halves hold k = 0, 4, 1, 5, 2, 6, 3, 7 of that block (the paired order), for the activations
@@ -132,20 +132,22 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     static_assert(SWI || EPI == EPI_BF16, "SwiGLU h or BF16 outputs");
     static_assert(GS == 32 || GS == 64 || GS == 128, "group sizes 32, 64, 128");
     constexpr int CPG = GS > BK ? GS / BK : 1;  // chunks that start with a new scale and min
-    // X16 at G 128 with an even number of groups a row: a span's two groups' scales (and mins) come as one aligned
+    // G 128 with an even number of groups a row: a span's two groups' scales (and mins) come as one aligned
     // dword a row, loaded a span ahead (4 instead of 8 loads a span, each over the 12 lines of 32 rows)
-    constexpr bool SPAN_SM = X16 && CPG == 2 && SE;
-    static_assert(!SE || SPAN_SM, "SE: X16 at G 128 only");
+    constexpr bool SPAN_SM = CPG == 2 && SE;
+    static_assert(!SE || SPAN_SM, "SE: G 128 only");
+    // activations not already in the paired F16 form reach LDS as they are and each wave converts its own pieces
+    // there, a chunk ahead, before the barrier that publishes them
+    constexpr bool CONV = !X16;
     // the activation buffers [row * 8 + (col ^ ((row >> 1) & 7))], separate arrays picked at compile time: the
     // compiler then tells a read of one from the loads still landing in another and waits for those loads no longer
     // than it must
-    __shared__ __attribute__((aligned(16))) uint4 As0[BM * BK / 8], As1[BM * BK / 8], As2[X16 ? BM * BK / 8 : 1];
+    __shared__ __attribute__((aligned(16))) uint4 As0[BM * BK / 8], As1[BM * BK / 8], As2[BM * BK / 8];
     auto abuf = [&](int i) __attribute__((always_inline)) -> uint4 * { return i == 0 ? As0 : i == 1 ? As1 : As2; };
-    // X16: the codes of a 4-chunk span (256 k: 128 bytes of each of a wave's 64 weight rows, whole lines) reach LDS
-    // directly, 8 KB a wave; otherwise each lane loads its own 32 codes of a chunk (32 rows x 32 bytes an
-    // instruction: gfx950's vector memory path takes ~4x as long for those 32 lines as for 8 whole ones)
-    constexpr bool QLDS = X16;
-    __shared__ __attribute__((aligned(16))) uint4 Qs[QLDS ? 4 * 512 : 1];
+    // the codes of a 4-chunk span (256 k: 128 bytes of each of a wave's 64 weight rows, whole lines) reach LDS
+    // directly, 8 KB a wave (a lane's own 32 codes of a chunk would be 32 rows x 32 bytes an instruction: gfx950's
+    // vector memory path takes ~4x as long for those 32 lines as for 8 whole ones)
+    __shared__ __attribute__((aligned(16))) uint4 Qs[4 * 512];
     const int tid = threadIdx.x, lane = tid % kWave, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int h = lane / 32, l32 = lane % 32;
 
@@ -190,22 +192,18 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     };
 #pragma unroll
     for (int t = 0; t < 2; ++t) wrow[t] = wrow_of(t, l32);
-    const uint32_t qoff[2] = {wrow[0] * (K / 2) + 16 * h, wrow[1] * (K / 2) + 16 * h};
-    // QLDS: instruction i of a span's load brings rows 8 i .. 8 i + 7 of the wave's 64 (tile i / 4), 8 lanes a row;
+    // instruction i of a span's load brings rows 8 i .. 8 i + 7 of the wave's 64 (tile i / 4), 8 lanes a row;
     // lane p lands in LDS slot 64 i + p = row * 8 + 16-byte column p % 8, which holds the row's column (p % 8) ^
     // ((row >> 1) & 7) (the activations' swizzle: a lane group's 16 rows then read 16 distinct bank groups)
     // (rr >> 1) & 7 = (4 (i & 1) + lane / 16) & 7, so a lane's byte offsets of the 8 instructions are two bases plus
     // wave-uniform steps: 8 rows an instruction pair, and tile 1's distance from tile 0 (the up rows at N / 2, or 32
     // rows). A tile past the projection's rows (whole: N / 2 and N are multiples of 32) reads rows that are never
     // stored, in bounds or (past the last expert) as zeros.
-    uint32_t qd[2] = {0, 0}, qtile = 0;
-    if constexpr (QLDS) {
+    uint32_t qd[2];
 #pragma unroll
-        for (int e = 0; e < 2; ++e)
-            qd[e] = ((uint32_t)(expert * a.N + col0[0]) + lane / 8) * (K / 2) +
-                    16 * ((lane % 8) ^ ((4 * e + lane / 16) & 7));
-        qtile = (uint32_t)(SWI ? a.N / 2 : 32) * (K / 2);
-    }
+    for (int e = 0; e < 2; ++e)
+        qd[e] = ((uint32_t)(expert * a.N + col0[0]) + lane / 8) * (K / 2) + 16 * ((lane % 8) ^ ((4 * e + lane / 16) & 7));
+    const uint32_t qtile = (uint32_t)(SWI ? a.N / 2 : 32) * (K / 2);
     const uint32_t soff[2] = {wrow[0] * groups * 2, wrow[1] * groups * 2};
     // this lane's LDS fragment of K step ks in a buffer: row 32 i + l32 ((row >> 1) & 7 = (l32 >> 1) & 7), 16-byte
     // column 4 h + ks. gfx950 serves a 16-byte read 16 lanes at a time from 64 banks (256 bytes): lanes of rows r and
@@ -218,17 +216,9 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     asm("v_mov_b32 %0, 0x64006400" : "=v"(b64));
     asm("v_mov_b32 %0, 0x54005400" : "=v"(b54));
 
-    // Loads past the last chunk read in-bounds or zero data that is never used. X16: every chunk issues the same
-    // loads in the same order (4 scale and min loads at a chunk that starts a group, then codes and activations two
-    // chunks ahead), so the activations of chunk c are in LDS once at most 6 (chunk c - 1 loaded no scales: c odd at
-    // G 128, and chunk 0) or 10 later loads are outstanding.
-    uint4 ar[2][4];  // !X16: activations in flight
-    constexpr int QPF = 2;  // !QLDS: chunks of codes in flight
-    uint4 qr[QLDS ? 4 : QPF][2];  // QLDS: the span's codes, chunk c % 4
-    auto load_a = [&](int c, uint4 (&dst)[4]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) dst[v] = bld16(rx, xoff[v], (uint32_t)c * BK * 2);
-    };
+    // Loads past the last chunk read in-bounds or zero data that is never used; each chunk issues its loads in a
+    // fixed order, so the waits below can count them.
+    uint4 qr[4][2];  // the span's codes, chunk c % 4
     // piece v of chunk c's activations: rows 32 v .. 32 v + 31 (sub-tile v; a block loads only its live ones)
     auto dma_a_piece = [&](int c, int buf, int v) __attribute__((always_inline)) {
         lds_load16(rx, abuf(buf) + 256 * v + 64 * wave, xoff[v], (uint32_t)c * BK * 2);
@@ -250,14 +240,15 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
             qr[cc][0] = __builtin_bit_cast(uint4, v0), qr[cc][1] = __builtin_bit_cast(uint4, v1);
         }
     };
-    auto load_q = [&](int c, uint4 (&dst)[2]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) dst[t] = bld16(rq, qoff[t], (uint32_t)c * (BK / 2));
-    };
-    auto store_a = [&](const uint4 (&src)[4], int buf) __attribute__((always_inline)) {
+    // CONV: this wave's own pieces of a buffer (the slots its loads filled) into the paired F16 form, in place
+    auto convert = [&](int buf, int np) __attribute__((always_inline)) {
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-            abuf(buf)[tid + 256 * v] = XF == X_F16 ? f16x8_to_paired(src[v]) : bf16x8_to_f16_paired(src[v]);
+            if (v < np) {
+                uint4 *ptr = abuf(buf) + 256 * v + 64 * wave + lane;
+                *ptr = XF == X_F16 ? f16x8_to_paired(*ptr) : bf16x8_to_f16_paired(*ptr);
+            }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the writes are done before the publishing barrier
     };
     // scale and min of the current group for the two tiles (F16 pairs); the next group's raw bf16 loaded a group ahead
     // (chunk c: this lane half's k 64 c + 32 h lie in group (64 c + 32 h) / G)
@@ -284,21 +275,12 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     if constexpr (SPAN_SM) load_sm_span(0);
     else load_sm(0);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (!X16) {
-        load_a(0, ar[0]);
-        load_a(1, ar[1]);
-        load_q(0, qr[0]);
-        load_q(1, qr[1]);
-        store_a(ar[0], 0);
-        load_a(2, ar[0]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
 
     // the K loop and the epilogue for NT live 32-token sub-tiles (the block's slots, rounded up); K in trips of the
     // two chunks of a group
     auto run = [&](auto nt_c) __attribute__((always_inline)) {
         constexpr int NT = decltype(nt_c)::value;
-        if constexpr (X16) {
+        {
             // span 0's codes into LDS and then registers (they land with chunk 0's activations, which the K loop
             // waits for anyway), then the live activation pieces of chunks 0 and 1
 #pragma unroll
@@ -310,6 +292,10 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
             wait_vmcnt_n(2 * NT);
             read_q();
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): read before chunk 0 loads the next span
+            if constexpr (CONV) {
+                wait_vmcnt_n(NT);  // chunk 0's activations
+                convert(0, NT);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
         float16v acc[NT][2];
@@ -317,26 +303,28 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
         for (int i = 0; i < NT; ++i)
 #pragma unroll
             for (int t = 0; t < 2; ++t) acc[i][t] = float16v{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        // trips of TRIP chunks (X16: 12, so the three buffers' and the four span positions' turns are known at
-        // compile time; a multiple of CPG)
-        constexpr int TRIP = X16 ? 12 : 2;
+        // trips of 12 chunks, so the three buffers' and the four span positions' turns are known at compile time (a
+        // multiple of CPG)
+        constexpr int TRIP = 12;
         static_assert(TRIP % CPG == 0, "a trip starts a group");
         for (int c0 = 0; c0 < chunks; c0 += TRIP) {
 #pragma unroll
             for (int pt = 0; pt < TRIP; ++pt) {
-                const int c = c0 + pt, p = pt % 2;
+                const int c = c0 + pt;
                 if (c >= chunks) break;
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (X16) {
-                    // chunk c's activations (issued in chunk c - 2's K steps) have landed: the loads issued after
-                    // their last piece (K step NT - 1) are the span pieces of chunk c - 2's later K steps (if it
-                    // started a span), chunk c - 1's scales (at a group start), its NT activation pieces and its 8
-                    // span pieces (if it started a span); before chunk 0, only chunk 1's activations
-                    const int spn2 = (pt + TRIP - 2) % 4 == 0 ? 2 * (5 - NT) : 0;
-                    const int spn1 = (pt + TRIP - 1) % 4 == 0 ? 8 : 0;
-                    const int sm1 = (pt + TRIP - 1) % (SPAN_SM ? 4 : CPG) == 0 ? 4 : 0;
-                    wait_vmcnt_n(pt == 0 && c == 0 ? NT : NT + sm1 + spn2 + spn1);
-                }
+                // chunk c's activations (issued in chunk c - 2's K steps) have landed: the loads issued after their
+                // last piece (K step NT - 1) are the span pieces of chunk c - 2's later K steps (if it started a
+                // span), chunk c - 1's scales (at a group start), its NT activation pieces and its 8 span pieces (if
+                // it started a span); before chunk 0, only chunk 1's activations. CONV: waited for (and converted)
+                // at the end of chunk c - 1.
+                auto wait_a = [&](int ptc, bool first) __attribute__((always_inline)) {
+                    const int spn2 = (ptc + TRIP - 2) % 4 == 0 ? 2 * (5 - NT) : 0;
+                    const int spn1 = (ptc + TRIP - 1) % 4 == 0 ? 8 : 0;
+                    const int sm1 = (ptc + TRIP - 1) % (SPAN_SM ? 4 : CPG) == 0 ? 4 : 0;
+                    wait_vmcnt_n(first ? NT : NT + sm1 + spn2 + spn1);
+                };
+                if constexpr (!CONV) wait_a(pt, pt == 0 && c == 0);
                 if constexpr (SPAN_SM) {
                     if (pt % 4 == 0) {
 #pragma unroll
@@ -355,13 +343,13 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                     for (int t = 0; t < 2; ++t) sc[t] = bf16_to_f16x2(sraw[t]), mn[t] = bf16_to_f16x2(mraw[t]);
                     load_sm(c + CPG);
                 }
-                // chunk c's activations are visible; every wave is done with chunk c - 1's buffer. X16: each wave has
-                // waited for its own loads into LDS above; a plain barrier (no fence) keeps the later loads in flight.
-                if constexpr (X16) __builtin_amdgcn_s_barrier();
-                else __syncthreads();
+                // chunk c's activations are visible; every wave is done with chunk c - 1's buffer. Each wave has
+                // waited for its own loads into LDS (and CONV: its writes); a plain barrier (no fence) keeps the later
+                // loads in flight.
+                __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                const uint4 *as = abuf(X16 ? pt % 3 : p);
-                const uint4(&q)[2] = qr[QLDS ? pt % 4 : pt % QPF];
+                const uint4 *as = abuf(pt % 3);
+                const uint4(&q)[2] = qr[pt % 4];
                 Frag af[2][NT];
                 auto read_a = [&](int ks, Frag (&dst)[NT]) __attribute__((always_inline)) {
 #pragma unroll
@@ -375,9 +363,8 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                 for (int ks = 0; ks < 4; ++ks) {
                     if (ks + 1 < 4) read_a(ks + 1, af[(ks + 1) & 1]);
                     // the next K step's reads stay ahead of this step's MFMAs (the scheduler would otherwise pull
-                    // them down to just before their use, where each pair's LDS latency stalls the wave); the
-                    // register-staged forms have no VGPRs to spare for it
-                    if constexpr (X16) __builtin_amdgcn_sched_barrier(0);
+                    // them down to just before their use, where each pair's LDS latency stalls the wave)
+                    __builtin_amdgcn_sched_barrier(0);
                     const uint32_t cw0 = ks == 0 ? q[0].x : ks == 1 ? q[0].y : ks == 2 ? q[0].z : q[0].w;
                     const uint32_t cw1 = ks == 0 ? q[1].x : ks == 1 ? q[1].y : ks == 2 ? q[1].z : q[1].w;
                     const Frag b0 = q4_dequant_f16(cw0, sc[0], mn[0], b64, b54),
@@ -387,7 +374,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                         acc[i][0] = mfma32_f16(af[ks & 1][i], b0, acc[i][0]);
                         acc[i][1] = mfma32_f16(af[ks & 1][i], b1, acc[i][1]);
                     }
-                    if constexpr (X16) {
+                    {
                         // the loads ahead, spread over the K steps (a burst of them fills the vector memory
                         // path's queues and stalls the issuing wave): activation piece ks of chunk c + 2 into buffer
                         // (c + 2) % 3 (last read at chunk c - 1); at a span's first chunk, two of the 8 pieces of
@@ -402,8 +389,13 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (!QLDS) load_q(c + QPF, qr[pt % QPF]);
-                if constexpr (X16) {
+                if constexpr (CONV) {
+                    // the next chunk's activations: once this wave's pieces have landed, into the paired F16 form
+                    // (beside this chunk's MFMAs still in the matrix pipe)
+                    wait_a(pt + 1, false);
+                    convert((pt + 1) % 3, NT);
+                }
+                {
                     if (pt % 4 == 3) {
                         // the next span's codes to registers (the LDS is then free for the span after it). The
                         // span's load (issued in chunk c - 3's K steps) has landed once the loads of chunks c - 2 ..
@@ -412,10 +404,6 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                         read_q();
                         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
                     }
-                } else {
-                    // the next chunk's activations to the other buffer, then the load of the one after next
-                    store_a(ar[p ^ 1], p ^ 1);
-                    load_a(c + 3, ar[p ^ 1]);
                 }
             }
         }
@@ -426,7 +414,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
             // BF16 rows go out through LDS as whole 128-byte lines: per 32-token sub-tile the wave writes its 32 x 64
             // values into its own part of a free activation buffer (the part only its own loads fill: 16-byte slots
             // 256 v + 64 w, v = 0..3, one a group of 8 rows), then stores 16 bytes a lane, 8 lanes a row
-            uint16_t *st = reinterpret_cast<uint16_t *>(abuf(X16 ? chunks % 3 : chunks & 1));
+            uint16_t *st = reinterpret_cast<uint16_t *>(abuf(chunks % 3));
             auto sidx = [&](int r, int c) { return ((r >> 3) * 256 + 64 * wave) * 8 + (r & 7) * 64 + c; };
             // column pairs as dwords: lanes 2 j and 2 j + 1 (columns c, c + 1) swap one of the two token rows they
             // hold, so the even lane packs row r's (c, c + 1) and the odd lane row r + 1's
@@ -539,13 +527,8 @@ bool launch_expert_gemm2(const GemmArgs &a, hipStream_t stream) {
         case 32: go(std::integral_constant<int, 32>{}, F{}); break;
         case 64: go(std::integral_constant<int, 64>{}, F{}); break;
         default:
-            if constexpr (XF == X_F16P) {
-                if ((a.K / a.G) % 2 == 0) {
-                    go(std::integral_constant<int, 128>{}, std::true_type{});
-                    break;
-                }
-            }
-            go(std::integral_constant<int, 128>{}, F{});
+            if ((a.K / a.G) % 2 == 0) go(std::integral_constant<int, 128>{}, std::true_type{});
+            else go(std::integral_constant<int, 128>{}, F{});
             break;
     }
     return true;
