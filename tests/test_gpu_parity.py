@@ -691,7 +691,7 @@ def test_layer_config3_uniform_logits():
     say("layer cfg3")
     layer = moe.MoeLayer.synth(3072, 512, 10, 512, seed=0)
     lg = moe.synth_uniform_pm1(0, "logits", 0, (512, 513))
-    out, _, _ = _layer_parity(layer, 512, 1, logits_in=lg, sample=48)
+    out, _, _ = _layer_parity(layer, 512, 1, logits_in=lg)  # every token's output
     # routing on all 512 tokens: the top-k of the given logits
     rids, rcoef, _ = orc.topk(np.ascontiguousarray(to_np(lg)[:, :512]), 512, 10)
     assert np.array_equal(to_np(out["ids"]), rids)
@@ -700,11 +700,11 @@ def test_layer_config3_uniform_logits():
 
 def test_layer_config4_zipf_prefill():
     """4096-token prefill, router biased to Zipf(1.1) expert popularity: every token's routing
-    bit-exact, the output on 48 seeded tokens."""
+    bit-exact and every token's output within tolerance (the oracle runs the whole layer on all 4096 tokens)."""
     say("layer cfg4")
     bias = torch.from_numpy(zipf_bias(0, 512, 1.0)).to(DEV)
     layer = moe.MoeLayer.synth(3072, 512, 10, 512, seed=0, router_bias=bias)
-    out, o, e = _layer_parity(layer, 4096, 0, sample=48)
+    out, o, e = _layer_parity(layer, 4096, 0)
     # routing on all tokens: the oracle's canonical logits for every token
     x = to_np(moe.synth_bf16_normal(0, "x", 0, (4096, 3072), 1.0))
     lg = orc.router_logits(x, to_np(layer.router), bias=to_np(bias))
