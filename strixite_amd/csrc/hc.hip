@@ -445,18 +445,27 @@ __global__ void __launch_bounds__(256)
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int64_t K = kStreams * d, t0 = (int64_t)blockIdx.y * MT;
     const int nt = (int)(Tn - t0 < MT ? Tn - t0 : MT);
-    // wave s: the inverse RMS of stream s of each token of the group
-    for (int tt = 0; tt < nt; ++tt) {
-        const T *xs = x + (t0 + tt) * K + (int64_t)wave * d;
-        float sq = 0.f;
-        for (int64_t i = 8 * lane; i < d; i += 8 * kWave) {
-            float v[8];
-            ld8(xs, i, v);
+    // wave s: the inverse RMS of stream s of each token of the group (the tokens' loads of a step issued together)
+    {
+        float sq[MT];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) sq = fmaf(v[k], v[k], sq);
+        for (int tt = 0; tt < MT; ++tt) sq[tt] = 0.f;
+        for (int64_t i = 8 * lane; i < d; i += 8 * kWave) {
+            float v[MT][8];
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt)
+                if (tt < nt) ld8(x + (t0 + tt) * K + (int64_t)wave * d, i, v[tt]);
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt)
+                if (tt < nt)
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) sq[tt] = fmaf(v[tt][k], v[tt][k], sq[tt]);
         }
-        sq = wave_sum(sq);
-        if (lane == 0) invs[tt][wave] = 1.0f / sqrtf(sq / (float)d + eps);
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt) {
+            const float tot = wave_sum(sq[tt]);
+            if (lane == 0 && tt < nt) invs[tt][wave] = 1.0f / sqrtf(tot / (float)d + eps);
+        }
     }
     __syncthreads();
     if (blockIdx.x == 0 && lane == 0)
@@ -475,6 +484,7 @@ __global__ void __launch_bounds__(256)
     float acc[MT];
 #pragma unroll
     for (int tt = 0; tt < MT; ++tt) acc[tt] = 0.f;
+#pragma unroll 2
     for (int64_t c = (int64_t)part * kWave + lane; c < nc; c += (int64_t)kWave * KS) {
         uint32_t w[BITS];
 #pragma unroll
