@@ -325,6 +325,13 @@ def main():
                                                                         K_TOP, h=ph) for l in range(nl)])
         pgu_ms = timer(lambda i: gpg.replay(), steps=max(2, args.steps // nl)) / nl
         del gpg
+        # the same projection in the exact-weight kind (MoeMath::WmmaBf16: bf16 MFMA over the scaled codes, each
+        # group's scale and min applied on the FP32 accumulators), for comparison only
+        gpx = capture(torch, lambda: [moe.experts_gather_grouped_swiglu(xp[l], players[l].gate_up, E, proutes[l], Mp,
+                                                                        K_TOP, h=ph, math=moe.MOE_MATH_WMMA_BF16)
+                                      for l in range(nl)])
+        pgx_ms = timer(lambda i: gpx.replay(), steps=max(2, args.steps // nl)) / nl
+        del gpx
         pgu_tflops = slots * 2 * 2 * I * H / (pgu_ms / 1e3) / 1e12
         line["prefill"] = {
             "workload": "cfg4: prefill 4096 tokens, Zipf(1.1) router bias (beta 1.0), H3072 E512 top-10 + shared Q8, "
@@ -337,9 +344,11 @@ def main():
                          "frac": round(pgu_tflops / PEAK_F16_TFLOPS, 4), "us_per_launch": round(pgu_ms * 1e3, 2),
                          "algorithmic_flops_per_launch": slots * 2 * 2 * I * H},
             "experts_with_0_rows": int((cnt == 0).sum()), "max_rows_per_expert": int(cnt.max()),
+            "gate_up_exact_weights_us": round(pgx_ms * 1e3, 2),
         }
         log(f"cfg4 prefill: {pre_ms:.3f} ms/layer, {Mp / (pre_ms / 1e3):,.0f} tokens/s, {pre_tflops:.1f} TFLOP/s "
-            f"({pre_tflops / PEAK_F16_TFLOPS:.1%} MFMA); gate_up {pgu_ms * 1e3:.0f} us = {pgu_tflops:.1f} TFLOP/s")
+            f"({pre_tflops / PEAK_F16_TFLOPS:.1%} MFMA); gate_up {pgu_ms * 1e3:.0f} us = {pgu_tflops:.1f} TFLOP/s; "
+            f"exact-weight kind {pgx_ms * 1e3:.0f} us")
 
     # ---------------------------------------------------------------------------------------- cfg1: 1-token Q8 decode
     if want("cfg1"):
