@@ -165,7 +165,12 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
     const bool nan = bucket < 0 || bucket >= a.E;
     const uint32_t expert = nan ? 0u : (uint32_t)bucket;
     const int32_t *slots = a.ws + route::slots_at(a.E) + start;
-    auto orow = [&](int r) __attribute__((always_inline)) { return r < rows ? slots[r] : -1; };
+    // the output row of the block's slot 32 i + x (-1 past its rows): the 128 slots held two a lane, loaded now so
+    // their round trip is long over by the epilogue, and fetched across lanes there
+    const int32_t srow0 = lane < rows ? slots[lane] : -1, srow1 = lane + 64 < rows ? slots[lane + 64] : -1;
+    auto orow = [&](int i, int x) __attribute__((always_inline)) {
+        return __shfl(i < 2 ? srow0 : srow1, (32 * i + x) & 63, kWave);
+    };
 
     const __amdgpu_buffer_rsrc_t rx = rsrc(a.x, x_bytes), rq = rsrc(a.q, q_bytes), rs = rsrc(a.scale, s_bytes),
                                  rm = rsrc(a.minv, s_bytes), ry = rsrc(a.y, y_bytes);
@@ -439,7 +444,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                 for (int q = 0; q < 4; ++q) {
                     const int row = 8 * q + lane / 8, seg = lane % 8;
                     const uint4 v = *reinterpret_cast<const uint4 *>(st + sidx(row, 8 * seg));
-                    const int32_t orw = orow(32 * i + row);
+                    const int32_t orw = orow(i, row);
                     const int64_t col = col0[0] + 8 * seg;  // the wave's 64 columns from col0[0]
                     const bool live = orw >= 0 && col < nrows;
                     __builtin_amdgcn_raw_buffer_store_b128(
@@ -481,7 +486,7 @@ __global__ void __launch_bounds__(g2::kThreads) __attribute__((amdgpu_waves_per_
                     const float lo = upper ? got : v[0], hi = upper ? v[1] : got;
                     // F16 forms: the BF16-rounded h toward zero (what a BF16 h converts to on the way into the down)
                     const uint32_t bits = HF == H_BF16 ? f32x2_to_bf16x2(lo, hi) : pk_f16_rtz(bf16_round(lo), bf16_round(hi));
-                    const int32_t orw = orow(32 * i + 8 * (r / 4) + 4 * h + r % 4 + (upper ? 1 : 0));
+                    const int32_t orw = orow(i, 8 * (r / 4) + 4 * h + r % 4 + (upper ? 1 : 0));
                     __builtin_amdgcn_raw_buffer_store_b32(
                         bits, ry, orw >= 0 && live_col ? ((uint32_t)orw * (uint32_t)a.ldy + dpos) * 2 : y_bytes, 0, 0);
                 }
