@@ -523,7 +523,7 @@ __global__ void __launch_bounds__((W + 1) * kWave) decode_gate_up_lds_kernel(Dec
         const uint32_t expert = bucket < 0 || bucket >= a.E ? 0u : (uint32_t)bucket;
         const uint32_t row0 = expert * (uint32_t)a.N + (half ? ldh : 0u) + 16u * (uint32_t)c;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) lds_load16(rq, R + i * kWave, valid ? row0 * rowb + loff[i] : a.q_bytes, 0);
+        for (int i = 0; i < 2; ++i) lds_load16_nt(rq, R + i * kWave, valid ? row0 * rowb + loff[i] : a.q_bytes, 0);
         if constexpr (half == 0) {
             // unit row r = l % 32 of lane l; the scale load's lanes 32..63 and the min load's lanes 0..31 read past
             // the end and write zeros, both into dwords 32..63 (the min load lands 32 dwords on): no branch, so each
@@ -805,7 +805,7 @@ __global__ void __launch_bounds__(WB * kWave) decode_down_lds_kernel(DecodeArgs 
         const bool valid = rb < rbs;
         const uint32_t row0 = row_e + 16u * (uint32_t)rb;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) lds_load16(rq, R + i * kWave, valid ? row0 * 256u + loff[i] : a.q_bytes, 0);
+        for (int i = 0; i < 4; ++i) lds_load16_nt(rq, R + i * kWave, valid ? row0 * 256u + loff[i] : a.q_bytes, 0);
         if (lane < 32) {  // dword l of the rows' scales (16 rows x 4 bf16 = 32 dwords), then of the mins
             const uint32_t so = valid ? row0 * (uint32_t)(KS * 2) + 4u * (uint32_t)lane : a.s_bytes;
             uint32_t *dst = reinterpret_cast<uint32_t *>(R + 4 * kWave);

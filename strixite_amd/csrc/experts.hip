@@ -335,6 +335,12 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint4 *dst,
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)dst, 16, voff, soff, 0, 0);
 }
 
+// the same with the non-temporal policy: for streams read once (the decode kernels' weight codes; measured on MI355X
+// at cfg2: layer 99.2 -> 88.0 us)
+__device__ __forceinline__ void lds_load16_nt(__amdgpu_buffer_rsrc_t r, uint4 *dst, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)dst, 16, voff, soff, 0, 2);
+}
+
 // The wave's uniform stream parameters.
 template <int RT> struct Stream {
     __amdgpu_buffer_rsrc_t rq, rs, rm, rx;
@@ -915,8 +921,10 @@ __global__ void __launch_bounds__(kThreads)
             const int64_t a = a0 + b;
             if (a < A) {
                 const int64_t e = (m * A + a) * N + n;
-                if constexpr (PB) {
-                    ld_bf16(static_cast<const uint16_t *>(partial) + e, p[b]);
+                if constexpr (PB) {  // read once: non-temporal (cfg4's 252 MB of partials: 68 -> 58 us)
+                    const u32x4v u = __builtin_nontemporal_load(
+                        reinterpret_cast<const u32x4v *>(static_cast<const uint16_t *>(partial) + e));
+                    p[b][0] = u[0], p[b][1] = u[1], p[b][2] = u[2], p[b][3] = u[3];
                 } else {
                     const float4 q = *reinterpret_cast<const float4 *>(static_cast<const float *>(partial) + e);
                     p[b][0] = __float_as_uint(q.x), p[b][1] = __float_as_uint(q.y), p[b][2] = __float_as_uint(q.z),
