@@ -865,7 +865,8 @@ struct InjectArgs {
 };
 // UNI: no wave straddles two tokens (N a multiple of 64 VEC): the token index is wave-uniform, so the per-slot ids and
 // coefficients are scalar loads instead of a broadcast vector load each (half the kernel's vector memory traffic)
-template <bool SH, bool RES, bool PB, bool INJ = false, bool UNI = false>
+// SPK: the shared expert's down arrives as FP32 K parts (s_part, 1 <= s_parts), summed here (4 outputs a thread)
+template <bool SH, bool RES, bool PB, bool INJ = false, bool UNI = false, bool SPK = false>
 __global__ void __launch_bounds__(kThreads)
     combine_reduce_kernel(const void *partial, const int32_t *ids, const float *coef, int64_t M, int64_t A, int64_t E,
                           int64_t N, uint16_t *y, const uint16_t *s, const float *gate_logit, int64_t gate_ld,
@@ -894,9 +895,20 @@ __global__ void __launch_bounds__(kThreads)
     // the loads that do not depend on the sum go out with the partials' (one round trip for the thread)
     float gl = 0.f;
     uint32_t su[W] = {}, xu[W] = {};
+    // with FP32 partials (4 outputs a thread), the shared down's first SPU K parts are loaded here too and summed after
+    // the slots' loop (a loop that summed them here waited a round trip a part)
+    static_assert(!SPK || (SH && VEC == 4), "K parts of the shared expert: FP32 partials' combine only");
+    constexpr int SPU = SPK ? kSharedParts : 0;
+    float4 sq[SPU > 0 ? SPU : 1];
     if constexpr (SH) {
         gl = gate_logit[m * gate_ld];
-        if (s_part == nullptr) {
+        if constexpr (SPK) {
+#pragma unroll
+            for (int p = 0; p < SPU; ++p) {  // unconditional (a part past s_parts repeats the last; not summed)
+                const int pc = p < s_parts ? p : s_parts - 1;
+                sq[p] = *reinterpret_cast<const float4 *>(s_part + (pc * M + m) * N + n);
+            }
+        } else if (s_part == nullptr) {
             ld_bf16(s + i, su);
         } else {  // s = bf16 of the in-order sum of the shared down's K parts (parts_sum's arithmetic)
             float sv[VEC] = {};
@@ -951,6 +963,20 @@ __global__ void __launch_bounds__(kThreads)
     if (!ok)
 #pragma unroll
         for (int k = 0; k < VEC; ++k) v[k] = qnan();
+    if constexpr (SPK) {  // the in-order sum of the parts (parts_sum's arithmetic), then bf16
+        float4 sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < SPU; ++p) {
+            const bool in = p < s_parts;
+            sv.x = in ? sv.x + sq[p].x : sv.x, sv.y = in ? sv.y + sq[p].y : sv.y;
+            sv.z = in ? sv.z + sq[p].z : sv.z, sv.w = in ? sv.w + sq[p].w : sv.w;
+        }
+        for (int p = SPU; p < s_parts; ++p) {
+            const float4 q = *reinterpret_cast<const float4 *>(s_part + (p * M + m) * N + n);
+            sv.x += q.x, sv.y += q.y, sv.z += q.z, sv.w += q.w;
+        }
+        su[0] = pack(sv.x, sv.y), su[1] = pack(sv.z, sv.w);
+    }
     if constexpr (SH) {
         const bool gok = isfinite(gl);
         if (!gok && n == 0 && atomicCAS(&err[0], 0u, 1u) == 0u) {
@@ -1364,6 +1390,7 @@ void combine_reduce(const void *partial, const int32_t *ids, const float *coef, 
                     const InjectArgs *inj = nullptr) {
     const int vec = combine_vec(partial_bf16);
     STRIX_CHECK(N % vec == 0, "combine: N = ", N, " must be a multiple of ", vec);
+    STRIX_CHECK(s_part == nullptr || s_parts >= 1, "combine: the shared expert's K parts without a part count");
     const unsigned blocks = (unsigned)((M * N / vec + kThreads - 1) / kThreads);
     const uint16_t *s = sh ? static_cast<const uint16_t *>(sh->s) : nullptr;
     const float *gl = sh ? sh->gate_logit : nullptr;
@@ -1384,13 +1411,27 @@ void combine_reduce(const void *partial, const int32_t *ids, const float *coef, 
                                                       nullptr, s_part, s_parts, *inj);
         };
         if (sh && partial_bf16) gi_(std::true_type{}, std::true_type{});
-        else if (sh) gi_(std::true_type{}, std::false_type{});
+        else if (sh && s_part != nullptr) {
+            auto k = uni ? combine_reduce_kernel<true, false, false, true, true, true>
+                         : combine_reduce_kernel<true, false, false, true, false, true>;
+            k<<<blocks, kThreads, 0, stream>>>(partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, nullptr, nullptr,
+                                               s_part, s_parts, *inj);
+        } else if (sh) gi_(std::true_type{}, std::false_type{});
         else if (partial_bf16) gi_(std::false_type{}, std::true_type{});
         else gi_(std::false_type{}, std::false_type{});
         return;
     }
     auto go = [&](auto shc, auto resc) {
         constexpr bool SHV = decltype(shc)::value, RV = decltype(resc)::value;
+        if constexpr (SHV) {
+            if (!partial_bf16 && s_part != nullptr) {
+                auto k = uni ? combine_reduce_kernel<true, RV, false, false, true, true>
+                             : combine_reduce_kernel<true, RV, false, false, false, true>;
+                k<<<blocks, kThreads, 0, stream>>>(partial, ids, coef, M, A, E, N, y, s, gl, gld, gi, err, resid, out,
+                                                   s_part, s_parts, InjectArgs{});
+                return;
+            }
+        }
         auto k = partial_bf16 ? (uni ? combine_reduce_kernel<SHV, RV, true, false, true>
                                      : combine_reduce_kernel<SHV, RV, true, false, false>)
                               : (uni ? combine_reduce_kernel<SHV, RV, false, false, true>
