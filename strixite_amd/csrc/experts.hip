@@ -526,13 +526,27 @@ __device__ __forceinline__ void dense_part_unit(const GemmArgs &a, int spp, int 
     for (int r = 0; r < 4; ++r)
         if (4 * g + r < a.M) part[(pt * a.M + 4 * g + r) * a.N + tile * 16 + j] = acc[0][r];
 }
-// Output i of the in-order sum of the parts: SWI: h[m, c] = bf16(silu(g) * u), g and u the sums of rows c and N / 2 + c
-// (i = m * N / 2 + c); otherwise y[m, n] = bf16(sum) (i = m * N + n).
+constexpr int kSharedParts = 8;  // most K parts of the shared expert's split-K projections
+// Output i of the in-order sum of the parts (1 <= parts): SWI: h[m, c] = bf16(silu(g) * u), g and u the sums of rows c
+// and N / 2 + c (i = m * N / 2 + c); otherwise y[m, n] = bf16(sum) (i = m * N + n). The first kSharedParts parts' loads
+// go out together (unconditionally, a part past the count repeating the last; one round trip instead of one a part).
 template <bool SWI>
 __device__ __forceinline__ float parts_sum(const float *part, int parts, int64_t M, int64_t N, int64_t i) {
     const int64_t no = SWI ? N / 2 : N, m = i / no, c = i % no;
+    float g[kSharedParts], u[kSharedParts];
+#pragma unroll
+    for (int p = 0; p < kSharedParts; ++p) {
+        const int64_t pc = p < parts ? p : parts - 1;
+        g[p] = part[(pc * M + m) * N + c];
+        u[p] = SWI ? part[(pc * M + m) * N + no + c] : 0.f;
+    }
     float v0 = 0.f, v1 = 0.f;
-    for (int p = 0; p < parts; ++p) {
+#pragma unroll
+    for (int p = 0; p < kSharedParts; ++p) {
+        v0 = p < parts ? v0 + g[p] : v0;
+        if constexpr (SWI) v1 = p < parts ? v1 + u[p] : v1;
+    }
+    for (int p = kSharedParts; p < parts; ++p) {
         v0 += part[(p * M + m) * N + c];
         if constexpr (SWI) v1 += part[(p * M + m) * N + no + c];
     }
@@ -762,7 +776,6 @@ __global__ void __launch_bounds__(kThreads) perslot_combine_kernel(GemmArgs a, c
     }
 }
 
-constexpr int kSharedParts = 8;  // most K parts of the shared expert's split-K projections
 constexpr int kSharedUnitsPerBlock = 4;  // shared-expert units a block of the top-k launch takes
 
 // Top-k + packing of a small batch (block 0, route_small.hpp) with the shared expert's gate_up parts riding along in
